@@ -1,0 +1,183 @@
+/*
+ * nwd_attn.h — C ABI of the MI355X (gfx950) decode-attention path.
+ *
+ * This library replaces the two leaf kernels that the reference engine
+ * dispatches for every attention layer of every token:
+ *
+ *   kernels/kv_append.wgsl    main  :12-18  (dispatched twice, K then V,
+ *                                            engine/runtime.js:389-390)
+ *   kernels/sparse_attn.wgsl  main  :31-114 (dispatched with H workgroups,
+ *                                            engine/runtime.js:391)
+ *
+ * and keeps their buffer contract: a query buffer, a K cache, a V cache, a
+ * position, and an output buffer (bind groups built at engine/runtime.js:331-333).
+ * The reference passes the position through two uniforms,
+ * uKv.seq = seq and uAttn.seq = seq + 1 (engine/runtime.js:451-452). Here the
+ * position lives in a device int32 buffer, one entry per sequence:
+ *
+ *   pos[b]  = index at which the newest token of sequence b is (or was) written;
+ *   L_b     = pos[b] + 1 keys are attended (keys 0..pos[b], all visible, which
+ *             is the reference's causal rule, kernels/sparse_attn.wgsl:9).
+ *
+ * Differences from the reference, all requested by the caller's descriptor:
+ *   - the cache is fp16 and head-major per sequence (see nwd_cache_offset);
+ *   - Q and O may be fp16 or fp32 (the reference is fp32 only,
+ *     kernels/sparse_attn.wgsl:19-22); arithmetic is fp32 either way;
+ *   - there is a batch dimension and no 256-key cap
+ *     (kernels/sparse_attn.wgsl:29, engine/config.js:24);
+ *   - a causal chunked-prefill entry point replaces the reference's
+ *     token-by-token prefill (engine/runtime.js:640-643) with one call.
+ *
+ * All buffers are caller-owned device memory. Every call only enqueues work
+ * on the given HIP stream (0 = the null stream); nothing synchronises unless
+ * documented. A context is not thread-safe and its calls must be ordered on
+ * one stream: the split-K workspace belongs to the context.
+ */
+#ifndef NWD_ATTN_H
+#define NWD_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. 0 is success; every failing call also sets nwd_last_error. */
+enum {
+  NWD_OK = 0,
+  NWD_ERR_INVALID = 1,     /* bad descriptor, null pointer, bad shape      */
+  NWD_ERR_UNSUPPORTED = 2, /* shape the kernels are not built for           */
+  NWD_ERR_CAPACITY = 3,    /* a position would write/read past max_seq,
+                              or batch > max_batch (engine/runtime.js:448)  */
+  NWD_ERR_HIP = 4,         /* a HIP runtime call failed                     */
+  NWD_ERR_DEVICE = 5       /* a kernel flagged an out-of-range device
+                              position (reported by nwd_device_status)      */
+};
+
+/* Element types of Q, O and of the new K/V rows. The cache is always fp16. */
+enum { NWD_F32 = 0, NWD_F16 = 1 };
+
+/* Descriptor. Mirrors the attention Params uniform {n_heads, n_kv_heads,
+ * head_dim, seq} (kernels/sparse_attn.wgsl:12-17, engine/runtime.js:182) plus
+ * the allocation sizes the engine derives from engine/config.js:10-12,24. */
+typedef struct nwd_desc {
+  int32_t n_heads;     /* H, query heads (32 in the benchmark shapes, 40 in
+                          the Nano-4B model, engine/config.js:10)           */
+  int32_t n_kv_heads;  /* Hkv; H must be a multiple of Hkv and the group
+                          H/Hkv one of 1, 2, 4, 5, 8 (sparse_attn.wgsl:38)  */
+  int32_t head_dim;    /* D; 128 (engine/config.js:12)                      */
+  int32_t max_seq;     /* cache capacity in tokens per sequence             */
+  int32_t max_batch;   /* sequences per call                                */
+  int32_t q_dtype;     /* NWD_F16 or NWD_F32                                */
+  int32_t o_dtype;     /* NWD_F16 or NWD_F32                                */
+  int32_t kv_dtype;    /* type of the new K/V rows given to nwd_kv_append   */
+  float scale;         /* softmax scale; 0 means 1/sqrt(D) as the reference
+                          computes it (kernels/sparse_attn.wgsl:42)         */
+} nwd_desc;
+
+typedef struct nwd_ctx nwd_ctx;
+
+/* Creates a context on the current HIP device and allocates its split-K
+ * workspace and status word once (the reference allocates once too,
+ * engine/runtime.js:109-211). Replaces the attention slice of
+ * DecodeEngine._compile/_alloc (engine/runtime.js:101-102,170-173,182-183). */
+int nwd_create(const nwd_desc* desc, nwd_ctx** out_ctx);
+
+/* Frees the context's own device memory (never the caller's buffers). */
+void nwd_destroy(nwd_ctx* ctx);
+
+/* Message for the last failing call on ctx (or for nwd_create when ctx is
+ * NULL). Never NULL. */
+const char* nwd_last_error(const nwd_ctx* ctx);
+
+/* Bytes of ONE cache (K or V) for max_batch sequences of max_seq tokens:
+ * max_batch * n_kv_heads * max_seq * head_dim * 2. The reference's cache is
+ * f32 [maxSeq][kvHeads][headDim] (engine/runtime.js:171-172). */
+size_t nwd_cache_bytes(const nwd_ctx* ctx);
+
+/* Element index of (sequence b, token t, kv head h, dim d) in a cache:
+ * ((b * n_kv_heads + h) * max_seq + t) * head_dim + d. Each (b, h) owns one
+ * contiguous [max_seq][head_dim] fp16 slab, so a run of keys is one
+ * contiguous stream. The reference indexes (t * n_kv + h) * hd + d
+ * (kernels/sparse_attn.wgsl:49,107, kernels/kv_append.wgsl:17). */
+int64_t nwd_cache_offset(const nwd_ctx* ctx, int32_t b, int32_t t, int32_t h,
+                         int32_t d);
+
+/* Fused K+V append; replaces kv_append.wgsl main (:12-18) dispatched once for
+ * K and once for V (engine/runtime.js:389-390). For each sequence b < batch
+ * and new token j < n_tokens, copies row k_new[b][j][:][:] and
+ * v_new[b][j][:][:] ([n_kv_heads][head_dim], type desc.kv_dtype) into the
+ * caches at token pos[b] + j. fp16 rows are copied bit for bit; fp32 rows are
+ * rounded to nearest-even fp16. pos is a device int32[batch]. A position with
+ * pos[b] + n_tokens > max_seq is not written; the kernel records it in the
+ * status word (nwd_device_status). One launch. */
+int nwd_kv_append(nwd_ctx* ctx, const void* k_new, const void* v_new,
+                  void* k_cache, void* v_cache, const int32_t* pos,
+                  int32_t batch, int32_t n_tokens, void* stream);
+
+/* Decode attention; replaces sparse_attn.wgsl main (:31-114). For sequence b
+ * and query head h: out[b][h][:] = softmax(q[b][h] . K[b][h/G][0..L_b)^T *
+ * scale) . V[b][h/G][0..L_b), L_b = pos[b] + 1. q and out are
+ * [batch][n_heads][head_dim] in desc.q_dtype / desc.o_dtype. max_len bounds
+ * max_b L_b from the host side (the reference host knows seq, runtime.js:452);
+ * it only sizes the split-K grid: results are exact for any device positions,
+ * and 0 means max_seq. Long contexts are split across CUs into partial
+ * (max, sum, o) records that a merge pass combines (the argmax_partial /
+ * argmax_merge pattern, kernels/argmax_partial.wgsl:16-52,
+ * kernels/argmax_merge.wgsl:8-42); see nwd_set_decode_merge. */
+int nwd_decode_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
+                    const void* v_cache, const int32_t* pos, void* out,
+                    int32_t batch, int32_t max_len, void* stream);
+
+/* One attention-layer step in one launch: the fused form of kv_append for K
+ * and V followed by sparse_attn, which the reference encodes as three
+ * dispatches in one compute pass (engine/runtime.js:389-391). Appends one new
+ * token per sequence (k_new / v_new [batch][n_kv_heads][head_dim], type
+ * desc.kv_dtype, written at pos[b] exactly as nwd_kv_append does) and
+ * attends over L_b = pos[b] + 1 keys including it; q and out as in
+ * nwd_decode_attn. A position outside [0, max_seq) writes nothing and is
+ * reported by nwd_device_status. */
+int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new,
+                      const void* v_new, void* k_cache, void* v_cache,
+                      const int32_t* pos, void* out, int32_t batch,
+                      int32_t max_len, void* stream);
+
+/* Causal chunked prefill; replaces the token-by-token prefill of
+ * engine/runtime.js:640-643 (each prompt token runs kv_append then
+ * sparse_attn). The n_new new rows must already be in the caches at tokens
+ * pos0[b] .. pos0[b] + n_new - 1 (nwd_kv_append with n_tokens = n_new).
+ * Query i of sequence b attends keys 0 .. pos0[b] + i. q and out are
+ * [batch][n_new][n_heads][head_dim]. QK^T and PV run on fp16 MFMA with fp32
+ * accumulation. max_len bounds pos0[b] + n_new (0 means max_seq). */
+int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
+                     const void* v_cache, const int32_t* pos0, void* out,
+                     int32_t batch, int32_t n_new, int32_t max_len,
+                     void* stream);
+
+/* Synchronises the stream, returns NWD_OK if no kernel since the last call
+ * flagged an out-of-range device position (else NWD_ERR_DEVICE), and clears
+ * the flag. The reference throws at the host guard instead
+ * (engine/runtime.js:448). */
+int nwd_device_status(nwd_ctx* ctx, void* stream);
+
+/* Number of split-K partitions nwd_decode_attn launches for (batch, max_len),
+ * exposed so tests can force both the single-pass and the merged path. */
+int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len);
+
+/* Overrides the split count chosen by nwd_decode_attn (0 restores the
+ * automatic choice). Values are clamped to [1, 256]. Results do not depend on
+ * it beyond fp32 reordering. */
+int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
+
+/* Chooses where split-K records are merged: 0 (default) in the last
+ * workgroup of each (sequence, kv head) to finish, 1 in a separate merge
+ * kernel launched after the split kernel (the argmax_partial /
+ * argmax_merge two-launch shape, engine/runtime.js:398-399). Same results. */
+int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NWD_ATTN_H */

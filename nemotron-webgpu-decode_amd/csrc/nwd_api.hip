@@ -1,0 +1,314 @@
+// nwd_api.hip — the C ABI of libnwd_attn (declared in include/nwd_attn.h).
+//
+// Host-side validation and launch planning. Kernels never see a shape the
+// checks below have not accepted, and the context owns the only device
+// memory the library allocates (split-K workspace and the status word), once,
+// at nwd_create — as the reference engine allocates its buffers once in
+// DecodeEngine._alloc (engine/runtime.js:109-211).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/nwd_attn.h"
+#include "nwd_common.h"
+#include "nwd_internal.h"
+
+struct nwd_ctx {
+  nwd_desc desc;
+  nwd::Shape shape;
+  nwd::Workspace ws;
+  int device;
+  int forced_splits;
+  int separate_merge;
+  std::string err;
+};
+
+namespace {
+
+thread_local std::string g_create_err;
+
+// Workgroups one decode launch aims for: one 512-thread workgroup per CU.
+constexpr int kTargetWorkgroups = 256;
+constexpr int kMinKeysPerSplit = 128;    // one workgroup iteration
+constexpr int kMaxKeysPerSplit = 2048;   // bounds the slowest workgroup
+constexpr int kMaxSplits = 256;
+
+int fail(nwd_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
+int fail(nwd_ctx* ctx, int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  if (ctx) ctx->err = buf;
+  else g_create_err = buf;
+  return code;
+}
+
+int hip_fail(nwd_ctx* ctx, const char* what, hipError_t e) {
+  return fail(ctx, NWD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool group_supported(int g) { return g == 1 || g == 2 || g == 4 || g == 5 || g == 8; }
+
+int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
+  return max_len <= 0 ? ctx->desc.max_seq : max_len;
+}
+
+int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
+  const int units = (max_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
+  const int per_wave = batch * ctx->desc.n_kv_heads;
+  int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
+  const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work
+  if (by_len > n) n = by_len;
+  if (n > units) n = units;  // at least one 128-key unit per split
+  return n < 1 ? 1 : n;
+}
+
+int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
+  int cap = nwd::max_decode_splits(ctx->shape, ctx->ws, batch);
+  if (cap > kMaxSplits) cap = kMaxSplits;
+  if (n > cap) n = cap;
+  return n < 1 ? 1 : n;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
+  if (!out_ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_create: out_ctx is NULL");
+  *out_ctx = nullptr;
+  if (!d) return fail(nullptr, NWD_ERR_INVALID, "nwd_create: desc is NULL");
+  if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->head_dim <= 0 || d->max_seq <= 0 ||
+      d->max_batch <= 0)
+    return fail(nullptr, NWD_ERR_INVALID,
+                "nwd_create: sizes must be positive (n_heads=%d n_kv_heads=%d head_dim=%d "
+                "max_seq=%d max_batch=%d)",
+                d->n_heads, d->n_kv_heads, d->head_dim, d->max_seq, d->max_batch);
+  if (d->n_heads % d->n_kv_heads != 0)
+    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: n_heads %d is not a multiple of n_kv_heads %d",
+                d->n_heads, d->n_kv_heads);
+  const int group = d->n_heads / d->n_kv_heads;
+  if (!group_supported(group))
+    return fail(nullptr, NWD_ERR_UNSUPPORTED,
+                "nwd_create: group size n_heads/n_kv_heads = %d is not one of 1, 2, 4, 5, 8", group);
+  if (d->head_dim != nwd::kHeadDim)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "nwd_create: head_dim %d is not supported (only 128)",
+                d->head_dim);
+  for (int t : {d->q_dtype, d->o_dtype, d->kv_dtype})
+    if (t != NWD_F16 && t != NWD_F32)
+      return fail(nullptr, NWD_ERR_INVALID, "nwd_create: dtype %d is neither NWD_F16 nor NWD_F32", t);
+  if (!(d->scale >= 0.f) || std::isinf(d->scale))
+    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: scale must be finite and >= 0");
+  // Largest element index of a cache and of the query/output buffers must
+  // fit the kernels' 64-bit index math; keep the per-slab token index in int.
+  if ((int64_t)d->max_batch * d->n_kv_heads * (int64_t)d->max_seq > ((int64_t)1 << 40))
+    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: cache too large");
+  if ((int64_t)d->max_batch * d->n_kv_heads > (1 << 30))
+    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: max_batch * n_kv_heads too large");
+
+  nwd_ctx* ctx = new nwd_ctx();
+  ctx->desc = *d;
+  ctx->forced_splits = 0;
+  ctx->separate_merge = 0;
+  ctx->shape.n_heads = d->n_heads;
+  ctx->shape.n_kv = d->n_kv_heads;
+  ctx->shape.group = group;
+  ctx->shape.cap = d->max_seq;
+  ctx->shape.q16 = d->q_dtype == NWD_F16;
+  ctx->shape.o16 = d->o_dtype == NWD_F16;
+  ctx->shape.kv16 = d->kv_dtype == NWD_F16;
+  ctx->shape.qk_scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
+
+  hipError_t e = hipGetDevice(&ctx->device);
+  if (e != hipSuccess) {
+    delete ctx;
+    return fail(nullptr, NWD_ERR_HIP, "nwd_create: hipGetDevice: %s", hipGetErrorString(e));
+  }
+  // Split-K records: enough for kMaxSplits splits of one sequence, or
+  // kTargetWorkgroups*2 workgroups' worth at max_batch.
+  int64_t per_seq = (int64_t)d->n_heads * kMaxSplits;
+  int64_t at_batch = (int64_t)group * 2 * kTargetWorkgroups;
+  if ((int64_t)d->max_batch * d->n_heads > at_batch) at_batch = (int64_t)d->max_batch * d->n_heads;
+  ctx->ws.records = per_seq > at_batch ? per_seq : at_batch;
+  ctx->ws.part_o = nullptr;
+  ctx->ws.part_ml = nullptr;
+  ctx->ws.counters = nullptr;
+  ctx->ws.status = nullptr;
+  const size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
+  e = hipMalloc(&ctx->ws.part_o, ctx->ws.records * nwd::kHeadDim * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
+  if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
+  if (e == hipSuccess) e = hipMalloc(&ctx->ws.status, sizeof(int));
+  if (e == hipSuccess) e = hipMemset(ctx->ws.status, 0, sizeof(int));
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) {
+    nwd_destroy(ctx);
+    return fail(nullptr, NWD_ERR_HIP, "nwd_create: workspace allocation: %s", hipGetErrorString(e));
+  }
+  *out_ctx = ctx;
+  return NWD_OK;
+}
+
+void nwd_destroy(nwd_ctx* ctx) {
+  if (!ctx) return;
+  int prev = -1;
+  (void)hipGetDevice(&prev);
+  (void)hipSetDevice(ctx->device);
+  if (ctx->ws.part_o) (void)hipFree(ctx->ws.part_o);
+  if (ctx->ws.part_ml) (void)hipFree(ctx->ws.part_ml);
+  if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
+  if (ctx->ws.status) (void)hipFree(ctx->ws.status);
+  if (prev >= 0) (void)hipSetDevice(prev);
+  delete ctx;
+}
+
+const char* nwd_last_error(const nwd_ctx* ctx) {
+  return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+size_t nwd_cache_bytes(const nwd_ctx* ctx) {
+  if (!ctx) return 0;
+  return (size_t)ctx->desc.max_batch * ctx->desc.n_kv_heads * (size_t)ctx->desc.max_seq *
+         ctx->desc.head_dim * 2;
+}
+
+int64_t nwd_cache_offset(const nwd_ctx* ctx, int32_t b, int32_t t, int32_t h, int32_t d) {
+  if (!ctx || b < 0 || b >= ctx->desc.max_batch || t < 0 || t >= ctx->desc.max_seq || h < 0 ||
+      h >= ctx->desc.n_kv_heads || d < 0 || d >= ctx->desc.head_dim)
+    return -1;
+  return nwd::cache_index(b, t, h, d, ctx->desc.n_kv_heads, ctx->desc.max_seq);
+}
+
+int nwd_kv_append(nwd_ctx* ctx, const void* k_new, const void* v_new, void* k_cache,
+                  void* v_cache, const int32_t* pos, int32_t batch, int32_t n_tokens,
+                  void* stream) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_kv_append: ctx is NULL");
+  if (!k_new || !v_new || !k_cache || !v_cache || !pos)
+    return fail(ctx, NWD_ERR_INVALID, "nwd_kv_append: null buffer");
+  if (batch < 1 || batch > ctx->desc.max_batch)
+    return fail(ctx, NWD_ERR_CAPACITY, "nwd_kv_append: batch %d outside [1, max_batch=%d]", batch,
+                ctx->desc.max_batch);
+  if (n_tokens < 1 || n_tokens > ctx->desc.max_seq)
+    return fail(ctx, NWD_ERR_CAPACITY, "nwd_kv_append: n_tokens %d outside [1, max_seq=%d]",
+                n_tokens, ctx->desc.max_seq);
+  hipError_t e = nwd::launch_kv_append(ctx->shape, k_new, v_new, k_cache, v_cache, pos, batch,
+                                       n_tokens, ctx->ws.status, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_kv_append: launch", e);
+  return NWD_OK;
+}
+
+int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len) {
+  if (!ctx || batch < 1 || batch > ctx->desc.max_batch) return 0;
+  int len = resolve_len(ctx, max_len);
+  if (len > ctx->desc.max_seq) len = ctx->desc.max_seq;
+  int n = ctx->forced_splits > 0 ? ctx->forced_splits : auto_splits(ctx, batch, len);
+  return clamp_splits(ctx, batch, n);
+}
+
+int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_splits: ctx is NULL");
+  if (n_splits < 0) return fail(ctx, NWD_ERR_INVALID, "nwd_set_decode_splits: negative count");
+  ctx->forced_splits = n_splits > kMaxSplits ? kMaxSplits : n_splits;
+  return NWD_OK;
+}
+
+static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const void* k_new,
+                         const void* v_new, void* k_cache, void* v_cache, const int32_t* pos,
+                         void* out, int32_t batch, int32_t max_len, void* stream) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "%s: ctx is NULL", who);
+  if (!q || !k_cache || !v_cache || !pos || !out)
+    return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (batch < 1 || batch > ctx->desc.max_batch)
+    return fail(ctx, NWD_ERR_CAPACITY, "%s: batch %d outside [1, max_batch=%d]", who, batch,
+                ctx->desc.max_batch);
+  const int len = resolve_len(ctx, max_len);
+  if (len > ctx->desc.max_seq)
+    return fail(ctx, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
+                ctx->desc.max_seq);
+  nwd::DecodeCall c;
+  c.q = q;
+  c.k_cache = k_cache;
+  c.v_cache = v_cache;
+  c.pos = pos;
+  c.out = out;
+  c.k_new = k_new;
+  c.v_new = v_new;
+  c.batch = batch;
+  c.nsplit = nwd_decode_splits(ctx, batch, len);
+  c.fused_merge = ctx->separate_merge ? 0 : 1;
+  hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, who, e);
+  return NWD_OK;
+}
+
+int nwd_decode_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const void* v_cache,
+                    const int32_t* pos, void* out, int32_t batch, int32_t max_len,
+                    void* stream) {
+  return decode_common(ctx, "nwd_decode_attn", q, nullptr, nullptr, const_cast<void*>(k_cache),
+                       const_cast<void*>(v_cache), pos, out, batch, max_len, stream);
+}
+
+int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new, const void* v_new,
+                      void* k_cache, void* v_cache, const int32_t* pos, void* out,
+                      int32_t batch, int32_t max_len, void* stream) {
+  if (ctx && (!k_new || !v_new))
+    return fail(ctx, NWD_ERR_INVALID, "nwd_append_decode: null new K/V rows");
+  return decode_common(ctx, "nwd_append_decode", q, k_new, v_new, k_cache, v_cache, pos, out,
+                       batch, max_len, stream);
+}
+
+int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_merge: ctx is NULL");
+  ctx->separate_merge = separate_kernel ? 1 : 0;
+  return NWD_OK;
+}
+
+int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const void* v_cache,
+                     const int32_t* pos0, void* out, int32_t batch, int32_t n_new,
+                     int32_t max_len, void* stream) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_prefill_attn: ctx is NULL");
+  if (!q || !k_cache || !v_cache || !pos0 || !out)
+    return fail(ctx, NWD_ERR_INVALID, "nwd_prefill_attn: null buffer");
+  if (batch < 1 || batch > ctx->desc.max_batch)
+    return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: batch %d outside [1, max_batch=%d]",
+                batch, ctx->desc.max_batch);
+  if (n_new < 1 || n_new > ctx->desc.max_seq)
+    return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: n_new %d outside [1, max_seq=%d]", n_new,
+                ctx->desc.max_seq);
+  const int len = resolve_len(ctx, max_len);
+  if (len > ctx->desc.max_seq || len < n_new)
+    return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: max_len %d outside [n_new, max_seq=%d]",
+                len, ctx->desc.max_seq);
+  hipError_t e = nwd::launch_prefill(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new,
+                                     len, ctx->ws, (hipStream_t)stream);
+  if (e == hipErrorNotSupported)
+    return fail(ctx, NWD_ERR_UNSUPPORTED, "nwd_prefill_attn: this shape is not built");
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_prefill_attn: launch", e);
+  return NWD_OK;
+}
+
+int nwd_device_status(nwd_ctx* ctx, void* stream) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_device_status: ctx is NULL");
+  hipStream_t s = (hipStream_t)stream;
+  int host = 0;
+  hipError_t e = hipMemcpyAsync(&host, ctx->ws.status, sizeof(int), hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_device_status", e);
+  if (host == 0) return NWD_OK;
+  e = hipMemsetAsync(ctx->ws.status, 0, sizeof(int), s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_device_status: clear", e);
+  return fail(ctx, NWD_ERR_DEVICE,
+              "a kernel saw a position outside [0, max_seq=%d): the cache was not written "
+              "there and attention was clamped to the capacity",
+              ctx->desc.max_seq);
+}
+
+}  // extern "C"

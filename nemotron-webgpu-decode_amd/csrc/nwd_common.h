@@ -1,0 +1,63 @@
+// nwd_common.h — device helpers shared by the gfx950 kernels of libnwd_attn.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nwd {
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kHeadDim = 128;            // D, the only head size built
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -3.4028234663852886e38f;  // finite "minus infinity"
+
+// Status bits written by kernels into the context's device status word.
+constexpr int kStatusBadPos = 1;
+
+// Element index of (b, t, h, d) in a cache: each (sequence, kv head) owns a
+// contiguous [cap][D] fp16 slab, so the keys a workgroup streams are one run.
+__host__ __device__ inline int64_t cache_index(int b, int t, int h, int d,
+                                               int n_kv, int cap) {
+  return ((int64_t)(b * n_kv + h) * cap + t) * kHeadDim + d;
+}
+
+// DPP lane moves inside a row of 16 lanes (data-parallel primitives, no LDS).
+template <int kCtrl>
+__device__ inline float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), kCtrl,
+                                                    0xF, 0xF, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;   // lane i <- lane 7-i within 8 lanes
+constexpr int kDppRowMirror = 0x140;    // lane i <- lane 15-i within 16 lanes
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+__device__ inline float sum8(float x) {
+  x += dpp_mov<kDppQuadXor1>(x);
+  x += dpp_mov<kDppQuadXor2>(x);
+  x += dpp_mov<kDppHalfMirror>(x);
+  return x;
+}
+
+// Max over each aligned group of 8 lanes.
+__device__ inline float max8(float x) {
+  x = fmaxf(x, dpp_mov<kDppQuadXor1>(x));
+  x = fmaxf(x, dpp_mov<kDppQuadXor2>(x));
+  x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  return x;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float dot2(f16x2 a, f16x2 b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+}  // namespace nwd

@@ -1,0 +1,513 @@
+// nwd_decode.hip — decode GQA attention for gfx950 (split-K + merge).
+//
+// Replaces kernels/sparse_attn.wgsl main (:31-114). The reference runs one
+// 64-thread workgroup per QUERY head (engine/runtime.js:391), so each of the
+// G = H/Hkv query heads of a group re-reads the same K/V rows, with one
+// thread streaming one whole key row (uncoalesced), and it caps the context
+// at 256 keys (:29).
+//
+// Here one 512-thread workgroup (8 wavefronts, one workgroup per CU) owns
+// (sequence b, KV head hkv, split s): it loads each K/V row of its key range
+// once and serves all G query heads of the group from it.
+//
+// Mapping inside a wavefront: rows of kLanes lanes (8 for G <= 4, 16 for
+// larger groups); a row owns one key at a time and each lane holds 16 (or 8)
+// of its 128 dims as 16-byte runs, so one load instruction reads whole
+// 128-byte cache lines of consecutive keys. q.k is a packed fp16 dot
+// (v_dot2_f32_f16) or an fp32 FMA chain, summed over the row's lanes with DPP
+// moves, so every lane of the row holds the score. Each row runs its own
+// online softmax (running max and sum in log2 units, exp2 on the hardware)
+// and accumulates p * V for its dims in fp32 with no cross-lane traffic. The
+// next iteration's K/V loads are issued before the current one is computed,
+// unconditionally (clamped in range), so the wait before the compute only
+// waits for the older loads. At the end the row states are merged
+// (shuffles inside a wave, LDS across waves) into one record (m, l, o[128])
+// per query head.
+//
+// With one split the record is normalised and written to `out`. With
+// several, records go to the workspace and are merged — the partial/merge
+// structure of kernels/argmax_partial.wgsl:16-52 and
+// kernels/argmax_merge.wgsl:8-42, with (max, sum, o[D]) records instead of
+// (value, index) pairs. The merge runs either in a separate kernel
+// (decode_merge_kernel) or in the last workgroup of each (b, hkv) to finish
+// (an atomic arrival counter, no waiting), which saves a launch.
+//
+// Fused append: when new K/V rows are given, the workgroup whose range holds
+// the new position writes them into the caches and uses them from registers,
+// so an attention-layer step (kv_append x2 + attention in the reference,
+// engine/runtime.js:389-391) is one launch.
+#include "nwd_common.h"
+#include "nwd_internal.h"
+
+namespace nwd {
+
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+
+template <int G> struct DecodeCfg {
+  static constexpr int kLanes = G <= 4 ? 8 : 16;  // lanes per key row
+  static constexpr int kRows = 64 / kLanes;       // key rows per wavefront
+  static constexpr int kRuns = 16 / kLanes;       // 16-byte runs per lane per key
+  static constexpr int kDims = 8 * kRuns;          // dims per lane
+  static constexpr int kKpr = 2;                  // keys per row per iteration
+  static constexpr int kBlockKeys = kWaves * kRows * kKpr;
+};
+
+// Units the key range is split in (the largest block size, 128 keys).
+constexpr int kUnitKeys = 128;
+
+template <int N>
+__device__ inline float sum_lanes(float x) {
+  x += dpp_mov<kDppQuadXor1>(x);
+  x += dpp_mov<kDppQuadXor2>(x);
+  x += dpp_mov<kDppHalfMirror>(x);
+  if constexpr (N == 16) x += dpp_mov<kDppRowMirror>(x);
+  return x;
+}
+
+// One 16-byte run (8 values) of a new K/V row, fp16 or fp32 (rounded to
+// nearest even, as kv_append does).
+__device__ inline f16x8 load_src_run(const void* src, int64_t elem, bool src16) {
+  if (src16) return *reinterpret_cast<const f16x8*>(static_cast<const f16*>(src) + elem);
+  const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + elem);
+  f32x4 a = p[0], c = p[1];
+  f16x8 r;
+  r[0] = (f16)a[0]; r[1] = (f16)a[1]; r[2] = (f16)a[2]; r[3] = (f16)a[3];
+  r[4] = (f16)c[0]; r[5] = (f16)c[1]; r[6] = (f16)c[2]; r[7] = (f16)c[3];
+  return r;
+}
+
+// Merges the nsplit records of the G heads of one (b, hkv) and writes the
+// normalised outputs. 512 threads: thread t handles 4 dims (d4) of head g for
+// the splits s = r, r + R, ...; the R partial states are combined in LDS.
+template <int G, bool kO16>
+__device__ inline void merge_group(const float* __restrict__ part_o,
+                                   const float2* __restrict__ part_ml, void* __restrict__ out,
+                                   int64_t hrow0, int nsplit, float* lds) {
+  constexpr int P = G * 32;          // (head, 4-dim run) pairs
+  constexpr int R = kThreads / P;    // threads per pair
+  const int t = threadIdx.x;
+  const int p = t % P, r = t / P;
+  const int g = p / 32, d4 = p % 32;
+  const int64_t rec0 = (hrow0 + g) * nsplit;
+  float M = kNegBig, Lsum = 0.f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  if (r < R) {
+    int s = r;
+    for (; s + 3 * R < nsplit; s += 4 * R) {
+      float2 ml[4];
+      f32x4 ov[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ml[u] = part_ml[rec0 + s + u * R];
+        ov[u] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s + u * R) * kHeadDim + d4 * 4);
+      }
+      float Mn = M;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) Mn = fmaxf(Mn, ml[u].x);
+      const float a = fast_exp2(M - Mn);
+      Lsum *= a;
+      o *= a;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float w = fast_exp2(ml[u].x - Mn);
+        Lsum = fmaf(ml[u].y, w, Lsum);
+        o += ov[u] * w;
+      }
+      M = Mn;
+    }
+    for (; s < nsplit; s += R) {
+      const float2 ml = part_ml[rec0 + s];
+      const f32x4 ov = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
+      const float Mn = fmaxf(M, ml.x);
+      const float a = fast_exp2(M - Mn), w = fast_exp2(ml.x - Mn);
+      Lsum = fmaf(ml.y, w, Lsum * a);
+      o = o * a + ov * w;
+      M = Mn;
+    }
+    float* e = lds + (r * P + p) * 6;
+    e[0] = M; e[1] = Lsum; e[2] = o[0]; e[3] = o[1]; e[4] = o[2]; e[5] = o[3];
+  }
+  __syncthreads();
+  if (r == 0) {
+    float Mx = kNegBig;
+#pragma unroll
+    for (int k = 0; k < R; ++k) Mx = fmaxf(Mx, lds[(k * P + p) * 6]);
+    float lt = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+      const float* e = lds + (k * P + p) * 6;
+      const float w = fast_exp2(e[0] - Mx);
+      lt = fmaf(e[1], w, lt);
+      acc += f32x4{e[2], e[3], e[4], e[5]} * w;
+    }
+    const float inv = 1.f / lt;
+    const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
+    if constexpr (kO16) {
+      f16x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = (f16)(acc[i] * inv);
+      *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = v;
+    } else {
+      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = acc * inv;
+    }
+  }
+}
+
+struct DecodeArgs {
+  const void* q;
+  f16* k_cache;  // written only at the fused-append row
+  f16* v_cache;
+  const int32_t* pos;
+  void* out;
+  float* part_o;
+  float2* part_ml;
+  int* counters;      // [batch][n_kv] arrival counters, zero between calls
+  const void* k_new;  // optional new rows [batch][n_kv][D] (fused append)
+  const void* v_new;
+  int new16;          // new rows are fp16 (else fp32)
+  int n_heads, n_kv, cap, nsplit, fused_merge;
+  float qk_scale_log2;
+  int* status;
+};
+
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeArgs a) {
+  using C = DecodeCfg<G>;
+  constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
+  constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys;
+  constexpr int kWaveKeys = kRows * kKpr;
+  constexpr int kMergeFloats = kThreads * 6;
+  constexpr int kWaveFloats = kWaves * G * (kHeadDim + 2);
+  constexpr int kLdsFloats = kMergeFloats > kWaveFloats ? kMergeFloats : kWaveFloats;
+
+  __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
+  __shared__ int lds_last;
+  float* lds_o = lds;                                 // [kWaves][G][D]
+  float* lds_ml = lds + kWaves * G * kHeadDim;         // [kWaves][G][2]
+
+  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int row = lane / kLanes, col = lane % kLanes;
+
+  const int pos_raw = a.pos[b];
+  const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
+  if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
+  const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
+  const int nsplit = a.nsplit;
+
+  // This split's key range: whole 128-key units spread evenly over splits.
+  const int units = (L + kUnitKeys - 1) / kUnitKeys;
+  const int u0 = (int)((int64_t)split * units / nsplit);
+  const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
+  const int t0 = u0 * kUnitKeys;
+  const int t1 = min(L, u1 * kUnitKeys);
+  const int n_it = t1 > t0 ? (t1 - t0 + kBlockKeys - 1) / kBlockKeys : 0;
+
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  const f16* kbase = a.k_cache + slab + col * 8;
+  const f16* vbase = a.v_cache + slab + col * 8;
+
+  // Fused append: the split holding the new position writes the new rows
+  // and substitutes them for the cache rows it loads.
+  const int pnew = L - 1;
+  const bool owns_new = a.k_new != nullptr && pos_ok && t0 <= pnew && pnew < t1;
+  f16x8 nk[kRuns], nv[kRuns];
+  if (owns_new) {
+    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      nk[i] = load_src_run(a.k_new, src + (col + i * kLanes) * 8, a.new16);
+      nv[i] = load_src_run(a.v_new, src + (col + i * kLanes) * 8, a.new16);
+    }
+    if (tid < 32) {
+      const int run = tid & 15;
+      const void* s = tid < 16 ? a.k_new : a.v_new;
+      f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab +
+                 (int64_t)pnew * kHeadDim + run * 8;
+      *reinterpret_cast<f16x8*>(dst) = load_src_run(s, src + run * 8, a.new16);
+    }
+  }
+
+  // Query registers: this lane's dims of each of the G heads.
+  const int h0 = hkv * G;
+  const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kHeadDim + col * 8;
+  f16x8 q16[kQ16 ? G : 1][kRuns];
+  float q32[kQ16 ? 1 : G][kDims];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      const int64_t e = qoff + g * kHeadDim + i * kLanes * 8;
+      if constexpr (kQ16) {
+        q16[g][i] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + e);
+      } else {
+        const f32x4* qp = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + e);
+        const f32x4 x0 = qp[0], x1 = qp[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          q32[g][i * 8 + k] = x0[k];
+          q32[g][i * 8 + 4 + k] = x1[k];
+        }
+      }
+    }
+  }
+
+  struct Tile {
+    f16x8 k[kKpr][kRuns], v[kKpr][kRuns];
+  };
+
+  // Unconditional: iterations past the end reload the last key (cache hits).
+  auto load_tile = [&](Tile& tl, int it) {
+    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
+#pragma unroll
+    for (int j = 0; j < kKpr; ++j) {
+      const int t = min(base + j * kRows, t1 - 1);
+      const int64_t off = (int64_t)t * kHeadDim;
+#pragma unroll
+      for (int i = 0; i < kRuns; ++i) {
+        tl.k[j][i] = *reinterpret_cast<const f16x8*>(kbase + off + i * kLanes * 8);
+        tl.v[j][i] = *reinterpret_cast<const f16x8*>(vbase + off + i * kLanes * 8);
+      }
+    }
+  };
+
+  auto qk = [&](const Tile& tl, int j, int g) -> float {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      const f16x8& kk = tl.k[j][i];
+      if constexpr (kQ16) {
+        const f16x8& qq = q16[g][i];
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          acc = dot2(f16x2{qq[e], qq[e + 1]}, f16x2{kk[e], kk[e + 1]}, acc);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf(q32[g][i * 8 + e], (float)kk[e], acc);
+      }
+    }
+    return acc;
+  };
+
+  float m[G], l[G], acc[G][kDims];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDims; ++i) acc[g][i] = 0.f;
+  }
+
+  auto compute_tile = [&](Tile& tl, int it) {
+    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
+    if (owns_new) {
+#pragma unroll
+      for (int j = 0; j < kKpr; ++j) {
+        const bool sub = base + j * kRows == pnew;
+#pragma unroll
+        for (int i = 0; i < kRuns; ++i) {
+          tl.k[j][i] = sub ? nk[i] : tl.k[j][i];
+          tl.v[j][i] = sub ? nv[i] : tl.v[j][i];
+        }
+      }
+    }
+    float s[kKpr][G];
+#pragma unroll
+    for (int j = 0; j < kKpr; ++j) {
+      const bool valid = base + j * kRows < t1;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float d = sum_lanes<kLanes>(qk(tl, j, g));
+        s[j][g] = valid ? d * a.qk_scale_log2 : -INFINITY;
+      }
+    }
+    float mn[G];
+    bool grow = false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      mn[g] = m[g];
+#pragma unroll
+      for (int j = 0; j < kKpr; ++j) mn[g] = fmaxf(mn[g], s[j][g]);
+      grow |= mn[g] > m[g];
+    }
+    if (grow) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float al = fast_exp2(m[g] - mn[g]);
+        m[g] = mn[g];
+        l[g] *= al;
+#pragma unroll
+        for (int i = 0; i < kDims; ++i) acc[g][i] *= al;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kKpr; ++j) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = fast_exp2(s[j][g] - m[g]);
+        l[g] += p;
+#pragma unroll
+        for (int i = 0; i < kRuns; ++i)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            acc[g][i * 8 + e] = fmaf(p, (float)tl.v[j][i][e], acc[g][i * 8 + e]);
+      }
+    }
+  };
+
+  // Two register tiles; the loads of iteration it+1 are in flight while
+  // iteration it is computed.
+  if (n_it > 0) {
+    Tile ta, tb;
+    load_tile(ta, 0);
+    for (int it = 0; it < n_it; it += 2) {
+      load_tile(tb, min(it + 1, n_it - 1));
+      compute_tile(ta, it);
+      load_tile(ta, min(it + 2, n_it - 1));
+      if (it + 1 < n_it) compute_tile(tb, it + 1);
+    }
+  }
+
+  // Merge the row states of this wavefront (rows differ in the lane bits
+  // above log2(kLanes)).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = m[g];
+#pragma unroll
+    for (int sh = kLanes; sh < 64; sh <<= 1) M = fmaxf(M, __shfl_xor(M, sh));
+    const float sc = fast_exp2(m[g] - M);
+    float lg = l[g] * sc;
+#pragma unroll
+    for (int sh = kLanes; sh < 64; sh <<= 1) lg += __shfl_xor(lg, sh);
+#pragma unroll
+    for (int i = 0; i < kDims; ++i) {
+      float v = acc[g][i] * sc;
+#pragma unroll
+      for (int sh = kLanes; sh < 64; sh <<= 1) v += __shfl_xor(v, sh);
+      acc[g][i] = v;
+    }
+    m[g] = M;
+    l[g] = lg;
+  }
+  if (row == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int i = 0; i < kRuns; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          lds_o[(wave * G + g) * kHeadDim + (col + i * kLanes) * 8 + e] = acc[g][i * 8 + e];
+      if (col == 0) {
+        lds_ml[(wave * G + g) * 2] = m[g];
+        lds_ml[(wave * G + g) * 2 + 1] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  // Merge the wavefronts: one record (or the output) per head.
+  const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
+  for (int idx = tid; idx < G * kHeadDim; idx += kThreads) {
+    const int g = idx / kHeadDim, d = idx - g * kHeadDim;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
+    float o = 0.f, lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
+      o = fmaf(lds_o[(w * G + g) * kHeadDim + d], sc, o);
+      lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
+    }
+    if (nsplit == 1) {
+      const float r = o / lt;
+      if constexpr (kO16) static_cast<f16*>(a.out)[(hrow0 + g) * kHeadDim + d] = (f16)r;
+      else static_cast<float*>(a.out)[(hrow0 + g) * kHeadDim + d] = r;
+    } else {
+      const int64_t rec = (hrow0 + g) * nsplit + split;
+      a.part_o[rec * kHeadDim + d] = o;
+      if (d == 0) a.part_ml[rec] = make_float2(M, lt);
+    }
+  }
+  if (nsplit == 1 || !a.fused_merge) return;
+
+  // Last workgroup of this (b, hkv) to arrive merges the records.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) lds_last = atomicAdd(&a.counters[b * a.n_kv + hkv], 1) == nsplit - 1;
+  __syncthreads();
+  if (!lds_last) return;
+  __threadfence();
+  merge_group<G, kO16>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
+  if (tid == 0) a.counters[b * a.n_kv + hkv] = 0;
+}
+
+// Separate merge: one 512-thread workgroup per (kv head, sequence).
+template <int G, bool kO16>
+__global__ __launch_bounds__(kThreads) void decode_merge_kernel(
+    const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+    void* __restrict__ out, int n_heads, int nsplit) {
+  __shared__ __attribute__((aligned(16))) float lds[kThreads * 6];
+  const int hkv = blockIdx.x, b = blockIdx.y;
+  merge_group<G, kO16>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
+}
+
+template <int G, bool kQ16, bool kO16>
+static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
+  dim3 grid((unsigned)a.nsplit, (unsigned)a.n_kv, (unsigned)batch);
+  decode_split_kernel<G, kQ16, kO16><<<grid, kThreads, 0, stream>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
+  decode_merge_kernel<G, kO16><<<dim3((unsigned)a.n_kv, (unsigned)batch), kThreads, 0, stream>>>(
+      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit);
+  return hipGetLastError();
+}
+
+template <int G>
+static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, int batch, hipStream_t st) {
+  if (s.q16) return s.o16 ? launch_g<G, true, true>(a, batch, st) : launch_g<G, true, false>(a, batch, st);
+  return s.o16 ? launch_g<G, false, true>(a, batch, st) : launch_g<G, false, false>(a, batch, st);
+}
+
+hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
+                         hipStream_t stream) {
+  DecodeArgs a;
+  a.q = c.q;
+  a.k_cache = static_cast<f16*>(c.k_cache);
+  a.v_cache = static_cast<f16*>(c.v_cache);
+  a.pos = c.pos;
+  a.out = c.out;
+  a.part_o = ws.part_o;
+  a.part_ml = ws.part_ml;
+  a.counters = ws.counters;
+  a.k_new = c.k_new;
+  a.v_new = c.v_new;
+  a.new16 = s.kv16;
+  a.n_heads = s.n_heads;
+  a.n_kv = s.n_kv;
+  a.cap = s.cap;
+  a.nsplit = c.nsplit;
+  a.fused_merge = c.fused_merge;
+  a.qk_scale_log2 = s.qk_scale * kLog2e;
+  a.status = ws.status;
+  switch (s.group) {
+    case 1: return launch_qo<1>(s, a, c.batch, stream);
+    case 2: return launch_qo<2>(s, a, c.batch, stream);
+    case 4: return launch_qo<4>(s, a, c.batch, stream);
+    case 5: return launch_qo<5>(s, a, c.batch, stream);
+    case 8: return launch_qo<8>(s, a, c.batch, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int max_decode_splits(const Shape& s, const Workspace& ws, int batch) {
+  const int64_t per = (int64_t)batch * s.n_heads;
+  int64_t m = per > 0 ? ws.records / per : 0;
+  if (m > 256) m = 256;
+  return (int)m;
+}
+
+}  // namespace nwd

@@ -1,0 +1,150 @@
+"""Parity of the causal chunked prefill (nwd_prefill_attn, fp16 MFMA) with the
+oracle. The reference's prefill is token-by-token decode
+(engine/runtime.js:640-643), so query i of a chunk appended at pos0 must equal
+decode attention over keys 0..pos0+i; the oracle's sparse_attn restatement is
+run with seq = pos0 + i + 1 for each checked query."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import nwd_attn as nw  # noqa: E402
+import oracle  # noqa: E402
+from attn_cases import f32, kv_rows, max_abs, normal_f16, rng, to_cache  # noqa: E402
+from gpu_util import cache_rows_f32, dev, pos_tensor, randn_f16, say  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+D = 128
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a visible MI355X")
+    nw.load_library()
+
+
+def _run_prefill(H, Hkv, pos0s, n_new, seed, io="f16"):
+    """Appends n_new rows per sequence with nwd_kv_append, then prefills.
+    Returns (out [B][n_new][H][D] f32, q f16, per-seq token-major k, v)."""
+    B = len(pos0s)
+    g = rng(seed)
+    cap = max(pos0s) + n_new + 5
+    rows = [kv_rows(g, p + n_new, Hkv) for p in pos0s]
+    q16 = normal_f16(g, (B, n_new, H, D))
+    with nw.AttnContext(H, Hkv, cap, max_batch=B, q_dtype=io, o_dtype=io, kv_dtype="f16") as ctx:
+        kc = dev(to_cache([r[0][:p] for r, p in zip(rows, pos0s)], Hkv, cap))
+        vc = dev(to_cache([r[1][:p] for r, p in zip(rows, pos0s)], Hkv, cap))
+        pos = pos_tensor(pos0s)
+        knew = np.stack([r[0][p:] for r, p in zip(rows, pos0s)])
+        vnew = np.stack([r[1][p:] for r, p in zip(rows, pos0s)])
+        ctx.kv_append(dev(knew), dev(vnew), kc, vc, pos, B, n_new)
+        q = dev(f32(q16) if io == "f32" else q16)
+        out = torch.empty((B, n_new, H, D), dtype=q.dtype, device="cuda")
+        ctx.prefill(q, kc, vc, pos, out, B, n_new, max_len=cap)
+        assert ctx.device_status() == nw.NWD_OK
+        return out.float().cpu().numpy(), q16, rows
+
+
+def _check_rows(out, q16, rows, pos0s, queries):
+    worst = 0.0
+    for b, p in enumerate(pos0s):
+        kf, vf = f32(rows[b][0]), f32(rows[b][1])
+        for i in queries:
+            want = oracle.sparse_attn_f32(f32(q16[b, i]), kf[:p + i + 1], vf[:p + i + 1], threads=0)
+            worst = max(worst, max_abs(out[b, i], want))
+    return worst
+
+
+@pytest.mark.parametrize("G", [1, 2, 4, 5, 8])
+def test_prefill_small_all_queries(G):
+    Hkv = 2
+    say(f"prefill small G={G}")
+    pos0s, n_new = [100], 37
+    out, q16, rows = _run_prefill(G * Hkv, Hkv, pos0s, n_new, 80 + G)
+    assert _check_rows(out, q16, rows, pos0s, range(n_new)) < TOL
+
+
+def test_prefill_batch_ragged_f32_io():
+    say("prefill batch=3 f32 io")
+    pos0s, n_new = [0, 65, 300], 70
+    out, q16, rows = _run_prefill(32, 8, pos0s, n_new, 90, io="f32")
+    assert _check_rows(out, q16, rows, pos0s, range(0, n_new, 3)) < TOL
+
+
+def test_prefill_from_empty_cache_is_causal():
+    """pos0 = 0: query 0 sees only itself, so O = V[0] up to fp16 P rounding."""
+    say("prefill from empty cache")
+    out, q16, rows = _run_prefill(8, 2, [0], 129, 91)
+    assert max_abs(out[0, 0], np.repeat(f32(rows[0][1][0]), 4, axis=0)) < 1e-3
+    assert _check_rows(out, q16, rows, [0], range(129)) < TOL
+
+
+def test_config5_chunk512_onto_8192():
+    """32q/8kv/d128: 512 new tokens appended at 8192, causal within the chunk.
+    Sampled queries against the oracle; every query against a torch fp32
+    reference of the same masked softmax."""
+    H, Hkv, P, n_new = 32, 8, 8192, 512
+    cap = P + n_new
+    say("config5 prefill 512 onto 8192")
+    kc = randn_f16((1, Hkv, cap, D), 500)
+    vc = randn_f16((1, Hkv, cap, D), 501)
+    q = randn_f16((1, n_new, H, D), 502)
+    with nw.AttnContext(H, Hkv, cap) as ctx:
+        out = torch.empty_like(q)
+        ctx.prefill(q, kc, vc, pos_tensor([P]), out, 1, n_new, max_len=cap)
+        assert ctx.device_status() == nw.NWD_OK
+    got = out.float()
+    # torch fp32 reference, one kv head at a time
+    G = H // Hkv
+    worst_t = 0.0
+    keys = torch.arange(cap, device="cuda")
+    lim = P + torch.arange(n_new, device="cuda")
+    mask = keys[None, :] > lim[:, None]
+    for h in range(Hkv):
+        kf = kc[0, h].float()
+        vf = vc[0, h].float()
+        for g in range(G):
+            qf = q[0, :, h * G + g, :].float()
+            s = (qf @ kf.t()) / np.sqrt(D)
+            s = s.masked_fill(mask, float("-inf"))
+            ref = torch.softmax(s, dim=-1) @ vf
+            worst_t = max(worst_t, float((ref - got[0, :, h * G + g, :]).abs().max()))
+    assert worst_t < TOL, worst_t
+    # oracle on sampled queries (first, last, and a spread)
+    qh = q.float().cpu().numpy()
+    oh = got.cpu().numpy()
+    worst = 0.0
+    for i in (0, 1, 63, 64, 255, 256, 400, 511):
+        L = P + i + 1
+        want = oracle.sparse_attn_f32(qh[0, i], cache_rows_f32(kc, 0, L), cache_rows_f32(vc, 0, L),
+                                      threads=0)
+        worst = max(worst, max_abs(oh[0, i], want))
+    assert worst < TOL, worst
+
+
+def test_prefill_matches_sequential_decode():
+    """The chunk equals the reference's token-by-token loop run on the GPU
+    decode path (append one token, attend, repeat)."""
+    say("prefill == sequential decode")
+    H, Hkv, P, n_new = 32, 8, 40, 20
+    cap = P + n_new
+    g = rng(93)
+    k, v = kv_rows(g, cap, Hkv)
+    q = normal_f16(g, (1, n_new, H, D))
+    with nw.AttnContext(H, Hkv, cap, o_dtype="f32", q_dtype="f16") as ctx:
+        kc, vc = dev(to_cache([k[:P]], Hkv, cap)), dev(to_cache([v[:P]], Hkv, cap))
+        seq = []
+        for i in range(n_new):
+            pos = pos_tensor([P + i])
+            ctx.kv_append(dev(k[P + i:P + i + 1][None]), dev(v[P + i:P + i + 1][None]), kc, vc, pos, 1, 1)
+            o = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+            ctx.decode(dev(q[:, i]), kc, vc, pos, o, 1)
+            seq.append(o)
+        out = torch.empty((1, n_new, H, D), dtype=torch.float32, device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor([P]), out, 1, n_new)
+        torch.cuda.synchronize()
+    stepwise = torch.stack(seq, dim=1).cpu().numpy()
+    assert max_abs(out.cpu().numpy(), stepwise) < TOL
