@@ -185,6 +185,28 @@ def measure_32k(torch, nw):
     return res
 
 
+def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 10):
+    """Achievable HBM bandwidth of a plain device copy (torch copy_), read +
+    write bytes per second; also the kernel used to calibrate the
+    FETCH_SIZE / WRITE_SIZE counters (--copy-only)."""
+    a = torch.empty(nbytes // 2, dtype=torch.float16, device="cuda").uniform_()
+    b = torch.empty_like(a)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            b.copy_(a)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        for _ in range(reps):
+            b.copy_(a)
+        e1.record(s)
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return round(gbs, 1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,6 +214,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=256)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-32k", action="store_true")
+    ap.add_argument("--copy-only", action="store_true",
+                    help="only run 4 copies of 256 MiB (counter calibration) and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the decode-attention path runs on a single MI355X "
@@ -204,6 +228,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_only:
+        log(f"[bench] copy 256 MiB x4: {copy_bandwidth(torch, 1 << 28, 4)} GB/s")
+        return
     nw.load_library()
 
     past, window, layers = 4096, 64, 32
@@ -232,6 +259,8 @@ def main():
         log("[bench] 32k split-K")
         extra = measure_32k(torch, nw)
         log(f"[bench] 32k: {extra}")
+    copy_gbs = copy_bandwidth(torch)
+    log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
@@ -264,7 +293,7 @@ def main():
         "eager_us_per_step": round(eager_us, 3),
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_split_kernel (split-K with the merge in the last workgroup)",
+            "kernel": "nwd_decode_attn = decode_split_kernel + decode_merge_kernel",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -274,6 +303,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "decode_32k": extra,
+        "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(wall, 4),
     }
     print(json.dumps(line), flush=True)

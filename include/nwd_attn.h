@@ -123,16 +123,17 @@ int nwd_kv_append(nwd_ctx* ctx, const void* k_new, const void* v_new,
  * max_b L_b from the host side (the reference host knows seq, runtime.js:452);
  * it only sizes the split-K grid: results are exact for any device positions,
  * and 0 means max_seq. Long contexts are split across CUs into partial
- * (max, sum, o) records that a merge pass combines (the argmax_partial /
+ * (max, sum, o) records that are then merged (the argmax_partial /
  * argmax_merge pattern, kernels/argmax_partial.wgsl:16-52,
  * kernels/argmax_merge.wgsl:8-42); see nwd_set_decode_merge. */
 int nwd_decode_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
                     const void* v_cache, const int32_t* pos, void* out,
                     int32_t batch, int32_t max_len, void* stream);
 
-/* One attention-layer step in one launch: the fused form of kv_append for K
- * and V followed by sparse_attn, which the reference encodes as three
- * dispatches in one compute pass (engine/runtime.js:389-391). Appends one new
+/* One attention-layer step: the fused form of kv_append for K and V followed
+ * by sparse_attn, which the reference encodes as three dispatches in one
+ * compute pass (engine/runtime.js:389-391); here one launch, plus the merge
+ * kernel when the context is split (see nwd_set_decode_merge). Appends one new
  * token per sequence (k_new / v_new [batch][n_kv_heads][head_dim], type
  * desc.kv_dtype, written at pos[b] exactly as nwd_kv_append does) and
  * attends over L_b = pos[b] + 1 keys including it; q and out as in
@@ -170,10 +171,12 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len);
  * it beyond fp32 reordering. */
 int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 
-/* Chooses where split-K records are merged: 0 (default) in the last
- * workgroup of each (sequence, kv head) to finish, 1 in a separate merge
- * kernel launched after the split kernel (the argmax_partial /
- * argmax_merge two-launch shape, engine/runtime.js:398-399). Same results. */
+/* Chooses where split-K records are merged: 1 (default) in a separate merge
+ * kernel launched after the split kernel (the two-dispatch shape of
+ * argmax_partial / argmax_merge, engine/runtime.js:398-399); 0 inside the
+ * split kernel, by the last workgroup of each (sequence, kv head) to finish,
+ * for callers that want one launch per call. Same results, bit for bit; on
+ * MI355X the separate kernel is faster. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
 #ifdef __cplusplus

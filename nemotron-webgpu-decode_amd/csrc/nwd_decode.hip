@@ -6,14 +6,13 @@
 // thread streaming one whole key row (uncoalesced), and it caps the context
 // at 256 keys (:29).
 //
-// Here one 512-thread workgroup (8 wavefronts, one workgroup per CU) owns
-// (sequence b, KV head hkv, split s): it loads each K/V row of its key range
-// once and serves all G query heads of the group from it.
+// Here one 512-thread workgroup (8 wavefronts) owns (sequence b, KV head
+// hkv, split s): it loads each K/V row of its key range once and serves all G
+// query heads of the group from it. Two workgroups fit on a CU.
 //
-// Mapping inside a wavefront: rows of kLanes lanes (8 for G <= 4, 16 for
-// larger groups); a row owns one key at a time and each lane holds 16 (or 8)
-// of its 128 dims as 16-byte runs, so one load instruction reads whole
-// 128-byte cache lines of consecutive keys. q.k is a packed fp16 dot
+// Mapping inside a wavefront: 4 rows of 16 lanes; a row owns one key at a
+// time and each lane holds 8 of its 128 dims (one 16-byte run), so one load
+// instruction reads 1 KB of consecutive keys. q.k is a packed fp16 dot
 // (v_dot2_f32_f16) or an fp32 FMA chain, summed over the row's lanes with DPP
 // moves, so every lane of the row holds the score. Each row runs its own
 // online softmax (running max and sum in log2 units, exp2 on the hardware)
@@ -25,12 +24,22 @@
 // per query head.
 //
 // With one split the record is normalised and written to `out`. With
-// several, records go to the workspace and are merged — the partial/merge
-// structure of kernels/argmax_partial.wgsl:16-52 and
+// several, records go to the workspace and decode_merge_kernel combines them
+// — the partial/merge structure of kernels/argmax_partial.wgsl:16-52 and
 // kernels/argmax_merge.wgsl:8-42, with (max, sum, o[D]) records instead of
-// (value, index) pairs. The merge runs either in a separate kernel
-// (decode_merge_kernel) or in the last workgroup of each (b, hkv) to finish
-// (an atomic arrival counter, no waiting), which saves a launch.
+// (value, index) pairs. Optionally (nwd_set_decode_merge) the merge runs in
+// the split kernel itself: records are written with device-scope atomic
+// stores and the workgroup that takes the last arrival ticket of its
+// (b, hkv) merges them. That saves the second launch but costs three
+// serialised memory round trips at the end of every workgroup; on MI355X it
+// measured slower than the second kernel (15.2 vs 11.7 us for a 4K step), so
+// it is not the default. A release fence per workgroup instead of the
+// atomic stores would cost a full L2 write-back each (~0.15 us, serialised).
+//
+// The key range is partitioned from the host's length bound (max_len), not
+// from the device position, so a workgroup's first K/V loads do not wait for
+// the position load; the position only masks keys and bounds the loop, and
+// the last split extends past the bound if the position exceeds it.
 //
 // Fused append: when new K/V rows are given, the workgroup whose range holds
 // the new position writes them into the caches and uses them from registers,
@@ -41,15 +50,23 @@
 
 namespace nwd {
 
-constexpr int kWaves = 8;
+// Build-time tuning constants (the defaults are the measured best on MI355X).
+#ifndef NWD_DECODE_WAVES
+#define NWD_DECODE_WAVES 8
+#endif
+#ifndef NWD_DECODE_KEYS_PER_ROW
+#define NWD_DECODE_KEYS_PER_ROW 2
+#endif
+
+constexpr int kWaves = NWD_DECODE_WAVES;
 constexpr int kThreads = kWaves * 64;
 
 template <int G> struct DecodeCfg {
-  static constexpr int kLanes = G <= 4 ? 8 : 16;  // lanes per key row
+  static constexpr int kLanes = 16;               // lanes per key row
   static constexpr int kRows = 64 / kLanes;       // key rows per wavefront
   static constexpr int kRuns = 16 / kLanes;       // 16-byte runs per lane per key
   static constexpr int kDims = 8 * kRuns;          // dims per lane
-  static constexpr int kKpr = 2;                  // keys per row per iteration
+  static constexpr int kKpr = NWD_DECODE_KEYS_PER_ROW;  // keys per row per iteration
   static constexpr int kBlockKeys = kWaves * kRows * kKpr;
 };
 
@@ -77,10 +94,37 @@ __device__ inline f16x8 load_src_run(const void* src, int64_t elem, bool src16) 
   return r;
 }
 
+// Device-scope relaxed atomic accesses: coherent across the XCDs' L2 caches
+// without the full-L2 write-back a release fence costs.
+__device__ inline void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ inline float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// s_waitcnt vmcnt(0): every earlier global access of this thread is complete.
+__device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <bool kDev>
+__device__ inline float2 ld_ml(const float2* p) {
+  if constexpr (kDev) {
+    const float* f = reinterpret_cast<const float*>(p);
+    return make_float2(ld_dev(f), ld_dev(f + 1));
+  } else {
+    return *p;
+  }
+}
+template <bool kDev>
+__device__ inline f32x4 ld_o4(const float* p) {
+  if constexpr (kDev) return f32x4{ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
+  else return *reinterpret_cast<const f32x4*>(p);
+}
+
 // Merges the nsplit records of the G heads of one (b, hkv) and writes the
-// normalised outputs. 512 threads: thread t handles 4 dims (d4) of head g for
-// the splits s = r, r + R, ...; the R partial states are combined in LDS.
-template <int G, bool kO16>
+// normalised outputs. Thread t handles 4 dims (d4) of head g for the splits
+// s = r, r + R, ...; the R partial states are combined in LDS. kDev reads
+// the records with device-scope loads (merge inside the split kernel).
+template <int G, bool kO16, bool kDev>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
                                    int64_t hrow0, int nsplit, float* lds) {
@@ -93,36 +137,27 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
   float M = kNegBig, Lsum = 0.f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
   if (r < R) {
-    int s = r;
-    for (; s + 3 * R < nsplit; s += 4 * R) {
-      float2 ml[4];
-      f32x4 ov[4];
+    for (int s0 = r; s0 < nsplit; s0 += 8 * R) {
+      float2 ml[8];
+      f32x4 ov[8];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        ml[u] = part_ml[rec0 + s + u * R];
-        ov[u] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s + u * R) * kHeadDim + d4 * 4);
+      for (int u = 0; u < 8; ++u) {
+        const int s = min(s0 + u * R, nsplit - 1);  // in range; extras get zero weight
+        ml[u] = ld_ml<kDev>(part_ml + rec0 + s);
+        ov[u] = ld_o4<kDev>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
       }
       float Mn = M;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) Mn = fmaxf(Mn, ml[u].x);
+      for (int u = 0; u < 8; ++u) Mn = fmaxf(Mn, ml[u].x);
       const float a = fast_exp2(M - Mn);
       Lsum *= a;
       o *= a;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float w = fast_exp2(ml[u].x - Mn);
+      for (int u = 0; u < 8; ++u) {
+        const float w = s0 + u * R < nsplit ? fast_exp2(ml[u].x - Mn) : 0.f;
         Lsum = fmaf(ml[u].y, w, Lsum);
         o += ov[u] * w;
       }
-      M = Mn;
-    }
-    for (; s < nsplit; s += R) {
-      const float2 ml = part_ml[rec0 + s];
-      const f32x4 ov = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
-      const float Mn = fmaxf(M, ml.x);
-      const float a = fast_exp2(M - Mn), w = fast_exp2(ml.x - Mn);
-      Lsum = fmaf(ml.y, w, Lsum * a);
-      o = o * a + ov * w;
       M = Mn;
     }
     float* e = lds + (r * P + p) * 6;
@@ -163,11 +198,13 @@ struct DecodeArgs {
   void* out;
   float* part_o;
   float2* part_ml;
-  int* counters;      // [batch][n_kv] arrival counters, zero between calls
   const void* k_new;  // optional new rows [batch][n_kv][D] (fused append)
   const void* v_new;
   int new16;          // new rows are fp16 (else fp32)
-  int n_heads, n_kv, cap, nsplit, fused_merge;
+  int* counters;      // [batch][n_kv] arrival tickets, zero between calls
+  int n_heads, n_kv, cap, nsplit;
+  int span;           // host bound on L: keys [0, span) are partitioned
+  int fused_merge;    // merge in the split kernel's last workgroup
   float qk_scale_log2;
   int* status;
 };
@@ -183,7 +220,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   constexpr int kLdsFloats = kMergeFloats > kWaveFloats ? kMergeFloats : kWaveFloats;
 
   __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
-  __shared__ int lds_last;
   float* lds_o = lds;                                 // [kWaves][G][D]
   float* lds_ml = lds + kWaves * G * kHeadDim;         // [kWaves][G][2]
 
@@ -192,44 +228,41 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   const int lane = tid & 63, wave = tid >> 6;
   const int row = lane / kLanes, col = lane % kLanes;
 
-  const int pos_raw = a.pos[b];
-  const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
-  if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
-  const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
   const int nsplit = a.nsplit;
-
-  // This split's key range: whole 128-key units spread evenly over splits.
-  const int units = (L + kUnitKeys - 1) / kUnitKeys;
+  // This split's key range from the host bound: whole 128-key units spread
+  // evenly over the splits. Independent of the device position.
+  const int units = (a.span + kUnitKeys - 1) / kUnitKeys;
   const int u0 = (int)((int64_t)split * units / nsplit);
   const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
   const int t0 = u0 * kUnitKeys;
-  const int t1 = min(L, u1 * kUnitKeys);
-  const int n_it = t1 > t0 ? (t1 - t0 + kBlockKeys - 1) / kBlockKeys : 0;
+  const int t1h = min(a.span, u1 * kUnitKeys);
 
   const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
   const f16* kbase = a.k_cache + slab + col * 8;
   const f16* vbase = a.v_cache + slab + col * 8;
 
-  // Fused append: the split holding the new position writes the new rows
-  // and substitutes them for the cache rows it loads.
-  const int pnew = L - 1;
-  const bool owns_new = a.k_new != nullptr && pos_ok && t0 <= pnew && pnew < t1;
-  f16x8 nk[kRuns], nv[kRuns];
-  if (owns_new) {
-    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
+  struct Tile {
+    f16x8 k[kKpr][kRuns], v[kKpr][kRuns];
+  };
+
+  // Loads clamp to the capacity, never to the position: keys past L are
+  // loaded (in range) and masked, so no load address waits for pos.
+  auto load_tile = [&](Tile& tl, int it) {
+    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
 #pragma unroll
-    for (int i = 0; i < kRuns; ++i) {
-      nk[i] = load_src_run(a.k_new, src + (col + i * kLanes) * 8, a.new16);
-      nv[i] = load_src_run(a.v_new, src + (col + i * kLanes) * 8, a.new16);
+    for (int j = 0; j < kKpr; ++j) {
+      const int t = min(base + j * kRows, a.cap - 1);
+      const int64_t off = (int64_t)t * kHeadDim;
+#pragma unroll
+      for (int i = 0; i < kRuns; ++i) {
+        tl.k[j][i] = *reinterpret_cast<const f16x8*>(kbase + off + i * kLanes * 8);
+        tl.v[j][i] = *reinterpret_cast<const f16x8*>(vbase + off + i * kLanes * 8);
+      }
     }
-    if (tid < 32) {
-      const int run = tid & 15;
-      const void* s = tid < 16 ? a.k_new : a.v_new;
-      f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab +
-                 (int64_t)pnew * kHeadDim + run * 8;
-      *reinterpret_cast<f16x8*>(dst) = load_src_run(s, src + run * 8, a.new16);
-    }
-  }
+  };
+
+  Tile ta, tb;
+  load_tile(ta, 0);  // requested before the position is known
 
   // Query registers: this lane's dims of each of the G heads.
   const int h0 = hkv * G;
@@ -255,24 +288,35 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
     }
   }
 
-  struct Tile {
-    f16x8 k[kKpr][kRuns], v[kKpr][kRuns];
-  };
+  const int pos_raw = a.pos[b];
+  const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
+  if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
+  const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
+  // Keys this split attends: [t0, t1); the last split also takes any keys
+  // past the host bound.
+  const int t1 = split == nsplit - 1 ? L : min(t1h, L);
+  const int n_it = t1 > t0 ? (t1 - t0 + kBlockKeys - 1) / kBlockKeys : 0;
 
-  // Unconditional: iterations past the end reload the last key (cache hits).
-  auto load_tile = [&](Tile& tl, int it) {
-    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
+  // Fused append: the split holding the new position writes the new rows
+  // and substitutes them for the cache rows it loads.
+  const int pnew = L - 1;
+  const bool owns_new = a.k_new != nullptr && pos_ok && t0 <= pnew && pnew < t1;
+  f16x8 nk[kRuns], nv[kRuns];
+  if (owns_new) {
+    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
 #pragma unroll
-    for (int j = 0; j < kKpr; ++j) {
-      const int t = min(base + j * kRows, t1 - 1);
-      const int64_t off = (int64_t)t * kHeadDim;
-#pragma unroll
-      for (int i = 0; i < kRuns; ++i) {
-        tl.k[j][i] = *reinterpret_cast<const f16x8*>(kbase + off + i * kLanes * 8);
-        tl.v[j][i] = *reinterpret_cast<const f16x8*>(vbase + off + i * kLanes * 8);
-      }
+    for (int i = 0; i < kRuns; ++i) {
+      nk[i] = load_src_run(a.k_new, src + (col + i * kLanes) * 8, a.new16);
+      nv[i] = load_src_run(a.v_new, src + (col + i * kLanes) * 8, a.new16);
     }
-  };
+    if (tid < 32) {
+      const int run = tid & 15;
+      const void* s = tid < 16 ? a.k_new : a.v_new;
+      f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab +
+                 (int64_t)pnew * kHeadDim + run * 8;
+      *reinterpret_cast<f16x8*>(dst) = load_src_run(s, src + run * 8, a.new16);
+    }
+  }
 
   auto qk = [&](const Tile& tl, int j, int g) -> float {
     float acc = 0.f;
@@ -359,10 +403,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   };
 
   // Two register tiles; the loads of iteration it+1 are in flight while
-  // iteration it is computed.
+  // iteration it is computed. The first tile is requested before the
+  // position arrives.
   if (n_it > 0) {
-    Tile ta, tb;
-    load_tile(ta, 0);
     for (int it = 0; it < n_it; it += 2) {
       load_tile(tb, min(it + 1, n_it - 1));
       compute_tile(ta, it);
@@ -428,21 +471,38 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
       else static_cast<float*>(a.out)[(hrow0 + g) * kHeadDim + d] = r;
     } else {
       const int64_t rec = (hrow0 + g) * nsplit + split;
-      a.part_o[rec * kHeadDim + d] = o;
-      if (d == 0) a.part_ml[rec] = make_float2(M, lt);
+      if (a.fused_merge) {
+        st_dev(a.part_o + rec * kHeadDim + d, o);
+        if (d == 0) {
+          st_dev(reinterpret_cast<float*>(a.part_ml + rec), M);
+          st_dev(reinterpret_cast<float*>(a.part_ml + rec) + 1, lt);
+        }
+      } else {
+        a.part_o[rec * kHeadDim + d] = o;
+        if (d == 0) a.part_ml[rec] = make_float2(M, lt);
+      }
     }
   }
   if (nsplit == 1 || !a.fused_merge) return;
 
-  // Last workgroup of this (b, hkv) to arrive merges the records.
-  __threadfence();
+  // The workgroup that takes the last arrival ticket of this (b, hkv)
+  // merges. Each thread's record stores are complete (device-coherent)
+  // before the barrier, and the ticket is taken after it; the merging
+  // workgroup reads the records with device-scope loads. Nothing waits on
+  // another workgroup.
+  __shared__ int lds_last;
+  wait_vm();
   __syncthreads();
-  if (tid == 0) lds_last = atomicAdd(&a.counters[b * a.n_kv + hkv], 1) == nsplit - 1;
+  if (tid == 0) {
+    const int ticket = __hip_atomic_fetch_add(&a.counters[b * a.n_kv + hkv], 1, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+    lds_last = ticket == nsplit - 1;
+  }
   __syncthreads();
   if (!lds_last) return;
-  __threadfence();
-  merge_group<G, kO16>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
-  if (tid == 0) a.counters[b * a.n_kv + hkv] = 0;
+  merge_group<G, kO16, true>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
+  if (tid == 0)
+    __hip_atomic_store(&a.counters[b * a.n_kv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Separate merge: one 512-thread workgroup per (kv head, sequence).
@@ -452,7 +512,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
     void* __restrict__ out, int n_heads, int nsplit) {
   __shared__ __attribute__((aligned(16))) float lds[kThreads * 6];
   const int hkv = blockIdx.x, b = blockIdx.y;
-  merge_group<G, kO16>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
+  merge_group<G, kO16, false>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
 }
 
 template <int G, bool kQ16, bool kO16>
@@ -482,7 +542,6 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.out = c.out;
   a.part_o = ws.part_o;
   a.part_ml = ws.part_ml;
-  a.counters = ws.counters;
   a.k_new = c.k_new;
   a.v_new = c.v_new;
   a.new16 = s.kv16;
@@ -490,6 +549,8 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.n_kv = s.n_kv;
   a.cap = s.cap;
   a.nsplit = c.nsplit;
+  a.span = c.span;
+  a.counters = ws.counters;
   a.fused_merge = c.fused_merge;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;

@@ -23,7 +23,7 @@ struct Workspace {
   float* part_o;     // [records][D] unnormalised partial outputs
   float2* part_ml;   // [records] (running max in log2 units, sum of weights)
   int64_t records;   // capacity in records
-  int* counters;     // [max_batch][n_kv] merge arrival counters (zero between calls)
+  int* counters;     // [max_batch][n_kv] merge arrival tickets (zero between calls)
   int* status;       // device status word (kStatus* bits)
 };
 
@@ -39,7 +39,8 @@ struct DecodeCall {
   const void* v_new;
   int batch;
   int nsplit;
-  int fused_merge;  // merge in the last workgroup (else a separate kernel)
+  int span;  // host bound on the keys attended (max_len), partitions the splits
+  int fused_merge;  // merge in the split kernel (else a separate merge kernel)
 };
 
 hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new,

@@ -180,6 +180,8 @@ class AttnContext:
         self._check(self.lib.nwd_set_decode_splits(self.handle, n))
 
     def set_decode_merge(self, separate_kernel: bool):
+        """True (default): merge split-K records in a second kernel; False: in
+        the split kernel's last workgroup."""
         self._check(self.lib.nwd_set_decode_merge(self.handle, int(bool(separate_kernel))))
 
     # ------------------------------------------------------------ operations
@@ -198,7 +200,7 @@ class AttnContext:
 
     def append_decode(self, q, k_new, v_new, k_cache, v_cache, pos, out, batch: int,
                       max_len: int = 0, stream=None):
-        """kv_append (K, V) + sparse_attn of engine/runtime.js:389-391 in one launch."""
+        """kv_append (K, V) + sparse_attn of engine/runtime.js:389-391, fused."""
         self._check(self.lib.nwd_append_decode(self.handle, _ptr(q), _ptr(k_new), _ptr(v_new),
                                                _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out),
                                                batch, max_len, _stream(stream)))

@@ -190,15 +190,19 @@ def test_config3_past32768_outliers_split_k():
         assert auto > 1
         outs = {}
         for n in (0, 1, 7, 256):
-            for sep in (False, True):
+            for sep in (True, False):
                 say(f"config3 splits={n or auto} separate_merge={sep}")
                 ctx.set_decode_splits(n)
                 ctx.set_decode_merge(sep)
                 o = _decode(ctx, dev(q), kc, vc, pos, 1, max_len=P + 1)[0]
                 assert max_abs(o, want) < TOL, (n, sep)
-                if sep:
-                    assert np.array_equal(o, outs[n])  # same records, same merge order
+                if not sep:  # same records, same merge order: bit-identical
+                    assert np.array_equal(o, outs[n]), n
                 outs[n] = o
+        # a length bound below the true length still gives the exact result
+        ctx.set_decode_splits(0)
+        short = _decode(ctx, dev(q), kc, vc, pos, 1, max_len=1000)[0]
+        assert max_abs(short, want) < TOL
         assert ctx.device_status() == nw.NWD_OK
     for n in (1, 7, 256):
         assert max_abs(outs[n], outs[0]) < 1e-3
@@ -238,11 +242,13 @@ def test_split_invariance_small(L):
     with nw.AttnContext(H, Hkv, L, o_dtype="f32") as ctx:
         kc, vc = dev(to_cache([k], Hkv, L)), dev(to_cache([v], Hkv, L))
         for n in (1, 2, 3, 7, 64, 256):
-            for sep in (False, True):
-                ctx.set_decode_splits(n)
-                ctx.set_decode_merge(sep)
-                got = _decode(ctx, dev(q), kc, vc, pos_tensor([L - 1]), 1, torch.float32)[0]
-                assert max_abs(got, want) < TOL, (L, n, sep)
+            for max_len in (0, L, max(1, L // 3)):
+                for sep in (False, True):
+                    ctx.set_decode_splits(n)
+                    ctx.set_decode_merge(sep)
+                    got = _decode(ctx, dev(q), kc, vc, pos_tensor([L - 1]), 1, torch.float32,
+                                  max_len=max_len)[0]
+                    assert max_abs(got, want) < TOL, (L, n, max_len, sep)
 
 
 @pytest.mark.parametrize("G", [1, 4, 5, 8])
@@ -286,6 +292,31 @@ def test_append_decode_equals_two_launches(G, src):
         kk = f32(from_cache(host(kc1), b, past[b] + 1))
         vv = f32(from_cache(host(vc1), b, past[b] + 1))
         assert max_abs(want[b], oracle.sparse_attn_f32(f32(q[b]), kk, vv)) < TOL
+
+
+def test_fused_merge_repeated_calls_and_batches():
+    """Many back-to-back calls with changing inputs, batch sizes and split
+    counts: the in-kernel merge (arrival tickets) must give the separate-kernel
+    result every time."""
+    say("fused merge repeated")
+    H, Hkv, cap, B = 32, 8, 3000, 4
+    g = rng(77)
+    with nw.AttnContext(H, Hkv, cap, max_batch=B, o_dtype="f32") as ctx:
+        kc = randn_f16((B, Hkv, cap, D), 70)
+        vc = randn_f16((B, Hkv, cap, D), 71)
+        for it in range(12):
+            b = 1 + it % B
+            q = randn_f16((b, H, D), 100 + it)
+            pos = pos_tensor(g.integers(0, cap, size=b).tolist())
+            ctx.set_decode_splits([0, 3, 16, 64][it % 4])
+            outs = []
+            for sep in (True, False):
+                ctx.set_decode_merge(sep)
+                o = torch.empty((b, H, D), dtype=torch.float32, device="cuda")
+                ctx.decode(q, kc, vc, pos, o, b, cap)
+                outs.append(host(o))
+            assert np.array_equal(outs[0], outs[1]), it
+        assert ctx.device_status() == nw.NWD_OK
 
 
 def test_append_decode_bad_position_writes_nothing():
