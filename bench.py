@@ -20,7 +20,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -85,7 +84,87 @@ class DecodeWorkload:
         return tot / steps
 
 
-def time_graph(torch, wl: DecodeWorkload, steps: int, warmup: int, append=True):
+class RaggedWorkload:
+    """64 independent sequences, past lengths U{512..16384} from a seed, one
+    query per sequence per step; step s appends token s % window of every
+    sequence at past_b + token and attends (one nwd_append_decode call)."""
+
+    def __init__(self, torch, nw, batch: int = 64, window: int = 64, seed: int = 4):
+        import numpy as np
+
+        g = np.random.Generator(np.random.PCG64(seed))
+        self.past = g.integers(512, 16385, size=batch)
+        self.batch, self.window = batch, window
+        self.cap = int(self.past.max()) + window
+        tg = torch.Generator(device="cuda")
+        tg.manual_seed(seed)
+
+        def rnd(*shape):
+            return torch.randn(*shape, generator=tg, device="cuda", dtype=torch.float32).half()
+
+        self.kc = rnd(batch, HKV, self.cap, D)
+        self.vc = rnd(batch, HKV, self.cap, D)
+        self.q = rnd(window, batch, H, D)
+        self.knew = rnd(window, batch, HKV, D)
+        self.vnew = rnd(window, batch, HKV, D)
+        pos = self.past[None, :] + np.arange(window)[:, None]
+        self.pos = torch.tensor(pos, dtype=torch.int32, device="cuda")
+        self.out = torch.empty(batch, H, D, dtype=torch.float16, device="cuda")
+        self.ctx = nw.AttnContext(H, HKV, self.cap, max_batch=batch)
+
+    def step(self, s: int, stream, append=True):
+        i = s % self.window
+        if append:
+            self.ctx.append_decode(self.q[i], self.knew[i], self.vnew[i], self.kc, self.vc,
+                                   self.pos[i], self.out, self.batch, self.cap, stream)
+        else:
+            self.ctx.decode(self.q[i], self.kc, self.vc, self.pos[i], self.out, self.batch,
+                            self.cap, stream)
+
+    def mean_kv_bytes(self, steps: int) -> float:
+        tot = 0
+        for s in range(steps):
+            tot += sum(kv_bytes(int(p) + s % self.window + 1) for p in self.past)
+        return tot / steps
+
+
+class PrefillWorkload:
+    """Causal chunked prefill: 512 new tokens appended at 8192 (one
+    nwd_kv_append of 512 rows) then nwd_prefill_attn over them."""
+
+    def __init__(self, torch, nw, past: int = 8192, n_new: int = 512, seed: int = 5):
+        self.past, self.n_new, self.cap = past, n_new, past + n_new
+        tg = torch.Generator(device="cuda")
+        tg.manual_seed(seed)
+
+        def rnd(*shape):
+            return torch.randn(*shape, generator=tg, device="cuda", dtype=torch.float32).half()
+
+        self.kc = rnd(1, HKV, self.cap, D)
+        self.vc = rnd(1, HKV, self.cap, D)
+        self.q = rnd(1, n_new, H, D)
+        self.knew = rnd(1, n_new, HKV, D)
+        self.vnew = rnd(1, n_new, HKV, D)
+        self.out = torch.empty_like(self.q)
+        self.pos0 = torch.tensor([past], dtype=torch.int32, device="cuda")
+        self.ctx = nw.AttnContext(H, HKV, self.cap)
+
+    def step(self, s: int, stream, append=True):
+        if append:
+            self.ctx.kv_append(self.knew, self.vnew, self.kc, self.vc, self.pos0, 1, self.n_new,
+                               stream)
+        self.ctx.prefill(self.q, self.kc, self.vc, self.pos0, self.out, 1, self.n_new, self.cap,
+                         stream)
+
+    def flops(self) -> float:
+        """4*H*D*sum_i L_i: QK^T and PV, 2 flops per multiply-add each."""
+        return 4.0 * H * D * sum(self.past + i + 1 for i in range(self.n_new))
+
+    def mean_kv_bytes(self, steps: int) -> float:
+        return float(kv_bytes(self.cap))
+
+
+def time_graph(torch, wl, steps: int, warmup: int, append=True):
     """Warm up eagerly, capture `steps` steps into a HIP graph, replay it once
     untimed and once timed. Returns (wall seconds, device ms) of the timed replay."""
     stream = torch.cuda.Stream()
@@ -110,7 +189,7 @@ def time_graph(torch, wl: DecodeWorkload, steps: int, warmup: int, append=True):
     return wall, start.elapsed_time(end)
 
 
-def time_eager(torch, wl: DecodeWorkload, steps: int):
+def time_eager(torch, wl, steps: int):
     stream = torch.cuda.Stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -166,23 +245,86 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0):
     }
 
 
-def measure_32k(torch, nw):
-    """Split-K at 32K context: 4 rotating layer caches (537 MB), 64 steps."""
-    wl = DecodeWorkload(torch, nw, past=32768, window=64, layers=4, seed=33)
-    steps = 64
-    _, ms = time_graph(torch, wl, steps, warmup=8)
-    _, ms_dec = time_graph(torch, wl, steps, warmup=0, append=False)
-    b = wl.mean_kv_bytes(steps)
+EXTRA_WORKLOADS = {
+    "ragged-64": "ragged-64: 64 sequences, past U{512..16384} (seed 4), one query each, "
+                 "append+attend per step",
+    "prefill-512": "prefill-512: B=1, 512 new tokens onto 8192 cached, causal in the chunk, "
+                   "kv_append of 512 rows + fp16-MFMA prefill per step",
+}
+
+WORKLOADS = {
+    # name: (past, window, layers, description)
+    "decode-4k": (4096, 64, 32, "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, append+attend "
+                                "per step, 32 layer caches rotated (545 MB)"),
+    "decode-32k": (32768, 64, 4, "decode-32k: B=1, 32q/8kv/d128, past 32768 (1% +-8 outliers "
+                                 "in the parity tests), append+attend per step, split-K, 4 layer "
+                                 "caches rotated (537 MB)"),
+}
+
+
+def run_workload(torch, nw, name: str, steps: int, warmup: int):
+    """Times `steps` append+attend steps and `steps` decode-only calls of one
+    workload from HIP graphs; returns a dict of the measurements."""
+    past, window, layers, desc = WORKLOADS[name]
+    log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
+    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234)
+    wall, ms = time_graph(torch, wl, steps, warmup)
+    us_step = ms * 1e3 / steps
+    mean_b = wl.mean_kv_bytes(steps)
+    # the dominant work alone: one nwd_decode_attn call per step, same rotation
+    _, ms_dec = time_graph(torch, wl, steps, 0, append=False)
+    dec_us = ms_dec * 1e3 / steps
+    n_eager = min(steps, 512)
+    eager_us = time_eager(torch, wl, n_eager) * 1e3 / n_eager
     res = {
-        "workload": "decode-32k: past 32768, 4 layer caches rotated, 64 steps",
-        "us_per_step": round(ms * 1e3 / steps, 3),
-        "decode_us": round(ms_dec * 1e3 / steps, 3),
-        "kv_read_gbs": round(b / (ms_dec * 1e-3 / steps) / 1e9, 1),
+        "workload": name, "desc": desc, "past": past, "window": window, "layers": layers,
+        "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
+        "decode_us": dec_us, "decode_gbs": mean_b / (dec_us * 1e-6) / 1e9,
+        "eager_us_per_step": eager_us, "mean_kv_bytes": mean_b, "wall_s": wall,
         "splits": wl.ctx.decode_splits(1, wl.cap),
     }
-    res["hbm_frac"] = round(res["kv_read_gbs"] / HBM_PEAK_GBS, 4)
+    log(f"[bench] {name}: step {us_step:.3f} us ({res['gbs']:.1f} GB/s), decode {dec_us:.3f} us "
+        f"({res['decode_gbs']:.1f} GB/s), eager step {eager_us:.3f} us")
     wl.ctx.close()
+    del wl
+    torch.cuda.empty_cache()
     return res
+
+
+def run_extra(torch, nw, name: str, steps: int, warmup: int):
+    """The ragged batch and the prefill chunk (measured on request)."""
+    log(f"[bench] {name}: {steps} steps")
+    wl = RaggedWorkload(torch, nw) if name == "ragged-64" else PrefillWorkload(torch, nw)
+    wall, ms = time_graph(torch, wl, steps, warmup)
+    _, ms_main = time_graph(torch, wl, steps, 0, append=False)
+    us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
+    res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us_step,
+           "main_us": us_main, "wall_s": wall, "mean_kv_bytes": wl.mean_kv_bytes(steps)}
+    if name == "prefill-512":
+        res["tflops"] = wl.flops() / (us_main * 1e-6) / 1e12
+        res["flops"] = wl.flops()
+    else:
+        res["splits"] = wl.ctx.decode_splits(wl.batch, wl.cap)
+        res["gbs"] = res["mean_kv_bytes"] / (us_step * 1e-6) / 1e9
+        res["decode_gbs"] = res["mean_kv_bytes"] / (us_main * 1e-6) / 1e9
+    log(f"[bench] {name}: {res}")
+    wl.ctx.close()
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
+def measured_traffic(name: str):
+    """HBM bytes per nwd_decode_attn call of `name` from the committed
+    counter summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled by
+    the plain-copy calibration), or None if it has not been profiled."""
+    f = ROOT / "profiles" / f"{name}_pmc.md"
+    if not f.exists():
+        return None
+    for line in f.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_call:"):
+            return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 10):
@@ -212,8 +354,11 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2048)
     ap.add_argument("--warmup", type=int, default=256)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(EXTRA_WORKLOADS),
+                    default="decode-4k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-32k", action="store_true")
+    ap.add_argument("--no-32k", action="store_true",
+                    help="skip the secondary decode-32k measurement")
     ap.add_argument("--copy-only", action="store_true",
                     help="only run 4 copies of 256 MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -233,40 +378,29 @@ def main():
         return
     nw.load_library()
 
-    past, window, layers = 4096, 64, 32
-    log(f"[bench] setup: past={past} window={window} layers={layers}")
-    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234)
-    log(f"[bench] timing {args.steps} steps (graph), warmup {args.warmup}")
-    wall, ms = time_graph(torch, wl, args.steps, args.warmup)
-    us_step = ms * 1e3 / args.steps
-    mean_b = wl.mean_kv_bytes(args.steps)
-    gbs = mean_b / (us_step * 1e-6) / 1e9
-    log(f"[bench] step: {us_step:.3f} us, {gbs:.1f} GB/s")
-    # the dominant kernel work alone: decode calls only, same rotation
-    _, ms_dec = time_graph(torch, wl, args.steps, 0, append=False)
-    dec_us = ms_dec * 1e3 / args.steps
-    achieved = mean_b / (dec_us * 1e-6) / 1e9
-    eager_ms = time_eager(torch, wl, min(args.steps, 512))
-    eager_us = eager_ms * 1e3 / min(args.steps, 512)
-    log(f"[bench] decode-only {dec_us:.3f} us ({achieved:.1f} GB/s); eager step {eager_us:.3f} us")
-    splits = wl.ctx.decode_splits(1, wl.cap)
-    wl.ctx.close()
-    del wl
-    torch.cuda.empty_cache()
-
+    if args.workload in EXTRA_WORKLOADS:
+        r = run_extra(torch, nw, args.workload, args.steps, args.warmup)
+        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
+              flush=True)
+        return
+    main_res = run_workload(torch, nw, args.workload, args.steps, args.warmup)
     extra = None
-    if not args.no_32k:
-        log("[bench] 32k split-K")
-        extra = measure_32k(torch, nw)
-        log(f"[bench] 32k: {extra}")
+    if args.workload == "decode-4k" and not args.no_32k:
+        r = run_workload(torch, nw, "decode-32k", 256, 16)
+        extra = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
+                 if k not in ("desc", "mean_kv_bytes")}
+        extra["hbm_frac"] = round(r["decode_gbs"] / HBM_PEAK_GBS, 4)
     copy_gbs = copy_bandwidth(torch)
     log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
-        cpu = cpu_baseline(past, window)
+        cpu = cpu_baseline(main_res["past"], main_res["window"])
         log(f"[bench] cpu: {cpu}")
 
+    us_step, gbs = main_res["us_per_step"], main_res["gbs"]
+    achieved = main_res["decode_gbs"]
+    traffic = measured_traffic(args.workload)
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -284,13 +418,13 @@ def main():
         "storage_dtype": "f16",
         "data": "synthetic (seeded N(0,1) fp16 K/V/Q)",
         "config": {
-            "workload": "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, append+attend "
-                        "per step, 32 layer caches rotated",
-            "batch": 1, "n_heads": H, "n_kv_heads": HKV, "head_dim": D, "past": past,
-            "window": window, "layers": layers, "decode_splits": splits,
+            "workload": main_res["desc"],
+            "batch": 1, "n_heads": H, "n_kv_heads": HKV, "head_dim": D,
+            "past": main_res["past"], "window": main_res["window"],
+            "layers": main_res["layers"], "decode_splits": main_res["splits"],
             "timing": "one HIP graph replay of `steps` steps, hipEvents",
         },
-        "eager_us_per_step": round(eager_us, 3),
+        "eager_us_per_step": round(main_res["eager_us_per_step"], 3),
         "roofline": {
             "bound": "hbm",
             "kernel": "nwd_decode_attn = decode_split_kernel + decode_merge_kernel",
@@ -298,13 +432,14 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "decode_us": round(dec_us, 3),
+            "traffic": traffic,
+            "algorithmic_bytes": int(main_res["mean_kv_bytes"]),
+            "decode_us": round(main_res["decode_us"], 3),
         },
         "cpu_baseline": cpu,
         "decode_32k": extra,
         "device_copy_gbs": copy_gbs,
-        "wall_s_timed": round(wall, 4),
+        "wall_s_timed": round(main_res["wall_s"], 4),
     }
     print(json.dumps(line), flush=True)
 

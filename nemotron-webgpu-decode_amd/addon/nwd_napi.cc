@@ -1,0 +1,349 @@
+// nwd_napi.cc — Node.js N-API addon over the C ABI of libnwd_attn.
+//
+// This is the binding a JavaScript host (the reference's engine/runtime.js,
+// or js/attention_layer.js here) uses in place of WebGPU buffers, bind
+// groups and dispatches for the attention slice:
+//   createEmptyStorage (kernels/gpu.js:91-96)      -> malloc / free
+//   queue.writeBuffer / mapAsync readback
+//     (engine/runtime.js:451-452, kernels/gpu.js:141-169) -> upload / download
+//   dispatchWorkgroups of kv_append / sparse_attn
+//     (engine/runtime.js:389-391)                  -> kvAppend / decode /
+//                                                      appendDecode / prefill
+// Device addresses cross into JavaScript as BigInt so the host can offset
+// into a buffer (one position entry per step) the way the reference offsets
+// uniform writes. Every failing call throws an Error naming the operation
+// and carrying the library's message, as the reference names the failing
+// bind group (engine/runtime.js:431-445).
+#include <hip/hip_runtime_api.h>
+#include <node_api.h>
+
+#include <cstdint>
+#include <cstring>
+#include <string>
+
+#include "nwd_attn.h"
+
+namespace {
+
+napi_value throw_error(napi_env env, const std::string& msg) {
+  napi_throw_error(env, nullptr, msg.c_str());
+  return nullptr;
+}
+
+bool get_args(napi_env env, napi_callback_info info, size_t want, napi_value* argv) {
+  size_t argc = want;
+  if (napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr) != napi_ok) return false;
+  for (size_t i = argc; i < want; ++i) napi_get_undefined(env, &argv[i]);
+  return true;
+}
+
+bool get_ptr(napi_env env, napi_value v, void** out) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_null || t == napi_undefined) {
+    *out = nullptr;
+    return true;
+  }
+  uint64_t u = 0;
+  bool lossless = false;
+  if (t == napi_bigint) {
+    if (napi_get_value_bigint_uint64(env, v, &u, &lossless) != napi_ok || !lossless) return false;
+  } else if (t == napi_number) {
+    double d = 0;
+    napi_get_value_double(env, v, &d);
+    if (d < 0) return false;
+    u = (uint64_t)d;
+  } else {
+    return false;
+  }
+  *out = reinterpret_cast<void*>(static_cast<uintptr_t>(u));
+  return true;
+}
+
+bool get_i32(napi_env env, napi_value v, int32_t* out, int32_t dflt) {
+  napi_valuetype t;
+  napi_typeof(env, v, &t);
+  if (t == napi_undefined) {
+    *out = dflt;
+    return true;
+  }
+  return napi_get_value_int32(env, v, out) == napi_ok;
+}
+
+napi_value make_ptr(napi_env env, const void* p) {
+  napi_value r;
+  napi_create_bigint_uint64(env, static_cast<uint64_t>(reinterpret_cast<uintptr_t>(p)), &r);
+  return r;
+}
+
+napi_value make_i32(napi_env env, int32_t v) {
+  napi_value r;
+  napi_create_int32(env, v, &r);
+  return r;
+}
+
+nwd_ctx* get_ctx(napi_env env, napi_value v) {
+  void* p = nullptr;
+  if (!get_ptr(env, v, &p) || !p) return nullptr;
+  return static_cast<nwd_ctx*>(p);
+}
+
+napi_value check(napi_env env, nwd_ctx* ctx, const char* op, int rc) {
+  if (rc == NWD_OK) return make_i32(env, 0);
+  return throw_error(env, std::string(op) + ": " + nwd_last_error(ctx) + " (status " +
+                              std::to_string(rc) + ")");
+}
+
+// Typed array -> (data, bytes)
+bool get_bytes(napi_env env, napi_value v, void** data, size_t* bytes) {
+  bool is_ta = false;
+  napi_is_typedarray(env, v, &is_ta);
+  if (!is_ta) return false;
+  napi_typedarray_type type;
+  size_t length = 0, offset = 0;
+  napi_value ab;
+  if (napi_get_typedarray_info(env, v, &type, &length, data, &ab, &offset) != napi_ok) return false;
+  size_t elem = 1;
+  switch (type) {
+    case napi_int16_array: case napi_uint16_array: elem = 2; break;
+    case napi_int32_array: case napi_uint32_array: case napi_float32_array: elem = 4; break;
+    case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: elem = 8; break;
+    default: elem = 1;
+  }
+  *bytes = length * elem;
+  return true;
+}
+
+int32_t field(napi_env env, napi_value obj, const char* name, int32_t dflt) {
+  bool has = false;
+  napi_has_named_property(env, obj, name, &has);
+  if (!has) return dflt;
+  napi_value v;
+  napi_get_named_property(env, obj, name, &v);
+  int32_t r = dflt;
+  napi_get_value_int32(env, v, &r);
+  return r;
+}
+
+// create({nHeads, nKvHeads, headDim, maxSeq, maxBatch, qF16, oF16, kvF16, scale}) -> ctx
+napi_value Create(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  if (!get_args(env, info, 1, argv)) return throw_error(env, "create: bad arguments");
+  nwd_desc d;
+  d.n_heads = field(env, argv[0], "nHeads", 0);
+  d.n_kv_heads = field(env, argv[0], "nKvHeads", 0);
+  d.head_dim = field(env, argv[0], "headDim", 128);
+  d.max_seq = field(env, argv[0], "maxSeq", 0);
+  d.max_batch = field(env, argv[0], "maxBatch", 1);
+  d.q_dtype = field(env, argv[0], "qF16", 0) ? NWD_F16 : NWD_F32;
+  d.o_dtype = field(env, argv[0], "oF16", 0) ? NWD_F16 : NWD_F32;
+  d.kv_dtype = field(env, argv[0], "kvF16", 0) ? NWD_F16 : NWD_F32;
+  d.scale = 0.f;
+  bool has = false;
+  napi_has_named_property(env, argv[0], "scale", &has);
+  if (has) {
+    napi_value v;
+    double s = 0;
+    napi_get_named_property(env, argv[0], "scale", &v);
+    napi_get_value_double(env, v, &s);
+    d.scale = (float)s;
+  }
+  nwd_ctx* ctx = nullptr;
+  int rc = nwd_create(&d, &ctx);
+  if (rc != NWD_OK)
+    return throw_error(env, std::string("create: ") + nwd_last_error(nullptr));
+  return make_ptr(env, ctx);
+}
+
+napi_value Destroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  nwd_destroy(get_ctx(env, argv[0]));
+  return make_i32(env, 0);
+}
+
+napi_value CacheBytes(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  nwd_ctx* ctx = get_ctx(env, argv[0]);
+  if (!ctx) return throw_error(env, "cacheBytes: ctx is null");
+  napi_value r;
+  napi_create_bigint_uint64(env, nwd_cache_bytes(ctx), &r);
+  return r;
+}
+
+napi_value Malloc(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  int64_t bytes = 0;
+  bool lossless = true;
+  napi_valuetype t;
+  napi_typeof(env, argv[0], &t);
+  if (t == napi_bigint) napi_get_value_bigint_int64(env, argv[0], &bytes, &lossless);
+  else napi_get_value_int64(env, argv[0], &bytes);
+  if (bytes <= 0 || !lossless) return throw_error(env, "malloc: size must be positive");
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, (size_t)bytes);
+  if (e != hipSuccess) return throw_error(env, std::string("malloc: ") + hipGetErrorString(e));
+  return make_ptr(env, p);
+}
+
+napi_value Free(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  void* p = nullptr;
+  if (!get_ptr(env, argv[0], &p)) return throw_error(env, "free: bad pointer");
+  if (p) (void)hipFree(p);
+  return make_i32(env, 0);
+}
+
+// upload(devPtr, typedArray): synchronous host -> device copy
+napi_value Upload(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  void* dst = nullptr;
+  void* src = nullptr;
+  size_t bytes = 0;
+  if (!get_ptr(env, argv[0], &dst) || !dst || !get_bytes(env, argv[1], &src, &bytes))
+    return throw_error(env, "upload: expected (devicePtr, TypedArray)");
+  hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) return throw_error(env, std::string("upload: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+// download(typedArray, devPtr): synchronous device -> host copy
+napi_value Download(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  void* dst = nullptr;
+  void* src = nullptr;
+  size_t bytes = 0;
+  if (!get_bytes(env, argv[0], &dst, &bytes) || !get_ptr(env, argv[1], &src) || !src)
+    return throw_error(env, "download: expected (TypedArray, devicePtr)");
+  hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return throw_error(env, std::string("download: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+// zero(devPtr, bytes): the engine's reset() wipe (engine/runtime.js:615-633)
+napi_value Zero(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  void* dst = nullptr;
+  int64_t bytes = 0;
+  bool lossless = true;
+  napi_valuetype t;
+  napi_typeof(env, argv[1], &t);
+  if (t == napi_bigint) napi_get_value_bigint_int64(env, argv[1], &bytes, &lossless);
+  else napi_get_value_int64(env, argv[1], &bytes);
+  if (!get_ptr(env, argv[0], &dst) || !dst || bytes < 0 || !lossless)
+    return throw_error(env, "zero: expected (devicePtr, bytes)");
+  hipError_t e = hipMemset(dst, 0, (size_t)bytes);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (e != hipSuccess) return throw_error(env, std::string("zero: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+napi_value Sync(napi_env env, napi_callback_info info) {
+  (void)info;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return throw_error(env, std::string("sync: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+// kvAppend(ctx, kNew, vNew, kCache, vCache, pos, batch, nTokens)
+napi_value KvAppend(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  get_args(env, info, 8, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *kn, *vn, *kc, *vc, *pos;
+  int32_t batch, n;
+  if (!ctx || !get_ptr(env, a[1], &kn) || !get_ptr(env, a[2], &vn) || !get_ptr(env, a[3], &kc) ||
+      !get_ptr(env, a[4], &vc) || !get_ptr(env, a[5], &pos) || !get_i32(env, a[6], &batch, 1) ||
+      !get_i32(env, a[7], &n, 1))
+    return throw_error(env, "kvAppend: bad arguments");
+  return check(env, ctx, "kvAppend",
+               nwd_kv_append(ctx, kn, vn, kc, vc, static_cast<const int32_t*>(pos), batch, n, nullptr));
+}
+
+// decode(ctx, q, kCache, vCache, pos, out, batch, maxLen)
+napi_value Decode(napi_env env, napi_callback_info info) {
+  napi_value a[8];
+  get_args(env, info, 8, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *q, *kc, *vc, *pos, *out;
+  int32_t batch, max_len;
+  if (!ctx || !get_ptr(env, a[1], &q) || !get_ptr(env, a[2], &kc) || !get_ptr(env, a[3], &vc) ||
+      !get_ptr(env, a[4], &pos) || !get_ptr(env, a[5], &out) || !get_i32(env, a[6], &batch, 1) ||
+      !get_i32(env, a[7], &max_len, 0))
+    return throw_error(env, "decode: bad arguments");
+  return check(env, ctx, "decode",
+               nwd_decode_attn(ctx, q, kc, vc, static_cast<const int32_t*>(pos), out, batch,
+                               max_len, nullptr));
+}
+
+// appendDecode(ctx, q, kNew, vNew, kCache, vCache, pos, out, batch, maxLen)
+napi_value AppendDecode(napi_env env, napi_callback_info info) {
+  napi_value a[10];
+  get_args(env, info, 10, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *q, *kn, *vn, *kc, *vc, *pos, *out;
+  int32_t batch, max_len;
+  if (!ctx || !get_ptr(env, a[1], &q) || !get_ptr(env, a[2], &kn) || !get_ptr(env, a[3], &vn) ||
+      !get_ptr(env, a[4], &kc) || !get_ptr(env, a[5], &vc) || !get_ptr(env, a[6], &pos) ||
+      !get_ptr(env, a[7], &out) || !get_i32(env, a[8], &batch, 1) || !get_i32(env, a[9], &max_len, 0))
+    return throw_error(env, "appendDecode: bad arguments");
+  return check(env, ctx, "appendDecode",
+               nwd_append_decode(ctx, q, kn, vn, kc, vc, static_cast<const int32_t*>(pos), out,
+                                 batch, max_len, nullptr));
+}
+
+// prefill(ctx, q, kCache, vCache, pos0, out, batch, nNew, maxLen)
+napi_value Prefill(napi_env env, napi_callback_info info) {
+  napi_value a[9];
+  get_args(env, info, 9, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *q, *kc, *vc, *pos, *out;
+  int32_t batch, n_new, max_len;
+  if (!ctx || !get_ptr(env, a[1], &q) || !get_ptr(env, a[2], &kc) || !get_ptr(env, a[3], &vc) ||
+      !get_ptr(env, a[4], &pos) || !get_ptr(env, a[5], &out) || !get_i32(env, a[6], &batch, 1) ||
+      !get_i32(env, a[7], &n_new, 1) || !get_i32(env, a[8], &max_len, 0))
+    return throw_error(env, "prefill: bad arguments");
+  return check(env, ctx, "prefill",
+               nwd_prefill_attn(ctx, q, kc, vc, static_cast<const int32_t*>(pos), out, batch,
+                                n_new, max_len, nullptr));
+}
+
+// deviceStatus(ctx) -> 0, or throws with the position error
+napi_value DeviceStatus(napi_env env, napi_callback_info info) {
+  napi_value a[1];
+  get_args(env, info, 1, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  if (!ctx) return throw_error(env, "deviceStatus: ctx is null");
+  return check(env, ctx, "deviceStatus", nwd_device_status(ctx, nullptr));
+}
+
+napi_value Init(napi_env env, napi_value exports) {
+  const napi_property_descriptor props[] = {
+      {"create", nullptr, Create, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"destroy", nullptr, Destroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"cacheBytes", nullptr, CacheBytes, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"malloc", nullptr, Malloc, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"free", nullptr, Free, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"upload", nullptr, Upload, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"download", nullptr, Download, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"zero", nullptr, Zero, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"sync", nullptr, Sync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"kvAppend", nullptr, KvAppend, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"decode", nullptr, Decode, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"appendDecode", nullptr, AppendDecode, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"prefill", nullptr, Prefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"deviceStatus", nullptr, DeviceStatus, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+  };
+  napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
+  return exports;
+}
+
+}  // namespace
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, Init)

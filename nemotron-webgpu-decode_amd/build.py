@@ -20,7 +20,9 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libnwd_attn.so"
+ADDON = PKG / "lib" / "nwd_napi.node"
 INCLUDE = PKG.parent / "include"
+NODE_INCLUDE = Path(os.environ.get("NODE_INCLUDE", "/usr/include/node"))
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -68,7 +70,27 @@ def build(jobs: int | None = None) -> Path:
     return LIB
 
 
+def build_addon() -> Path | None:
+    """Builds the Node.js N-API addon (lib/nwd_napi.node) over libnwd_attn.so
+    with g++ (host code only). Returns None when the Node headers are absent."""
+    if not (NODE_INCLUDE / "node_api.h").exists():
+        return None
+    src = PKG / "addon" / "nwd_napi.cc"
+    tmp = ADDON.with_suffix(".node.tmp")
+    cmd = ["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           "-D__HIP_PLATFORM_AMD__", "-DNODE_GYP_MODULE_NAME=nwd_napi",
+           f"-I{NODE_INCLUDE}", f"-I{INCLUDE}", "-I/opt/rocm/include", str(src),
+           "-o", str(tmp), f"-L{LIB.parent}", "-lnwd_attn", "-L/opt/rocm/lib", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"addon build failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, ADDON)
+    return ADDON
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     print(build(ap.parse_args().jobs))
+    print(build_addon())

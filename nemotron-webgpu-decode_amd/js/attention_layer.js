@@ -1,0 +1,115 @@
+'use strict';
+// Attention slice of the reference DecodeEngine (engine/runtime.js) on the
+// MI355X library, through the N-API addon (addon/nwd_napi.cc).
+//
+// The reference, per attention layer and token:
+//   _alloc    f32 q/k/v/attnO buffers and per-layer K/V caches
+//             [maxSeq][kvHeads][headDim] (engine/runtime.js:120-123,170-173)
+//   _bind     kvK = [k, kCache, uKv], kvV = [v, vCache, uKv],
+//             attn = [q, kCache, vCache, attnO, uAttn]   (:331-333)
+//   _ops      kvK, kvV, attn dispatched in one pass        (:389-391)
+//   submitStep guard seq < maxSeq (:448); uKv.seq = seq, uAttn.seq = seq+1
+//             (:451-452); submit; seq++ (:467)
+//   reset     zero-fill the caches (:615-633)
+// Here the three dispatches are one appendDecode call, the caches are fp16
+// (head-major, see include/nwd_attn.h), and the position is one device int32
+// that the host writes before each step, as the reference writes its
+// uniforms. q/k/v/attnO stay f32, the reference's activation type, so the
+// q/k/v GEMVs and the o_proj GEMV bind unchanged.
+const path = require('path');
+
+const ADDON = path.join(__dirname, '..', 'lib', 'nwd_napi.node');
+// eslint-disable-next-line import/no-dynamic-require
+const addon = require(ADDON);
+
+// Nemotron-3-Nano-4B attention shapes (engine/config.js:10-12,24,31).
+const NANO4B = { heads: 40, kvHeads: 8, headDim: 128, maxSeq: 256 };
+const ATTN_LAYERS = [12, 17, 24, 32];
+
+class AttentionSlice {
+  constructor({ heads = NANO4B.heads, kvHeads = NANO4B.kvHeads, headDim = NANO4B.headDim,
+                maxSeq = NANO4B.maxSeq, layers = ATTN_LAYERS } = {}) {
+    this.heads = heads;
+    this.kvHeads = kvHeads;
+    this.headDim = headDim;
+    this.maxSeq = maxSeq;
+    this.layers = layers.slice();
+    this.ctx = addon.create({ nHeads: heads, nKvHeads: kvHeads, headDim, maxSeq, maxBatch: 1,
+                              qF16: 0, oF16: 0, kvF16: 0 });
+    const f32 = (n) => addon.malloc(n * 4);
+    this.q = f32(heads * headDim);
+    this.k = f32(kvHeads * headDim);
+    this.v = f32(kvHeads * headDim);
+    this.attnO = f32(heads * headDim);
+    this.cacheBytes = addon.cacheBytes(this.ctx);
+    this.kCache = new Map();
+    this.vCache = new Map();
+    for (const i of this.layers) {
+      this.kCache.set(i, addon.malloc(this.cacheBytes));
+      this.vCache.set(i, addon.malloc(this.cacheBytes));
+    }
+    this.pos = addon.malloc(4);
+    this.seq = 0;
+    this.reset();
+  }
+
+  // runtime.js:615-633 (the KV part of reset)
+  reset() {
+    this.seq = 0;
+    for (const i of this.layers) {
+      addon.zero(this.kCache.get(i), this.cacheBytes);
+      addon.zero(this.vCache.get(i), this.cacheBytes);
+    }
+  }
+
+  // runtime.js:448,451-452: guard and position write before the token's ops
+  beginStep() {
+    if (this.seq >= this.maxSeq) throw new Error(`seq ${this.seq} exceeds maxSeq ${this.maxSeq}`);
+    addon.upload(this.pos, new Int32Array([this.seq]));
+  }
+
+  // What the q/k/v GEMVs of a layer write (runtime.js:386-388, outputs :120-122).
+  setQKV(q, k, v) {
+    addon.upload(this.q, q);
+    addon.upload(this.k, k);
+    addon.upload(this.v, v);
+  }
+
+  // runtime.js:389-391 for attention layer i: kvK, kvV, attn in one call.
+  encodeLayer(i) {
+    if (!this.kCache.has(i)) throw new Error(`layer ${i} is not an attention layer`);
+    addon.appendDecode(this.ctx, this.q, this.k, this.v, this.kCache.get(i), this.vCache.get(i),
+                       this.pos, this.attnO, 1, this.seq + 1);
+  }
+
+  // The two-dispatch form kept by the reference (kv_append, then attention):
+  // same results, used by the harness to check both entry points.
+  encodeLayerTwoCalls(i) {
+    addon.kvAppend(this.ctx, this.k, this.v, this.kCache.get(i), this.vCache.get(i), this.pos, 1, 1);
+    addon.decode(this.ctx, this.q, this.kCache.get(i), this.vCache.get(i), this.pos, this.attnO, 1,
+                 this.seq + 1);
+  }
+
+  // runtime.js:467
+  endStep() {
+    addon.deviceStatus(this.ctx);  // synchronises; throws on a bad device position
+    this.seq += 1;
+  }
+
+  readAttnO(out = new Float32Array(this.heads * this.headDim)) {
+    addon.download(out, this.attnO);
+    return out;
+  }
+
+  destroy() {
+    for (const p of [this.q, this.k, this.v, this.attnO, this.pos]) addon.free(p);
+    for (const i of this.layers) {
+      addon.free(this.kCache.get(i));
+      addon.free(this.vCache.get(i));
+    }
+    addon.destroy(this.ctx);
+    this.ctx = null;
+  }
+}
+
+module.exports = { AttentionSlice, NANO4B, ATTN_LAYERS, addon };

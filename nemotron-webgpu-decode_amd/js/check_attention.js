@@ -1,0 +1,84 @@
+'use strict';
+// Drives AttentionSlice the way DecodeEngine.generate drives the attention
+// layers (engine/runtime.js:635-648): token after token, every attention
+// layer, the position advancing once per token. Inputs come from a seeded
+// LCG; inputs and attention outputs are written to <outDir> for the Python
+// parity test, which checks them against the oracle.
+//
+// usage: node check_attention.js <outDir> [heads kvHeads tokens maxSeq]
+const fs = require('fs');
+const path = require('path');
+const { AttentionSlice } = require('./attention_layer');
+
+function lcg(seed) {
+  let s = seed >>> 0;
+  return () => {
+    s = (Math.imul(s, 1664525) + 1013904223) >>> 0;
+    return s / 4294967296;
+  };
+}
+
+function normals(rand, n) {
+  const out = new Float32Array(n);
+  for (let i = 0; i < n; i += 2) {
+    const u = Math.max(rand(), 1e-12);
+    const r = Math.sqrt(-2 * Math.log(u));
+    const t = 2 * Math.PI * rand();
+    out[i] = r * Math.cos(t);
+    if (i + 1 < n) out[i + 1] = r * Math.sin(t);
+  }
+  return out;
+}
+
+function main() {
+  const outDir = process.argv[2];
+  const heads = Number(process.argv[3] || 40);
+  const kvHeads = Number(process.argv[4] || 8);
+  const tokens = Number(process.argv[5] || 153);
+  const maxSeq = Number(process.argv[6] || 256);
+  const headDim = 128;
+  fs.mkdirSync(outDir, { recursive: true });
+  const slice = new AttentionSlice({ heads, kvHeads, headDim, maxSeq });
+  const rand = lcg(20260512);
+  const qAll = [];
+  const kAll = [];
+  const vAll = [];
+  const oAll = [];
+  for (let t = 0; t < tokens; t++) {
+    slice.beginStep();
+    for (const layer of slice.layers) {
+      const q = normals(rand, heads * headDim);
+      const k = normals(rand, kvHeads * headDim);
+      const v = normals(rand, kvHeads * headDim);
+      slice.setQKV(q, k, v);
+      if ((t + layer) % 2 === 0) slice.encodeLayer(layer);
+      else slice.encodeLayerTwoCalls(layer);
+      qAll.push(q);
+      kAll.push(k);
+      vAll.push(v);
+      oAll.push(slice.readAttnO());
+    }
+    slice.endStep();
+  }
+  // the maxSeq guard (runtime.js:448) must throw, not write past the cache
+  let guard = 'no-throw';
+  if (tokens === maxSeq) {
+    try {
+      slice.beginStep();
+    } catch (e) {
+      guard = String(e.message);
+    }
+  }
+  const cat = (arrs) => Buffer.concat(arrs.map((a) => Buffer.from(a.buffer, a.byteOffset, a.byteLength)));
+  fs.writeFileSync(path.join(outDir, 'q.f32'), cat(qAll));
+  fs.writeFileSync(path.join(outDir, 'k.f32'), cat(kAll));
+  fs.writeFileSync(path.join(outDir, 'v.f32'), cat(vAll));
+  fs.writeFileSync(path.join(outDir, 'o.f32'), cat(oAll));
+  fs.writeFileSync(path.join(outDir, 'manifest.json'), JSON.stringify({
+    heads, kvHeads, headDim, tokens, maxSeq, layers: slice.layers, guard,
+  }));
+  slice.destroy();
+  console.log(`check_attention: ${tokens} tokens x ${slice.layers.length} layers written to ${outDir}`);
+}
+
+main();
