@@ -8,29 +8,54 @@
 //
 // GQA packing: for one KV head the G query heads of the group and the n_new
 // queries form n_new*G rows (row R = query R/G, head R%G) that all share the
-// same K/V stream. A workgroup owns 64*RB consecutive rows (4 wavefronts of
-// 16*RB rows) and walks 64-key tiles:
-//   - the tile's K rows are staged in LDS row-major and its V rows in LDS
-//     transposed (V^T[d][key]), both with padding against bank conflicts;
-//     the next tile's loads are in flight while the current one computes;
+// same K/V stream. A workgroup (8 wavefronts) owns 64 consecutive rows and
+// walks 128-key tiles. Wavefront w computes row group w%2 (32 rows, two
+// 16-row MFMA blocks) against key quarter w/2 (32 keys) of each tile: every
+// K/V fragment read from LDS feeds two MFMAs, which halves LDS traffic per
+// flop against 16-row waves, and two wavefronts share each SIMD so the
+// matrix cores always have a second wavefront to issue from.
+//   - K and V rows are staged in LDS row-major with coalesced 16-byte loads
+//     and stores, padded against bank conflicts and double-buffered: the
+//     next tile's global loads are in flight during the current tile's MFMAs
+//     and one barrier per tile suffices;
 //   - S^T = K Q^T on v_mfma_f32_16x16x32_f16 (K from LDS as the A operand,
-//     the query rows held in registers as the B operand), so each lane ends
-//     up with 4 consecutive keys of ONE row — its own softmax row;
-//   - scale, causal mask, online softmax in log2 units (exp2), then
-//     O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
+//     the query rows held in registers as the B operand), so each lane holds
+//     4 consecutive keys of ONE row — its own softmax row;
+//   - causal mask only on tiles that cross a row's limit; online softmax in
+//     log2 units with the scale folded into the exp2 argument (one FMA per
+//     score); O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
 //     registers from the S^T accumulators with no data movement between
-//     lanes, and V^T comes from LDS with two 8-byte reads per operand;
-//   - accumulation is fp32 throughout; O is normalised once at the end.
+//     lanes, and V^T is read from the row-major V tile with two
+//     ds_read_b64_tr_b16 transpose loads per operand (gfx950): within a
+//     16-lane group, output lane j element e comes from position j%4 of the
+//     8 bytes lane 4e + j/4 addresses, so lanes 4e..4e+3 addressing 16
+//     consecutive dims of key row e give lane j V[key_e][d0 + j];
+//   - the four key quarters of a row group are merged through LDS at the
+//     end; accumulation is fp32 throughout and O is normalised once.
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
 namespace nwd {
 
-constexpr int kPWaves = 4;
+constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPBN = 64;                   // keys per tile
-constexpr int kKsStride = kHeadDim + 8;    // halves per K row in LDS (272 B)
-constexpr int kVtStride = kPBN + 8;        // halves per V^T row in LDS (144 B)
+constexpr int kPBM = 64;                    // rows per workgroup
+constexpr int kPBN = 128;                   // keys per tile
+constexpr int kKsStride = kHeadDim + 8;     // halves per K row in LDS (68 dwords: 16-byte
+                                            // reads of 16 rows hit distinct banks)
+constexpr int kVsStride = kHeadDim + 16;    // halves per V row in LDS (72 dwords: the 4 rows
+                                            // of a transpose load hit distinct banks)
+constexpr int kKsHalves = kPBN * kKsStride;
+constexpr int kVsHalves = kPBN * kVsStride;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Transpose load of 4 fp16 values (see the header comment for the lanes).
+__device__ inline f16x4 lds_read_tr16(const f16* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
 
 __device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -51,19 +76,18 @@ __device__ inline f16x8 load_q8(const void* q, int64_t elem) {
 }
 
 // grid: one workgroup per (row tile, kv head, sequence), kv head fastest so
-// consecutive workgroups (which the dispatcher spreads over the XCDs) of one
-// XCD share a KV head and its K/V stream in that XCD's L2.
-template <int G, int RB, bool kQ16, bool kO16>
-__global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(
+// that the workgroups the dispatcher sends to one XCD share a KV head and its
+// K/V stream in that XCD's L2.
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
     const void* __restrict__ q, const f16* __restrict__ k_cache,
     const f16* __restrict__ v_cache, const int32_t* __restrict__ pos0,
     void* __restrict__ out, int n_heads, int n_kv, int cap, int n_new,
     int mtiles, float qk_scale_log2, int* __restrict__ status) {
-  constexpr int kWaveRows = 16 * RB;
-  constexpr int kBM = kPWaves * kWaveRows;
-
-  __shared__ __attribute__((aligned(16))) f16 Ks[kPBN * kKsStride];
-  __shared__ __attribute__((aligned(16))) f16 Vt[kHeadDim * kVtStride];
+  constexpr int RB = 2;  // 16-row MFMA blocks per wavefront
+  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  f16* Ks = smem;                       // [2][kPBN][kKsStride]
+  f16* Vs = smem + 2 * kKsHalves;       // [2][kPBN][kVsStride]
 
   const int id = blockIdx.x;
   const int hkv = id % n_kv;
@@ -73,6 +97,7 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lq = lane >> 4;
+  const int rg = wave & 1, kq = wave >> 1;  // row group (32 rows), key quarter (32 keys)
 
   int P0 = pos0[b];
   if (P0 < 0 || P0 > cap - n_new) {
@@ -80,22 +105,23 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(
     P0 = P0 < 0 ? 0 : cap - n_new;
   }
   const int total_rows = n_new * G;
-  const int row_base = mt * kBM + wave * kWaveRows;
-  const int r_last = min(mt * kBM + kBM, total_rows) - 1;
+  const int r_last = min(mt * kPBM + kPBM, total_rows) - 1;
   const int kend = P0 + r_last / G + 1;  // keys this workgroup needs
   const int ntiles = (kend + kPBN - 1) / kPBN;
 
-  // Query rows as the B operand of S^T = K Q^T: lane holds
-  // Q[row rb*16+lr][db*32 + 8*lq .. +7].
+  // This wave's rows: R = mt*64 + rg*32 + rb*16 + lr. Query rows are the B
+  // operand of S^T = K Q^T: lane holds Q[row][db*32 + 8*lq .. +7].
+  const int r0 = mt * kPBM + rg * 32;
+  int qi[RB], gq[RB], lim[RB];
   f16x8 qf[RB][4];
-  int lim[RB];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    const int R = row_base + rb * 16 + lr;
+    const int R = r0 + rb * 16 + lr;
     const bool ok = R < total_rows;
-    const int qi = ok ? R / G : 0, g = ok ? R - (R / G) * G : 0;
-    lim[rb] = ok ? P0 + qi : -1;
-    const int64_t qrow = ((int64_t)(b * n_new + qi) * n_heads + hkv * G + g) * kHeadDim;
+    qi[rb] = ok ? R / G : 0;
+    gq[rb] = ok ? R - qi[rb] * G : 0;
+    lim[rb] = ok ? P0 + qi[rb] : -1;  // last key this row attends
+    const int64_t qrow = ((int64_t)(b * n_new + qi[rb]) * n_heads + hkv * G + gq[rb]) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       if (ok) {
@@ -106,28 +132,38 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(
       }
     }
   }
+  // Keys at or below every row limit of this wave need no mask.
+  const bool wave_has_pad = r0 + 31 >= total_rows;
+  const int wave_min_lim = P0 + r0 / G;
 
   const int64_t slab = (int64_t)(b * n_kv + hkv) * cap * kHeadDim;
   const f16* kb_ptr = k_cache + slab;
   const f16* vb_ptr = v_cache + slab;
 
-  // Staging registers. K: 16 threads per key row, 4 instructions cover the
-  // 64 keys. V: lane = key, wave w takes dim runs 4w..4w+3 (written
-  // transposed into LDS, one 64-key row segment per store).
+  // Staging: thread t loads run (t&15) of keys (t>>4) + 32*i, i < 4, of K
+  // and of V — 16 lanes cover one 256-byte row — and stores them row-major.
   f16x8 kr[4], vr[4];
+  const int k_run = tid & 15, k_row = tid >> 4;
   auto load_tile = [&](int kt) {
     const int k0 = kt * kPBN;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int key = min(k0 + i * 16 + (tid >> 4), kend - 1);
-      kr[i] = *reinterpret_cast<const f16x8*>(kb_ptr + (int64_t)key * kHeadDim + (tid & 15) * 8);
+      const int64_t off = (int64_t)min(k0 + k_row + 32 * i, kend - 1) * kHeadDim + k_run * 8;
+      kr[i] = *reinterpret_cast<const f16x8*>(kb_ptr + off);
+      vr[i] = *reinterpret_cast<const f16x8*>(vb_ptr + off);
     }
-    const int vkey = min(k0 + lane, kend - 1);
+  };
+  auto store_tile = [&](int buf) {
+    f16* ks = Ks + buf * kKsHalves;
+    f16* vs = Vs + buf * kVsHalves;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      vr[i] = *reinterpret_cast<const f16x8*>(vb_ptr + (int64_t)vkey * kHeadDim + (wave * 4 + i) * 8);
+    for (int i = 0; i < 4; ++i) {
+      *reinterpret_cast<f16x8*>(&ks[(k_row + 32 * i) * kKsStride + k_run * 8]) = kr[i];
+      *reinterpret_cast<f16x8*>(&vs[(k_row + 32 * i) * kVsStride + k_run * 8]) = vr[i];
+    }
   };
 
+  // Running max of the raw scores (log2 units after scaling) and sums.
   float m[RB], lsum[RB];
   f32x4 o[RB][8];
 #pragma unroll
@@ -137,158 +173,188 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const float c = qk_scale_log2;
 
-  if (ntiles > 0) load_tile(0);
+  // Prologue: tile 0 into LDS, tile 1 in flight. Loads and stores in the
+  // loop are unconditional (indices clamped to the last tile) so the compiler
+  // can wait for exactly the older loads instead of all of them.
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  load_tile(min(1, ntiles - 1));
+
   for (int kt = 0; kt < ntiles; ++kt) {
-    __syncthreads();  // the previous tile's LDS reads are done
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      *reinterpret_cast<f16x8*>(&Ks[(i * 16 + (tid >> 4)) * kKsStride + (tid & 15) * 8]) = kr[i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) Vt[((wave * 4 + i) * 8 + e) * kVtStride + lane] = vr[i][e];
-    __syncthreads();
-    if (kt + 1 < ntiles) load_tile(kt + 1);
+    const int buf = kt & 1;
+    const f16* ks = Ks + buf * kKsHalves + kq * 32 * kKsStride;
+    // transpose-load addresses: lane 4e+c of a 16-lane group reads dims
+    // 4c..4c+3 (of each 16-dim block) of key row 4*lq + e (+16 for the
+    // second half of the operand)
+    const f16* vs = Vs + buf * kVsHalves + (kq * 32 + 4 * lq + (lr >> 2)) * kVsStride + 4 * (lr & 3);
+    const int k0 = kt * kPBN + kq * 32;
 
-    // S^T tile: st[kb][rb][e] = score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr)
-    f32x4 st[4][RB];
+    // st[kb][rb][e] = raw score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr)
+    f32x4 st[2][RB];
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) st[kb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&Ks[(kb * 16 + lr) * kKsStride + db * 32 + 8 * lq]);
+      for (int kb = 0; kb < 2; ++kb) {
+        const f16x8 a = *reinterpret_cast<const f16x8*>(&ks[(kb * 16 + lr) * kKsStride + db * 32 + 8 * lq]);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) st[kb][rb] = mfma16x16x32(a, qf[rb][db], st[kb][rb]);
       }
     }
 
-    const int k0 = kt * kPBN;
-    f16x8 pb[RB][2];
+    if (wave_has_pad || k0 + 31 > wave_min_lim) {  // this tile crosses a row limit
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (k0 + kb * 16 + 4 * lq + e > lim[rb]) st[kb][rb][e] = -INFINITY;
+    }
+
+    f16x8 pb[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      float mx = kNegBig;
-#pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int key = k0 + kb * 16 + 4 * lq + e;
-          const float s = key <= lim[rb] ? st[kb][rb][e] * qk_scale_log2 : -INFINITY;
-          st[kb][rb][e] = s;
-          mx = fmaxf(mx, s);
-        }
+      float mx = fmaxf(fmaxf(fmaxf(st[0][rb][0], st[0][rb][1]), fmaxf(st[0][rb][2], st[0][rb][3])),
+                       fmaxf(fmaxf(st[1][rb][0], st[1][rb][1]), fmaxf(st[1][rb][2], st[1][rb][3])));
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m[rb], mx);
-      const float alpha = fast_exp2(m[rb] - mnew);
-      m[rb] = mnew;
-      lsum[rb] *= alpha;
+      if (mx > m[rb]) {  // rescale only when the running max moves
+        const float alpha = fast_exp2((m[rb] - mx) * c);
+        lsum[rb] *= alpha;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
-      float ps = 0.f;
+        for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
+        m[rb] = mx;
+      }
+      const float mc = m[rb] * c;
+      // P^T operand (32 keys): element e < 4 is key k0 + 4*lq + e, element
+      // e >= 4 is key k0 + 16 + 4*lq + (e-4); V^T is read in the same order.
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = fast_exp2(st[kb][rb][e] - mnew);
-          st[kb][rb][e] = p;
-          ps += p;
-        }
-      lsum[rb] += ps;
-      // P^T operand for k-block h (32 keys): element e < 4 is key
-      // h*32 + 4*lq + e, element e >= 4 is key h*32 + 16 + 4*lq + (e-4).
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          pb[rb][h][e] = (f16)st[2 * h][rb][e];
-          pb[rb][h][4 + e] = (f16)st[2 * h + 1][rb][e];
+          const float p = fast_exp2(fmaf(st[kb][rb][e], c, -mc));
+          lsum[rb] += p;
+          pb[rb][kb * 4 + e] = (f16)p;
         }
     }
 
-    // O^T[d][row] += V^T[d][keys] P^T[keys][row], keys in the same order.
 #pragma unroll
     for (int dblk = 0; dblk < 8; ++dblk) {
-      const f16* vrow = &Vt[(dblk * 16 + lr) * kVtStride + 4 * lq];
+      const f16x4 lo = lds_read_tr16(vs + dblk * 16);
+      const f16x4 hi = lds_read_tr16(vs + 16 * kVsStride + dblk * 16);
+      const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(vrow + h * 32);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(vrow + h * 32 + 16);
-        const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) o[rb][dblk] = mfma16x16x32(a, pb[rb][h], o[rb][dblk]);
-      }
+      for (int rb = 0; rb < RB; ++rb) o[rb][dblk] = mfma16x16x32(a, pb[rb], o[rb][dblk]);
     }
+
+    store_tile(buf ^ 1);  // tile kt+1; its last readers passed the previous barrier
+    __syncthreads();
+    load_tile(min(kt + 2, ntiles - 1));
   }
 
-  // o[rb][dblk][e] = O^T[d = dblk*16 + 4*lq + e][row rb*16 + lr]
+  // Row totals of this key quarter, then merge the quarters through LDS:
+  // quarters 1..3 publish (m, l, o); quarter 0 combines and writes O.
+  constexpr int kX = 2 + 32;  // floats per (rb) state: m, l, o[8][4]
+  float* xch = reinterpret_cast<float*>(smem);  // [3 quarters][2 row groups][64 lanes][RB][kX]
+  auto slot = [&](int qq, int rb) { return xch + ((((qq - 1) * 2 + rg) * 64 + lane) * RB + rb) * kX; };
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    float lt = lsum[rb];
-    lt += __shfl_xor(lt, 16);
-    lt += __shfl_xor(lt, 32);
-    const int R = row_base + rb * 16 + lr;
+    lsum[rb] += __shfl_xor(lsum[rb], 16);
+    lsum[rb] += __shfl_xor(lsum[rb], 32);
+  }
+  if (kq > 0) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float* x = slot(kq, rb);
+      x[0] = m[rb];
+      x[1] = lsum[rb];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[2 + j * 4 + e] = o[rb][j][e];
+    }
+  }
+  __syncthreads();
+  if (kq > 0) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int R = r0 + rb * 16 + lr;
     if (R >= total_rows) continue;
+    float M = m[rb];
+#pragma unroll
+    for (int qq = 1; qq < 4; ++qq) M = fmaxf(M, slot(qq, rb)[0]);
+    const float a0 = fast_exp2((m[rb] - M) * c);
+    float lt = lsum[rb] * a0;
+    float w[3];
+#pragma unroll
+    for (int qq = 1; qq < 4; ++qq) {
+      w[qq - 1] = fast_exp2((slot(qq, rb)[0] - M) * c);
+      lt = fmaf(slot(qq, rb)[1], w[qq - 1], lt);
+    }
     const float inv = 1.f / lt;
-    const int qi = R / G, g = R - (R / G) * G;
-    const int64_t orow = ((int64_t)(b * n_new + qi) * n_heads + hkv * G + g) * kHeadDim;
+    // o[rb][dblk][e] = O^T[d = dblk*16 + 4*lq + e][row R]
+    const int64_t orow = ((int64_t)(b * n_new + qi[rb]) * n_heads + hkv * G + gq[rb]) * kHeadDim;
 #pragma unroll
     for (int dblk = 0; dblk < 8; ++dblk) {
+      f32x4 r = o[rb][dblk] * a0;
+#pragma unroll
+      for (int qq = 1; qq < 4; ++qq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = fmaf(slot(qq, rb)[2 + dblk * 4 + e], w[qq - 1], r[e]);
+      r *= inv;
       const int64_t at = orow + dblk * 16 + 4 * lq;
       if constexpr (kO16) {
-        f16x4 r;
+        f16x4 h;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (f16)(o[rb][dblk][e] * inv);
-        *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = r;
+        for (int e = 0; e < 4; ++e) h[e] = (f16)r[e];
+        *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = h;
       } else {
-        f32x4 r = o[rb][dblk] * inv;
         *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = r;
       }
     }
   }
 }
 
-template <int G, int RB>
-static void launch_prefill_rb(const Shape& s, const void* q, const void* kc, const void* vc,
-                              const int32_t* pos0, void* out, int batch, int n_new,
-                              const Workspace& ws, hipStream_t stream) {
-  constexpr int kBM = kPWaves * 16 * RB;
-  const int mtiles = (n_new * G + kBM - 1) / kBM;
-  const unsigned blocks = (unsigned)(mtiles * s.n_kv * batch);
-  const float sl = s.qk_scale * kLog2e;
-  const f16* k = static_cast<const f16*>(kc);
-  const f16* v = static_cast<const f16*>(vc);
-  if (s.q16) {
-    if (s.o16)
-      prefill_kernel<G, RB, true, true><<<blocks, kPThreads, 0, stream>>>(
-          q, k, v, pos0, out, s.n_heads, s.n_kv, s.cap, n_new, mtiles, sl, ws.status);
-    else
-      prefill_kernel<G, RB, true, false><<<blocks, kPThreads, 0, stream>>>(
-          q, k, v, pos0, out, s.n_heads, s.n_kv, s.cap, n_new, mtiles, sl, ws.status);
-  } else {
-    if (s.o16)
-      prefill_kernel<G, RB, false, true><<<blocks, kPThreads, 0, stream>>>(
-          q, k, v, pos0, out, s.n_heads, s.n_kv, s.cap, n_new, mtiles, sl, ws.status);
-    else
-      prefill_kernel<G, RB, false, false><<<blocks, kPThreads, 0, stream>>>(
-          q, k, v, pos0, out, s.n_heads, s.n_kv, s.cap, n_new, mtiles, sl, ws.status);
+constexpr size_t kPrefillLds = (size_t)(2 * kKsHalves + 2 * kVsHalves) * sizeof(f16);
+static_assert(kPrefillLds >= (size_t)3 * 2 * 64 * 2 * 34 * sizeof(float), "merge exchange fits");
+static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
+
+template <int G, bool kQ16, bool kO16>
+static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc, const void* vc,
+                                   const int32_t* pos0, void* out, int batch, int n_new,
+                                   const Workspace& ws, hipStream_t stream) {
+  auto kern = prefill_kernel<G, kQ16, kO16>;
+  static bool attr_set = false;  // the dynamic LDS size exceeds the 64 KB default
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds);
+    if (e != hipSuccess) return e;
+    attr_set = true;
   }
+  const int mtiles = (n_new * G + kPBM - 1) / kPBM;
+  const unsigned blocks = (unsigned)(mtiles * s.n_kv * batch);
+  kern<<<blocks, kPThreads, kPrefillLds, stream>>>(
+      q, static_cast<const f16*>(kc), static_cast<const f16*>(vc), pos0, out, s.n_heads, s.n_kv,
+      s.cap, n_new, mtiles, s.qk_scale * kLog2e, ws.status);
+  return hipGetLastError();
 }
 
 template <int G>
-static void launch_prefill_g(const Shape& s, const void* q, const void* kc, const void* vc,
-                             const int32_t* pos0, void* out, int batch, int n_new,
-                             const Workspace& ws, hipStream_t stream) {
-  // Two row blocks per wavefront when that still gives a workgroup per CU.
-  const int big_tiles = (n_new * G + 127) / 128;
-  if ((int64_t)big_tiles * s.n_kv * batch >= 256)
-    launch_prefill_rb<G, 2>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
-  else
-    launch_prefill_rb<G, 1>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
+static hipError_t launch_prefill_g(const Shape& s, const void* q, const void* kc, const void* vc,
+                                   const int32_t* pos0, void* out, int batch, int n_new,
+                                   const Workspace& ws, hipStream_t stream) {
+  if (s.q16)
+    return s.o16 ? launch_prefill_t<G, true, true>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream)
+                 : launch_prefill_t<G, true, false>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
+  return s.o16 ? launch_prefill_t<G, false, true>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream)
+               : launch_prefill_t<G, false, false>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
 }
 
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
@@ -297,14 +363,13 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           hipStream_t stream) {
   (void)max_len;
   switch (s.group) {
-    case 1: launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream); break;
-    case 2: launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream); break;
-    case 4: launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream); break;
-    case 5: launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream); break;
-    case 8: launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream); break;
+    case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
+    case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
+    case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
+    case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
+    case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 }  // namespace nwd
