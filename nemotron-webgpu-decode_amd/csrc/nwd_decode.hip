@@ -414,26 +414,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
     }
   }
 
-  // Merge the row states of this wavefront (rows differ in the lane bits
-  // above log2(kLanes)).
+  // Merge the 4 row states of this wavefront (rows of 16 lanes: lane ^ 16
+  // and lane ^ 32 hold the same dims of the other rows).
+  static_assert(kLanes == 16, "row merge assumes 16-lane rows");
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    float M = m[g];
-#pragma unroll
-    for (int sh = kLanes; sh < 64; sh <<= 1) M = fmaxf(M, __shfl_xor(M, sh));
+    const float M = max_xor32(max_xor16(m[g]));
     const float sc = fast_exp2(m[g] - M);
-    float lg = l[g] * sc;
+    l[g] = sum_xor32(sum_xor16(l[g] * sc));
 #pragma unroll
-    for (int sh = kLanes; sh < 64; sh <<= 1) lg += __shfl_xor(lg, sh);
-#pragma unroll
-    for (int i = 0; i < kDims; ++i) {
-      float v = acc[g][i] * sc;
-#pragma unroll
-      for (int sh = kLanes; sh < 64; sh <<= 1) v += __shfl_xor(v, sh);
-      acc[g][i] = v;
-    }
+    for (int i = 0; i < kDims; ++i) acc[g][i] = sum_xor32(sum_xor16(acc[g][i] * sc));
     m[g] = M;
-    l[g] = lg;
   }
   if (row == 0) {
 #pragma unroll

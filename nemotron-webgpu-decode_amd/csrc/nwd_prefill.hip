@@ -223,8 +223,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
     for (int rb = 0; rb < RB; ++rb) {
       float mx = fmaxf(fmaxf(fmaxf(st[0][rb][0], st[0][rb][1]), fmaxf(st[0][rb][2], st[0][rb][3])),
                        fmaxf(fmaxf(st[1][rb][0], st[1][rb][1]), fmaxf(st[1][rb][2], st[1][rb][3])));
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      mx = max_xor32(max_xor16(mx));
       if (mx > m[rb]) {  // rescale only when the running max moves
         const float alpha = fast_exp2((m[rb] - mx) * c);
         lsum[rb] *= alpha;
@@ -266,8 +265,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   auto slot = [&](int qq, int rb) { return xch + ((((qq - 1) * 2 + rg) * 64 + lane) * RB + rb) * kX; };
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
-    lsum[rb] += __shfl_xor(lsum[rb], 16);
-    lsum[rb] += __shfl_xor(lsum[rb], 32);
+    lsum[rb] = sum_xor32(sum_xor16(lsum[rb]));
   }
   if (kq > 0) {
 #pragma unroll
