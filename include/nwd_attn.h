@@ -171,12 +171,12 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len);
  * it beyond fp32 reordering. */
 int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 
-/* Chooses where split-K records are merged: 1 (default) in a separate merge
- * kernel launched after the split kernel (the two-dispatch shape of
- * argmax_partial / argmax_merge, engine/runtime.js:398-399); 0 inside the
- * split kernel, by the last workgroup of each (sequence, kv head) to finish,
- * for callers that want one launch per call. Same results, bit for bit; on
- * MI355X the separate kernel is faster. */
+/* Chooses where split-K records are merged: 1 in a separate merge kernel
+ * launched after the split kernel (the two-dispatch shape of argmax_partial /
+ * argmax_merge, engine/runtime.js:398-399); 0 inside the split kernel, by the
+ * last workgroup of each (sequence, kv head) to finish; negative (the
+ * default) picks by length — in-kernel from 512 keys per split, where it
+ * measured faster on MI355X. Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
 #ifdef __cplusplus

@@ -23,7 +23,7 @@ struct nwd_ctx {
   nwd::Workspace ws;
   int device;
   int forced_splits;
-  int separate_merge;
+  int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 by length
   std::string err;
 };
 
@@ -31,12 +31,14 @@ namespace {
 
 thread_local std::string g_create_err;
 
-// Workgroups one decode launch aims for: one 512-thread workgroup per CU
+// Workgroups one decode launch aims for: one 256-thread workgroup per CU
 // (measured on MI355X: 32 splits of a 4K or 32K context beat 16 and 64).
 constexpr int kTargetWorkgroups = 256;
 constexpr int kMinKeysPerSplit = 128;    // one workgroup iteration
 constexpr int kMaxKeysPerSplit = 2048;   // bounds the slowest workgroup
 constexpr int kMaxSplits = 256;
+// Keys per split from which the merge runs inside the split kernel by default.
+constexpr int kFusedMergeKeys = 512;
 
 int fail(nwd_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(nwd_ctx* ctx, int code, const char* fmt, ...) {
@@ -116,7 +118,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   nwd_ctx* ctx = new nwd_ctx();
   ctx->desc = *d;
   ctx->forced_splits = 0;
-  ctx->separate_merge = 1;
+  ctx->separate_merge = -1;
   ctx->shape.n_heads = d->n_heads;
   ctx->shape.n_kv = d->n_kv_heads;
   ctx->shape.group = group;
@@ -244,7 +246,10 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   c.batch = batch;
   c.nsplit = nwd_decode_splits(ctx, batch, len);
   c.span = len;
-  c.fused_merge = ctx->separate_merge ? 0 : 1;
+  if (ctx->separate_merge < 0)  // measured on MI355X: in-kernel wins from ~512 keys per split
+    c.fused_merge = (int64_t)len >= (int64_t)kFusedMergeKeys * c.nsplit ? 1 : 0;
+  else
+    c.fused_merge = ctx->separate_merge ? 0 : 1;
   hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, who, e);
   return NWD_OK;
@@ -268,7 +273,7 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new, const void
 
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel) {
   if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_merge: ctx is NULL");
-  ctx->separate_merge = separate_kernel ? 1 : 0;
+  ctx->separate_merge = separate_kernel < 0 ? -1 : (separate_kernel ? 1 : 0);
   return NWD_OK;
 }
 

@@ -6,9 +6,9 @@
 // thread streaming one whole key row (uncoalesced), and it caps the context
 // at 256 keys (:29).
 //
-// Here one 512-thread workgroup (8 wavefronts) owns (sequence b, KV head
+// Here one 256-thread workgroup (4 wavefronts) owns (sequence b, KV head
 // hkv, split s): it loads each K/V row of its key range once and serves all G
-// query heads of the group from it. Two workgroups fit on a CU.
+// query heads of the group from it.
 //
 // Mapping inside a wavefront: 4 rows of 16 lanes; a row owns one key at a
 // time and each lane holds 8 of its 128 dims (one 16-byte run), so one load
@@ -30,11 +30,10 @@
 // (value, index) pairs. Optionally (nwd_set_decode_merge) the merge runs in
 // the split kernel itself: records are written with device-scope atomic
 // stores and the workgroup that takes the last arrival ticket of its
-// (b, hkv) merges them. That saves the second launch but costs three
-// serialised memory round trips at the end of every workgroup; on MI355X it
-// measured slower than the second kernel (15.2 vs 11.7 us for a 4K step), so
-// it is not the default. A release fence per workgroup instead of the
-// atomic stores would cost a full L2 write-back each (~0.15 us, serialised).
+// (b, hkv) invalidates its L2 and merges them. That saves the second launch
+// but adds serialised memory round trips at the end of every workgroup. A
+// release fence per workgroup instead of the write-through stores would cost
+// a full L2 write-back each (~0.15 us, serialised on MI355X).
 //
 // The key range is partitioned from the host's length bound (max_len), not
 // from the device position, so a workgroup's first K/V loads do not wait for
@@ -52,7 +51,7 @@ namespace nwd {
 
 // Build-time tuning constants (the defaults are the measured best on MI355X).
 #ifndef NWD_DECODE_WAVES
-#define NWD_DECODE_WAVES 8
+#define NWD_DECODE_WAVES 4
 #endif
 #ifndef NWD_DECODE_KEYS_PER_ROW
 #define NWD_DECODE_KEYS_PER_ROW 2
@@ -99,32 +98,14 @@ __device__ inline f16x8 load_src_run(const void* src, int64_t elem, bool src16) 
 __device__ inline void st_dev(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ inline float ld_dev(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // s_waitcnt vmcnt(0): every earlier global access of this thread is complete.
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <bool kDev>
-__device__ inline float2 ld_ml(const float2* p) {
-  if constexpr (kDev) {
-    const float* f = reinterpret_cast<const float*>(p);
-    return make_float2(ld_dev(f), ld_dev(f + 1));
-  } else {
-    return *p;
-  }
-}
-template <bool kDev>
-__device__ inline f32x4 ld_o4(const float* p) {
-  if constexpr (kDev) return f32x4{ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
-  else return *reinterpret_cast<const f32x4*>(p);
-}
 
 // Merges the nsplit records of the G heads of one (b, hkv) and writes the
 // normalised outputs. Thread t handles 4 dims (d4) of head g for the splits
-// s = r, r + R, ...; the R partial states are combined in LDS. kDev reads
-// the records with device-scope loads (merge inside the split kernel).
-template <int G, bool kO16, bool kDev>
+// s = r, r + R, ...; the R partial states are combined in LDS.
+template <int G, bool kO16>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
                                    int64_t hrow0, int nsplit, float* lds) {
@@ -143,8 +124,8 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int s = min(s0 + u * R, nsplit - 1);  // in range; extras get zero weight
-        ml[u] = ld_ml<kDev>(part_ml + rec0 + s);
-        ov[u] = ld_o4<kDev>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
+        ml[u] = part_ml[rec0 + s];
+        ov[u] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
       }
       float Mn = M;
 #pragma unroll
@@ -491,7 +472,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
   if (!lds_last) return;
-  merge_group<G, kO16, true>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
+  // Acquire at device scope: invalidates this XCD's L2 (no write-back), so
+  // the plain loads of the merge see the records other XCDs wrote through.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  merge_group<G, kO16>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
   if (tid == 0)
     __hip_atomic_store(&a.counters[b * a.n_kv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -503,7 +487,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
     void* __restrict__ out, int n_heads, int nsplit) {
   __shared__ __attribute__((aligned(16))) float lds[kThreads * 6];
   const int hkv = blockIdx.x, b = blockIdx.y;
-  merge_group<G, kO16, false>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
+  merge_group<G, kO16>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
 }
 
 template <int G, bool kQ16, bool kO16>

@@ -179,10 +179,11 @@ class AttnContext:
     def set_decode_splits(self, n: int):
         self._check(self.lib.nwd_set_decode_splits(self.handle, n))
 
-    def set_decode_merge(self, separate_kernel: bool):
-        """True (default): merge split-K records in a second kernel; False: in
-        the split kernel's last workgroup."""
-        self._check(self.lib.nwd_set_decode_merge(self.handle, int(bool(separate_kernel))))
+    def set_decode_merge(self, separate_kernel):
+        """True: merge split-K records in a second kernel; False: in the split
+        kernel's last workgroup; None (default): chosen by length."""
+        v = -1 if separate_kernel is None else int(bool(separate_kernel))
+        self._check(self.lib.nwd_set_decode_merge(self.handle, v))
 
     # ------------------------------------------------------------ operations
     def kv_append(self, k_new, v_new, k_cache, v_cache, pos, batch: int, n_tokens: int = 1,
