@@ -67,7 +67,8 @@ typedef struct nwd_desc {
   int32_t n_kv_heads;  /* Hkv; H must be a multiple of Hkv and the group
                           H/Hkv one of 1, 2, 4, 5, 8 (sparse_attn.wgsl:38)  */
   int32_t head_dim;    /* D; 128 (engine/config.js:12)                      */
-  int32_t max_seq;     /* cache capacity in tokens per sequence             */
+  int32_t max_seq;     /* cache capacity in tokens per sequence, at most
+                          4194304 (2^22)                                    */
   int32_t max_batch;   /* sequences per call                                */
   int32_t q_dtype;     /* NWD_F16 or NWD_F32                                */
   int32_t o_dtype;     /* NWD_F16 or NWD_F32                                */
@@ -174,9 +175,9 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 /* Chooses where split-K records are merged: 1 in a separate merge kernel
  * launched after the split kernel (the two-dispatch shape of argmax_partial /
  * argmax_merge, engine/runtime.js:398-399); 0 inside the split kernel, by the
- * last workgroup of each (sequence, kv head) to finish; negative (the
- * default) picks by length — in-kernel from 512 keys per split, where it
- * measured faster on MI355X. Same results, bit for bit. */
+ * last workgroup of each (sequence, kv head) to finish; negative restores the
+ * default, the separate kernel (measured faster on MI355X at 4K and 32K
+ * keys). Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
 #ifdef __cplusplus

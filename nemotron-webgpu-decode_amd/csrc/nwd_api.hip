@@ -23,7 +23,7 @@ struct nwd_ctx {
   nwd::Workspace ws;
   int device;
   int forced_splits;
-  int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 by length
+  int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 default (separate)
   std::string err;
 };
 
@@ -37,8 +37,6 @@ constexpr int kTargetWorkgroups = 256;
 constexpr int kMinKeysPerSplit = 128;    // one workgroup iteration
 constexpr int kMaxKeysPerSplit = 2048;   // bounds the slowest workgroup
 constexpr int kMaxSplits = 256;
-// Keys per split from which the merge runs inside the split kernel by default.
-constexpr int kFusedMergeKeys = 512;
 
 int fail(nwd_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
 int fail(nwd_ctx* ctx, int code, const char* fmt, ...) {
@@ -108,6 +106,9 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
       return fail(nullptr, NWD_ERR_INVALID, "nwd_create: dtype %d is neither NWD_F16 nor NWD_F32", t);
   if (!(d->scale >= 0.f) || std::isinf(d->scale))
     return fail(nullptr, NWD_ERR_INVALID, "nwd_create: scale must be finite and >= 0");
+  if (d->max_seq > nwd::kMaxSeq)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "nwd_create: max_seq %d exceeds %d tokens",
+                d->max_seq, nwd::kMaxSeq);
   // Largest element index of a cache and of the query/output buffers must
   // fit the kernels' 64-bit index math; keep the per-slab token index in int.
   if ((int64_t)d->max_batch * d->n_kv_heads * (int64_t)d->max_seq > ((int64_t)1 << 40))
@@ -246,10 +247,10 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   c.batch = batch;
   c.nsplit = nwd_decode_splits(ctx, batch, len);
   c.span = len;
-  if (ctx->separate_merge < 0)  // measured on MI355X: in-kernel wins from ~512 keys per split
-    c.fused_merge = (int64_t)len >= (int64_t)kFusedMergeKeys * c.nsplit ? 1 : 0;
-  else
-    c.fused_merge = ctx->separate_merge ? 0 : 1;
+  // Default: the separate merge kernel, measured faster on MI355X at 4K and
+  // 32K keys (its one launch costs less than the in-kernel merge's serialised
+  // store, ticket and record round trips).
+  c.fused_merge = ctx->separate_merge == 0 ? 1 : 0;
   hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, who, e);
   return NWD_OK;

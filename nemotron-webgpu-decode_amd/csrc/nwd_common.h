@@ -14,6 +14,10 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kHeadDim = 128;            // D, the only head size built
+// Largest cache capacity in tokens: a (sequence, kv head) slab is then at most
+// 1 GiB, so 32-bit byte offsets into it, including those of the few tiles
+// requested past a range's end, stay below 2^31.
+constexpr int kMaxSeq = 1 << 22;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -3.4028234663852886e38f;  // finite "minus infinity"
 

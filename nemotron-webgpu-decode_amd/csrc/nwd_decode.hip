@@ -18,8 +18,10 @@
 // online softmax (running max and sum in log2 units, exp2 on the hardware)
 // and accumulates p * V for its dims in fp32 with no cross-lane traffic. The
 // next iteration's K/V loads are issued before the current one is computed,
-// unconditionally (clamped in range), so the wait before the compute only
-// waits for the older loads. At the end the row states are merged
+// unconditionally, so the wait before the compute only waits for the older
+// loads; they go through buffer descriptors that end at the split's last key,
+// so the prefetch past the end reads zeros without a memory round trip. At
+// the end the row states are merged
 // (shuffles inside a wave, LDS across waves) into one record (m, l, o[128])
 // per query head.
 //
@@ -60,6 +62,9 @@ namespace nwd {
 constexpr int kWaves = NWD_DECODE_WAVES;
 constexpr int kThreads = kWaves * 64;
 
+// Buffer descriptor word 3 for gfx9-family raw (stride 0) buffers.
+constexpr int kBufferWord3 = 0x00020000;
+
 template <int G> struct DecodeCfg {
   static constexpr int kLanes = 16;               // lanes per key row
   static constexpr int kRows = 64 / kLanes;       // key rows per wavefront
@@ -81,16 +86,35 @@ __device__ inline float sum_lanes(float x) {
   return x;
 }
 
-// One 16-byte run (8 values) of a new K/V row, fp16 or fp32 (rounded to
-// nearest even, as kv_append does).
-__device__ inline f16x8 load_src_run(const void* src, int64_t elem, bool src16) {
-  if (src16) return *reinterpret_cast<const f16x8*>(static_cast<const f16*>(src) + elem);
-  const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + elem);
-  f32x4 a = p[0], c = p[1];
-  f16x8 r;
-  r[0] = (f16)a[0]; r[1] = (f16)a[1]; r[2] = (f16)a[2]; r[3] = (f16)a[3];
-  r[4] = (f16)c[0]; r[5] = (f16)c[1]; r[6] = (f16)c[2]; r[7] = (f16)c[3];
+// One 16-byte run (8 values) of a new K/V row, fp16 or fp32, loaded as raw
+// words (fp16: the first 16 bytes) and converted later, so that the load
+// can be issued early and nothing waits for it until the values are used.
+struct SrcRun {
+  f32x4 w[2];
+};
+__device__ inline SrcRun load_src_run_raw(const void* src, int64_t elem, bool src16) {
+  SrcRun r;
+  if (src16) {
+    r.w[0] = *reinterpret_cast<const f32x4*>(static_cast<const f16*>(src) + elem);
+    r.w[1] = f32x4{0.f, 0.f, 0.f, 0.f};  // unused; no copy of w[0], which would wait for it
+  } else {
+    const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(src) + elem);
+    r.w[0] = p[0];
+    r.w[1] = p[1];
+  }
   return r;
+}
+// fp16 runs are bit copies; fp32 runs are rounded to nearest even, as
+// kv_append does.
+__device__ inline f16x8 convert_src_run(const SrcRun& r, bool src16) {
+  if (src16) return __builtin_bit_cast(f16x8, r.w[0]);
+  f16x8 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = (f16)r.w[0][e];
+    h[4 + e] = (f16)r.w[1][e];
+  }
+  return h;
 }
 
 // Device-scope relaxed atomic accesses: coherent across the XCDs' L2 caches
@@ -102,71 +126,135 @@ __device__ inline void st_dev(float* p, float v) {
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 
+// Max / sum over each aligned group of 32 lanes (4 DPP steps inside 16
+// lanes, then the lane ^ 16 exchange); every lane of the group gets it.
+__device__ inline float max32(float x) {
+  x = max8(x);
+  x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
+  return max_xor16(x);
+}
+__device__ inline float sum32(float x) {
+  x = sum8(x);
+  x += dpp_mov<kDppRowMirror>(x);
+  return sum_xor16(x);
+}
+
+// Splits the merge reads per pass: all loads of a pass are issued together,
+// one memory round trip (one pass for the usual 32 splits or fewer).
+constexpr int kMergeChunk = 32;
+
+// LDS floats merge_group uses: the per-wave partial outputs [4][G][32] x 4,
+// one (m, l) pair per thread and the pass's head max / sum [G] each.
+template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) + 2 * kThreads; }
+
 // Merges the nsplit records of the G heads of one (b, hkv) and writes the
-// normalised outputs. Thread t handles 4 dims (d4) of head g for the splits
-// s = r, r + R, ...; the R partial states are combined in LDS.
+// normalised outputs. Thread t owns the 4-dim run d4 = t % 32 of every head,
+// for the splits s = j, j + 8, ... of a pass (j = t / 32). Per pass:
+//   1. every (m, l) pair and every o run of the pass is requested at once;
+//   2. the (m, l) pairs go to LDS, and two heads per wavefront reduce their
+//      32 entries to the pass max Mp and sum Lp = sum l * 2^(m - Mp);
+//   3. each thread rescales its running sum to max(M, Mp) and adds its runs
+//      weighted by 2^(m - M). The running max M of a head is the same in
+//      every thread, so the 8 thread groups' sums add without rescaling
+//      (xor-32 lane exchange, then LDS across the 4 wavefronts).
 template <int G, bool kO16>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
                                    int64_t hrow0, int nsplit, float* lds) {
-  constexpr int P = G * 32;          // (head, 4-dim run) pairs
-  constexpr int R = kThreads / P;    // threads per pair
+  static_assert(kThreads == 256, "merge_group maps 8 groups of 32 threads");
+  static_assert(G * kMergeChunk <= kThreads, "one (m, l) pair per thread per pass");
+  constexpr int kPer = kMergeChunk / 8;  // splits per thread per head per pass
   const int t = threadIdx.x;
-  const int p = t % P, r = t / P;
-  const int g = p / 32, d4 = p % 32;
-  const int64_t rec0 = (hrow0 + g) * nsplit;
-  float M = kNegBig, Lsum = 0.f;
-  f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  if (r < R) {
-    for (int s0 = r; s0 < nsplit; s0 += 8 * R) {
-      float2 ml[8];
-      f32x4 ov[8];
+  const int lane = t & 63, wave = t >> 6;
+  const int d4 = t & 31, j = t >> 5;
+  f32x4* lds_acc = reinterpret_cast<f32x4*>(lds);               // [4][G][32]
+  float2* lds_ml = reinterpret_cast<float2*>(lds + G * 512);     // [kThreads]: [G][kMergeChunk], unused
+  float* lds_mp = lds + G * 512 + 2 * kThreads;                 // [G]
+  float* lds_lp = lds_mp + G;                                   // [G]
+  const int64_t rec0 = hrow0 * nsplit;  // record (g, s) is rec0 + g * nsplit + s
+
+  float M[G], Lr[G];
+  f32x4 acc[G];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int s = min(s0 + u * R, nsplit - 1);  // in range; extras get zero weight
-        ml[u] = part_ml[rec0 + s];
-        ov[u] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + s) * kHeadDim + d4 * 4);
+  for (int g = 0; g < G; ++g) {
+    M[g] = kNegBig;
+    Lr[g] = 0.f;
+    acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s0 = 0; s0 < nsplit; s0 += kMergeChunk) {
+    const int ns = min(kMergeChunk, nsplit - s0);
+    // 1. Loads (indexes clamped in range; entries past the pass get no weight).
+    const int mg = t / kMergeChunk, ms = t % kMergeChunk;
+    const bool mvalid = mg < G && ms < ns;
+    const float2 mlv = part_ml[rec0 + min(mg, G - 1) * nsplit + s0 + min(ms, ns - 1)];
+    __builtin_amdgcn_sched_barrier(0);  // the (m, l) load is waited for first: issue it first
+    f32x4 ov[G][kPer];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int s = s0 + min(j + 8 * k, ns - 1);
+        ov[g][k] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + g * nsplit + s) * kHeadDim + d4 * 4);
       }
-      float Mn = M;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) Mn = fmaxf(Mn, ml[u].x);
-      const float a = fast_exp2(M - Mn);
-      Lsum *= a;
-      o *= a;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = s0 + u * R < nsplit ? fast_exp2(ml[u].x - Mn) : 0.f;
-        Lsum = fmaf(ml[u].y, w, Lsum);
-        o += ov[u] * w;
+    // 2. Pass max and sum per head.
+    lds_ml[t] = mvalid ? mlv : make_float2(kNegBig, 0.f);
+    __syncthreads();
+    {
+      const int g = 2 * wave + (lane >> 5);
+      if (g < G) {
+        const float2 e = lds_ml[g * kMergeChunk + (lane & 31)];
+        const float mp = max32(e.x);
+        const float lp = sum32(e.y * fast_exp2(e.x - mp));
+        if ((lane & 31) == 0) {
+          lds_mp[g] = mp;
+          lds_lp[g] = lp;
+        }
       }
-      M = Mn;
     }
-    float* e = lds + (r * P + p) * 6;
-    e[0] = M; e[1] = Lsum; e[2] = o[0]; e[3] = o[1]; e[4] = o[2]; e[5] = o[3];
+    __syncthreads();
+    // 3. Weighted sums of this thread's runs.
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float mp = lds_mp[g];
+      const float mn = fmaxf(M[g], mp);
+      const float a = fast_exp2(M[g] - mn);
+      Lr[g] = Lr[g] * a + lds_lp[g] * fast_exp2(mp - mn);
+      acc[g] *= a;
+#pragma unroll
+      for (int k = 0; k < kPer; ++k) {
+        const int sr = j + 8 * k;
+        const float w = sr < ns ? fast_exp2(lds_ml[g * kMergeChunk + sr].x - mn) : 0.f;
+        acc[g] += ov[g][k] * w;
+      }
+      M[g] = mn;
+    }
+    if (s0 + kMergeChunk < nsplit) __syncthreads();  // lds_ml is rewritten by the next pass
+  }
+  // Sum the 8 thread groups: j and j ^ 1 share a wavefront (lane ^ 32).
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[g][i] = sum_xor32(acc[g][i]);
+    if (lane < 32) lds_acc[(wave * G + g) * 32 + d4] = acc[g];
   }
   __syncthreads();
-  if (r == 0) {
-    float Mx = kNegBig;
+  if (t < G * 32) {
+    const int g = t / 32;
+    f32x4 o = lds_acc[g * 32 + d4];
 #pragma unroll
-    for (int k = 0; k < R; ++k) Mx = fmaxf(Mx, lds[(k * P + p) * 6]);
-    float lt = 0.f;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 1; w < 4; ++w) o += lds_acc[(w * G + g) * 32 + d4];
+    float lt = Lr[0];
 #pragma unroll
-    for (int k = 0; k < R; ++k) {
-      const float* e = lds + (k * P + p) * 6;
-      const float w = fast_exp2(e[0] - Mx);
-      lt = fmaf(e[1], w, lt);
-      acc += f32x4{e[2], e[3], e[4], e[5]} * w;
-    }
+    for (int gg = 1; gg < G; ++gg) lt = gg == g ? Lr[gg] : lt;
     const float inv = 1.f / lt;
     const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
     if constexpr (kO16) {
       f16x4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (f16)(acc[i] * inv);
+      for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
       *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = v;
     } else {
-      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = acc * inv;
+      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = o * inv;
     }
   }
 }
@@ -196,7 +284,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys;
   constexpr int kWaveKeys = kRows * kKpr;
-  constexpr int kMergeFloats = kThreads * 6;
+  constexpr int kMergeFloats = merge_lds_floats<G>();
   constexpr int kWaveFloats = kWaves * G * (kHeadDim + 2);
   constexpr int kLdsFloats = kMergeFloats > kWaveFloats ? kMergeFloats : kWaveFloats;
 
@@ -219,31 +307,57 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   const int t1h = min(a.span, u1 * kUnitKeys);
 
   const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
-  const f16* kbase = a.k_cache + slab + col * 8;
-  const f16* vbase = a.v_cache + slab + col * 8;
+  // K/V are read through buffer descriptors over the slab that end at the
+  // last key a load may need: a load at or past the end fails the hardware
+  // range check and returns zeros without a memory access. So the prefetch
+  // past the last tile (unconditional, to keep the compiler's wait counts
+  // exact) costs no memory round trip for the waits that follow the loop.
+  auto slab_rsrc = [&](f16* cache, int end_key) {
+    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kHeadDim * 2),
+                                             kBufferWord3);
+  };
 
   struct Tile {
     f16x8 k[kKpr][kRuns], v[kKpr][kRuns];
   };
 
-  // Loads clamp to the capacity, never to the position: keys past L are
-  // loaded (in range) and masked, so no load address waits for pos.
-  auto load_tile = [&](Tile& tl, int it) {
+  // Loads never wait for the position: keys past L are loaded (or read as
+  // zeros past the descriptor's end) and masked.
+  auto load_tile = [&](Tile& tl, const __amdgpu_buffer_rsrc_t rk,
+                       const __amdgpu_buffer_rsrc_t rv, int it) {
     const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
 #pragma unroll
     for (int j = 0; j < kKpr; ++j) {
-      const int t = min(base + j * kRows, a.cap - 1);
-      const int64_t off = (int64_t)t * kHeadDim;
+      const uint32_t off = (uint32_t)(base + j * kRows) * (kHeadDim * 2) + col * 16;
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
-        tl.k[j][i] = *reinterpret_cast<const f16x8*>(kbase + off + i * kLanes * 8);
-        tl.v[j][i] = *reinterpret_cast<const f16x8*>(vbase + off + i * kLanes * 8);
+        tl.k[j][i] = __builtin_bit_cast(
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + i * kLanes * 16, 0, 0));
+        tl.v[j][i] = __builtin_bit_cast(
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off + i * kLanes * 16, 0, 0));
       }
     }
   };
 
+  // Fused append: every workgroup requests the new rows (this lane's runs,
+  // raw) before its first tile, and before the position says which split
+  // owns them, so that converting them later never waits for a tile.
+  const bool has_new = a.k_new != nullptr;
+  SrcRun nk_raw, nv_raw;
+  if (has_new) {
+    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim + col * 8;
+    nk_raw = load_src_run_raw(a.k_new, src, a.new16);
+    nv_raw = load_src_run_raw(a.v_new, src, a.new16);
+  }
+
+  // The first tile is requested before the position is known, over the keys
+  // this split can own: up to the host bound, or up to the capacity for the
+  // last split (which absorbs keys past the bound).
   Tile ta, tb;
-  load_tile(ta, 0);  // requested before the position is known
+  {
+    const int own_end = split == nsplit - 1 ? a.cap : t1h;
+    load_tile(ta, slab_rsrc(a.k_cache, own_end), slab_rsrc(a.v_cache, own_end), 0);
+  }
 
   // Query registers: this lane's dims of each of the G heads.
   const int h0 = hkv * G;
@@ -277,26 +391,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // past the host bound.
   const int t1 = split == nsplit - 1 ? L : min(t1h, L);
   const int n_it = t1 > t0 ? (t1 - t0 + kBlockKeys - 1) / kBlockKeys : 0;
+  const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
 
-  // Fused append: the split holding the new position writes the new rows
-  // and substitutes them for the cache rows it loads.
+  // Fused append: the split holding the new position substitutes the new
+  // rows for the cache rows it loads, and writes them to the caches at the
+  // end of the kernel.
   const int pnew = L - 1;
-  const bool owns_new = a.k_new != nullptr && pos_ok && t0 <= pnew && pnew < t1;
+  const bool owns_new = has_new && pos_ok && t0 <= pnew && pnew < t1;
+  static_assert(kRuns == 1, "one 16-byte run per lane");
   f16x8 nk[kRuns], nv[kRuns];
   if (owns_new) {
-    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
-#pragma unroll
-    for (int i = 0; i < kRuns; ++i) {
-      nk[i] = load_src_run(a.k_new, src + (col + i * kLanes) * 8, a.new16);
-      nv[i] = load_src_run(a.v_new, src + (col + i * kLanes) * 8, a.new16);
-    }
-    if (tid < 32) {
-      const int run = tid & 15;
-      const void* s = tid < 16 ? a.k_new : a.v_new;
-      f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab +
-                 (int64_t)pnew * kHeadDim + run * 8;
-      *reinterpret_cast<f16x8*>(dst) = load_src_run(s, src + run * 8, a.new16);
-    }
+    nk[0] = convert_src_run(nk_raw, a.new16);
+    nv[0] = convert_src_run(nv_raw, a.new16);
   }
 
   auto qk = [&](const Tile& tl, int j, int g) -> float {
@@ -388,9 +494,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // position arrives.
   if (n_it > 0) {
     for (int it = 0; it < n_it; it += 2) {
-      load_tile(tb, min(it + 1, n_it - 1));
+      load_tile(tb, rk, rv, it + 1);
       compute_tile(ta, it);
-      load_tile(ta, min(it + 2, n_it - 1));
+      load_tile(ta, rk, rv, it + 2);
       if (it + 1 < n_it) compute_tile(tb, it + 1);
     }
   }
@@ -455,6 +561,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
       }
     }
   }
+  // The new rows go to the caches last: lanes 0-15 hold the 16 runs of the
+  // new K row in nk, lanes 16-31 those of the new V row in nv.
+  if (owns_new && tid < 32) {
+    f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim + col * 8;
+    *reinterpret_cast<f16x8*>(dst) = tid < 16 ? nk[0] : nv[0];
+  }
   if (nsplit == 1 || !a.fused_merge) return;
 
   // The workgroup that takes the last arrival ticket of this (b, hkv)
@@ -480,12 +592,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
     __hip_atomic_store(&a.counters[b * a.n_kv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Separate merge: one 512-thread workgroup per (kv head, sequence).
+// Separate merge: one 256-thread workgroup per (kv head, sequence).
 template <int G, bool kO16>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float2* __restrict__ part_ml,
     void* __restrict__ out, int n_heads, int nsplit) {
-  __shared__ __attribute__((aligned(16))) float lds[kThreads * 6];
+  __shared__ __attribute__((aligned(16))) float lds[merge_lds_floats<G>()];
   const int hkv = blockIdx.x, b = blockIdx.y;
   merge_group<G, kO16>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
 }

@@ -181,7 +181,7 @@ class AttnContext:
 
     def set_decode_merge(self, separate_kernel):
         """True: merge split-K records in a second kernel; False: in the split
-        kernel's last workgroup; None (default): chosen by length."""
+        kernel's last workgroup; None: the default (the separate kernel)."""
         v = -1 if separate_kernel is None else int(bool(separate_kernel))
         self._check(self.lib.nwd_set_decode_merge(self.handle, v))
 

@@ -43,6 +43,7 @@ def _desc(**kw):
     (dict(n_heads=96), nw.NWD_ERR_UNSUPPORTED),      # group 12
     (dict(head_dim=64), nw.NWD_ERR_UNSUPPORTED),
     (dict(max_seq=0), nw.NWD_ERR_INVALID),
+    (dict(max_seq=(1 << 22) + 1), nw.NWD_ERR_UNSUPPORTED),  # slab byte offsets need 31 bits
     (dict(max_batch=0), nw.NWD_ERR_INVALID),
     (dict(q_dtype=7), nw.NWD_ERR_INVALID),
     (dict(scale=-1.0), nw.NWD_ERR_INVALID),
