@@ -180,6 +180,57 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * keys). Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
+/* ---------------------------------------------------------------------
+ * 4-bit projections around the path: the producer of q / k / v and the
+ * consumer of the attention output.
+ * ------------------------------------------------------------------- */
+
+/* One 4-bit projection [K -> n] in the reference's MatMulNBits format
+ * (engine/weights.js:99-104, engine/weight-index.json; read by
+ * kernels/matmul_nbits_sg.wgsl:15-18). Weight (c, k) of block blk = k / 32
+ * is (nib - zp) * scale with nib the low nibble of byte (k % 32) / 2 of
+ * quant[c][blk] for even k (high nibble for odd), scale = scales[c][blk] and
+ * zp nibble c * n_blocks + blk of the packed zero points (low nibble first,
+ * matmul_nbits_sg.wgsl:24-27). */
+typedef struct nwd_q4_weight {
+  const void* quant;     /* uint8 [n][n_blocks][16], 16-byte aligned         */
+  const float* scales;   /* float [n][n_blocks]                              */
+  const void* zp;        /* uint8 [(n * n_blocks + 1) / 2]                   */
+  int32_t n;             /* output columns N                                 */
+  int32_t n_blocks;      /* K / 32, 1..256                                   */
+} nwd_q4_weight;
+
+enum {
+  NWD_Q4_PLAIN = 0,      /* y = W . a                                        */
+  NWD_Q4_RELU2 = 1,      /* y = max(W . a, 0)^2 (matmul_nbits_sg.wgsl epilogue
+                            1, :76-79,125-127)                               */
+  NWD_Q4_ACCUMULATE = 2  /* y = y + W . a: a projection followed by the
+                            residual add of kernels/add.wgsl:15-18, as o_proj
+                            and L-add run at engine/runtime.js:392-393     */
+};
+
+/* matmul_nbits_sg.wgsl main (:81-137) for `batch` activation rows:
+ * y[b][n] = epilogue(W . a[b]). a is [batch][32 * n_blocks] f32 (16-byte
+ * aligned), y [batch][n] f32. Dispatched as ceil(N / 4) workgroups by the
+ * reference (engine/runtime.js:359-361); here the library picks the grid. */
+int nwd_q4_gemv(nwd_ctx* ctx, const float* a, const nwd_q4_weight* w, float* y,
+                int32_t batch, int32_t epilogue, void* stream);
+
+/* The attention layer's q / k / v projections and kv_append in one launch:
+ * the dispatches L-q, L-k, L-v, L-kvK and L-kvV of engine/runtime.js:386-390
+ * (matmul_nbits_sg.wgsl three times, then kv_append.wgsl:12-18 for k and
+ * v). x is [batch][K] f32 (the normalised hidden state, 16-byte aligned); wq
+ * has n_heads * head_dim columns, wk and wv n_kv_heads * head_dim, all with
+ * the same K. q_out gets [batch][n_heads][head_dim] in desc.q_dtype (the q
+ * input of nwd_decode_attn); the new k and v rows are rounded to fp16 (to
+ * nearest even, as nwd_kv_append does) into the caches at pos[b]. A position
+ * outside [0, max_seq) writes no cache row and sets the device status
+ * (nwd_device_status). batch <= max_batch. */
+int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq,
+                   const nwd_q4_weight* wk, const nwd_q4_weight* wv, void* q_out,
+                   void* k_cache, void* v_cache, const int32_t* pos, int32_t batch,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

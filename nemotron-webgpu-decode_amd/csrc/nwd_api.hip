@@ -319,4 +319,73 @@ int nwd_device_status(nwd_ctx* ctx, void* stream) {
               ctx->desc.max_seq);
 }
 
+// Checks one 4-bit projection descriptor; `cols` > 0 also fixes its width.
+static int check_q4(nwd_ctx* ctx, const char* who, const char* name, const nwd_q4_weight* w,
+                    int cols) {
+  if (!w) return fail(ctx, NWD_ERR_INVALID, "%s: %s is NULL", who, name);
+  if (!w->quant || !w->scales || !w->zp)
+    return fail(ctx, NWD_ERR_INVALID, "%s: %s has a null buffer", who, name);
+  if (reinterpret_cast<uintptr_t>(w->quant) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(w->scales) % 4 != 0)
+    return fail(ctx, NWD_ERR_INVALID, "%s: %s quant must be 16-byte and scales 4-byte aligned",
+                who, name);
+  if (w->n < 1 || (cols > 0 && w->n != cols))
+    return fail(ctx, NWD_ERR_INVALID, "%s: %s has %d columns, expected %d", who, name, w->n,
+                cols > 0 ? cols : 1);
+  if (w->n_blocks < 1 || w->n_blocks > nwd::kQ4MaxBlocks)
+    return fail(ctx, NWD_ERR_UNSUPPORTED, "%s: %s n_blocks %d outside [1, %d] (K <= %d)", who,
+                name, w->n_blocks, nwd::kQ4MaxBlocks, 32 * nwd::kQ4MaxBlocks);
+  return NWD_OK;
+}
+
+static nwd::Q4Mat q4_mat(const nwd_q4_weight* w) {
+  return nwd::Q4Mat{static_cast<const uint8_t*>(w->quant), w->scales,
+                    static_cast<const uint8_t*>(w->zp), w->n};
+}
+
+int nwd_q4_gemv(nwd_ctx* ctx, const float* a, const nwd_q4_weight* w, float* y, int32_t batch,
+                int32_t epilogue, void* stream) {
+  const char* who = "nwd_q4_gemv";
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "%s: ctx is NULL", who);
+  if (int rc = check_q4(ctx, who, "w", w, 0)) return rc;
+  if (!a || !y) return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (reinterpret_cast<uintptr_t>(a) % 16 != 0 || reinterpret_cast<uintptr_t>(y) % 4 != 0)
+    return fail(ctx, NWD_ERR_INVALID, "%s: a must be 16-byte and y 4-byte aligned", who);
+  if (batch < 1 || batch > 65535)
+    return fail(ctx, NWD_ERR_INVALID, "%s: batch %d outside [1, 65535]", who, batch);
+  if (epilogue != NWD_Q4_PLAIN && epilogue != NWD_Q4_RELU2 && epilogue != NWD_Q4_ACCUMULATE)
+    return fail(ctx, NWD_ERR_INVALID, "%s: unknown epilogue %d", who, epilogue);
+  hipError_t e = nwd::launch_q4_gemv(a, q4_mat(w), w->n_blocks, y, batch, epilogue,
+                                     (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_q4_gemv: launch", e);
+  return NWD_OK;
+}
+
+int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq, const nwd_q4_weight* wk,
+                   const nwd_q4_weight* wv, void* q_out, void* k_cache, void* v_cache,
+                   const int32_t* pos, int32_t batch, void* stream) {
+  const char* who = "nwd_qkv_append";
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "%s: ctx is NULL", who);
+  const int dq = ctx->desc.n_heads * ctx->desc.head_dim;
+  const int dkv = ctx->desc.n_kv_heads * ctx->desc.head_dim;
+  if (int rc = check_q4(ctx, who, "wq", wq, dq)) return rc;
+  if (int rc = check_q4(ctx, who, "wk", wk, dkv)) return rc;
+  if (int rc = check_q4(ctx, who, "wv", wv, dkv)) return rc;
+  if (wk->n_blocks != wq->n_blocks || wv->n_blocks != wq->n_blocks)
+    return fail(ctx, NWD_ERR_INVALID, "%s: wq, wk and wv must share K (n_blocks %d, %d, %d)", who,
+                wq->n_blocks, wk->n_blocks, wv->n_blocks);
+  if (!x || !q_out || !k_cache || !v_cache || !pos)
+    return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q_out) % 16 != 0)
+    return fail(ctx, NWD_ERR_INVALID, "%s: x and q_out must be 16-byte aligned", who);
+  if (batch < 1 || batch > ctx->desc.max_batch)
+    return fail(ctx, NWD_ERR_CAPACITY, "%s: batch %d outside [1, max_batch=%d]", who, batch,
+                ctx->desc.max_batch);
+  hipError_t e = nwd::launch_qkv_append(ctx->shape, x, q4_mat(wq), q4_mat(wk), q4_mat(wv),
+                                        wq->n_blocks, q_out, k_cache, v_cache, pos, batch,
+                                        ctx->ws.status, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_qkv_append: launch", e);
+  return NWD_OK;
+}
+
 }  // extern "C"

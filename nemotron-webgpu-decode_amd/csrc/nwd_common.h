@@ -79,6 +79,21 @@ __device__ inline float sum_xor32(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Max / sum over each aligned group of 32 lanes (4 DPP steps inside 16
+// lanes, then the lane ^ 16 exchange), and sum over the whole wavefront;
+// every lane of the group gets the result.
+__device__ inline float max32(float x) {
+  x = max8(x);
+  x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
+  return max_xor16(x);
+}
+__device__ inline float sum32(float x) {
+  x = sum8(x);
+  x += dpp_mov<kDppRowMirror>(x);
+  return sum_xor16(x);
+}
+__device__ inline float sum64(float x) { return sum_xor32(sum32(x)); }
+
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ inline float dot2(f16x2 a, f16x2 b, float c) {

@@ -126,19 +126,6 @@ __device__ inline void st_dev(float* p, float v) {
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 
-// Max / sum over each aligned group of 32 lanes (4 DPP steps inside 16
-// lanes, then the lane ^ 16 exchange); every lane of the group gets it.
-__device__ inline float max32(float x) {
-  x = max8(x);
-  x = fmaxf(x, dpp_mov<kDppRowMirror>(x));
-  return max_xor16(x);
-}
-__device__ inline float sum32(float x) {
-  x = sum8(x);
-  x += dpp_mov<kDppRowMirror>(x);
-  return sum_xor16(x);
-}
-
 // Splits the merge reads per pass: all loads of a pass are issued together,
 // one memory round trip (one pass for the usual 32 splits or fewer).
 constexpr int kMergeChunk = 32;

@@ -60,4 +60,30 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
 // Largest decode split count supported for `batch` sequences by `ws`.
 int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
+// One 4-bit projection [K -> n] in the reference's format (K = 32 * n_blocks).
+struct Q4Mat {
+  const uint8_t* quant;   // [n][n_blocks][16]
+  const float* scales;    // [n][n_blocks]
+  const uint8_t* zp;      // 4-bit zero points, flat index col * n_blocks + blk
+  int n;
+};
+
+// Largest K = 32 * n_blocks the 4-bit kernels accept (activation blocks are
+// held in registers, four per lane).
+constexpr int kQ4MaxBlocks = 256;
+
+enum Q4Epilogue { kQ4None = 0, kQ4Relu2 = 1, kQ4Accumulate = 2 };
+
+// y[b][n] = epilogue(dequant(W) . x[b]) for b < batch; x [batch][K] f32.
+hipError_t launch_q4_gemv(const float* x, const Q4Mat& w, int n_blocks, float* y, int batch,
+                          int epilogue, hipStream_t stream);
+
+// The attention layer's q/k/v projections of x [batch][K] with the new K/V
+// rows rounded to fp16 straight into the caches at pos[b] (q to q_out,
+// [batch][H][128] in the context's q dtype).
+hipError_t launch_qkv_append(const Shape& s, const float* x, const Q4Mat& wq, const Q4Mat& wk,
+                             const Q4Mat& wv, int n_blocks, void* q_out, void* k_cache,
+                             void* v_cache, const int32_t* pos, int batch, int* status,
+                             hipStream_t stream);
+
 }  // namespace nwd

@@ -46,6 +46,28 @@ class NwdDesc(ctypes.Structure):
     ]
 
 
+NWD_Q4_PLAIN = 0
+NWD_Q4_RELU2 = 1
+NWD_Q4_ACCUMULATE = 2
+
+
+class NwdQ4Weight(ctypes.Structure):
+    """nwd_q4_weight: one 4-bit projection [K -> n] in the reference's
+    MatMulNBits format (engine/weights.js:99-104)."""
+    _fields_ = [
+        ("quant", ctypes.c_void_p),
+        ("scales", ctypes.c_void_p),
+        ("zp", ctypes.c_void_p),
+        ("n", ctypes.c_int32),
+        ("n_blocks", ctypes.c_int32),
+    ]
+
+
+def q4_weight(quant, scales, zp, n: int, n_blocks: int) -> NwdQ4Weight:
+    """Descriptor of device buffers (addresses or tensors)."""
+    return NwdQ4Weight(_ptr(quant), _ptr(scales), _ptr(zp), n, n_blocks)
+
+
 class NwdError(RuntimeError):
     """A non-zero status from the C ABI, with the library's message."""
 
@@ -91,6 +113,10 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_decode_splits": (i32, [vp, i32, i32]),
         "nwd_set_decode_splits": (ctypes.c_int, [vp, i32]),
         "nwd_set_decode_merge": (ctypes.c_int, [vp, i32]),
+        "nwd_q4_gemv": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight), vp, i32, i32, vp]),
+        "nwd_qkv_append": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight),
+                                          ctypes.POINTER(NwdQ4Weight), ctypes.POINTER(NwdQ4Weight),
+                                          vp, vp, vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -212,6 +238,22 @@ class AttnContext:
         self._check(self.lib.nwd_prefill_attn(self.handle, _ptr(q), _ptr(k_cache), _ptr(v_cache),
                                               _ptr(pos0), _ptr(out), batch, n_new, max_len,
                                               _stream(stream)))
+
+    def q4_gemv(self, a, w: NwdQ4Weight, y, batch: int = 1, epilogue: int = NWD_Q4_PLAIN,
+                stream=None):
+        """kernels/matmul_nbits_sg.wgsl:81-137 for `batch` rows; epilogue
+        NWD_Q4_RELU2 (its epilogue 1) or NWD_Q4_ACCUMULATE (y += W.a, the
+        residual add of kernels/add.wgsl fused)."""
+        self._check(self.lib.nwd_q4_gemv(self.handle, _ptr(a), ctypes.byref(w), _ptr(y), batch,
+                                         epilogue, _stream(stream)))
+
+    def qkv_append(self, x, wq: NwdQ4Weight, wk: NwdQ4Weight, wv: NwdQ4Weight, q_out, k_cache,
+                   v_cache, pos, batch: int = 1, stream=None):
+        """The q/k/v projections and kv_append of engine/runtime.js:386-390 in one launch."""
+        self._check(self.lib.nwd_qkv_append(self.handle, _ptr(x), ctypes.byref(wq),
+                                            ctypes.byref(wk), ctypes.byref(wv), _ptr(q_out),
+                                            _ptr(k_cache), _ptr(v_cache), _ptr(pos), batch,
+                                            _stream(stream)))
 
     def device_status(self, stream=None) -> int:
         """Synchronises and returns the status code (raises nothing)."""

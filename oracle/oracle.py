@@ -4,7 +4,9 @@ The oracle is the checker of the HIP library. Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
 Each wrapped function cites the reference file:line its C code restates (see
 attn_oracle.c). Inputs are numpy arrays in the reference's layouts:
-Q/O [n_heads][head_dim] and K/V token-major [seq][n_kv_heads][head_dim].
+Q/O [n_heads][head_dim] and K/V token-major [seq][n_kv_heads][head_dim];
+4-bit weights as quant uint8 [N][n_blocks][16], scales float32 [N][n_blocks]
+and packed zero points uint8 [ceil(N * n_blocks / 2)] (q4_oracle.c).
 """
 from __future__ import annotations
 
@@ -52,6 +54,11 @@ def _load():
     lib.oracle_attn_f64.restype = ctypes.c_int
     lib.oracle_max_threads.argtypes = []
     lib.oracle_max_threads.restype = ctypes.c_int
+    u8 = P(dtype=np.uint8, flags="C_CONTIGUOUS")
+    lib.oracle_q4_gemv_f32.argtypes = [f32, u8, f32, u8, f32, u32, u32, u32, u32, ctypes.c_int]
+    lib.oracle_q4_gemv_f32.restype = ctypes.c_int
+    lib.oracle_q4_dequant.argtypes = [u8, f32, u8, f32, u32, u32]
+    lib.oracle_q4_dequant.restype = None
     _lib = lib
     return lib
 
@@ -118,3 +125,36 @@ def attn_f64(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float = 0.0) ->
     if rc != 0:
         raise ValueError("oracle_attn_f64: seq == 0 or heads do not divide")
     return o
+
+
+def q4_gemv_f32(a: np.ndarray, quant: np.ndarray, scales: np.ndarray, zp: np.ndarray,
+                epilogue: int = 0, threads: int = 1) -> np.ndarray:
+    """kernels/matmul_nbits_sg.wgsl:81-137 op for op in f32: Y[N] =
+    epilogue(dequant(W) . a). a [K] float32, K = 32 * n_blocks; epilogue 1 =
+    relu2. threads > 1 spreads the workgroups over OpenMP threads (same
+    result)."""
+    a = np.ascontiguousarray(a, np.float32).reshape(-1)
+    quant = np.ascontiguousarray(quant, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zp = np.ascontiguousarray(zp, np.uint8).reshape(-1)
+    N, n_blocks = scales.shape
+    assert quant.shape == (N, n_blocks, 16) and a.size == 32 * n_blocks
+    assert zp.size * 2 >= N * n_blocks
+    y = np.empty(N, np.float32)
+    rc = _load().oracle_q4_gemv_f32(a, quant.reshape(-1), scales.reshape(-1), zp, y, a.size, N,
+                                    n_blocks, epilogue, threads)
+    if rc != 0:
+        raise ValueError("oracle_q4_gemv_f32: K != 32 * n_blocks")
+    return y
+
+
+def q4_dequant(quant: np.ndarray, scales: np.ndarray, zp: np.ndarray) -> np.ndarray:
+    """(nib - zp) * scale of every weight, [N][K] float32, as dequant_dot forms it."""
+    quant = np.ascontiguousarray(quant, np.uint8)
+    scales = np.ascontiguousarray(scales, np.float32)
+    zp = np.ascontiguousarray(zp, np.uint8).reshape(-1)
+    N, n_blocks = scales.shape
+    assert quant.shape == (N, n_blocks, 16) and zp.size * 2 >= N * n_blocks
+    w = np.empty((N, 32 * n_blocks), np.float32)
+    _load().oracle_q4_dequant(quant.reshape(-1), scales.reshape(-1), zp, w, N, n_blocks)
+    return w
