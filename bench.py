@@ -164,6 +164,91 @@ class PrefillWorkload:
         return float(kv_bytes(self.cap))
 
 
+class Q4LayerWorkload:
+    """The attention layer's 4-bit projections at the Nano-4B shapes
+    (engine/config.js:2-26): `qkv-append` runs nwd_qkv_append (K = 3136 to
+    q 5120 + k 1024 + v 1024 columns, k/v rounded into the fp16 caches at
+    pos), `o-proj` runs nwd_q4_gemv with the residual accumulate (K = 5120
+    to 3136). `layers` distinct random weight sets are rotated so the weights
+    (14.4 MB / 8.3 MB per layer) come from HBM, not the 256 MB MALL."""
+
+    HIDDEN, HEADS, KV_HEADS = 3136, 40, 8
+
+    def __init__(self, torch, nw, kind: str, layers: int = 32, seed: int = 6):
+        self.kind, self.layers, self.nw = kind, layers, nw
+        tg = torch.Generator(device="cuda")
+        tg.manual_seed(seed)
+        if kind == "qkv-append":
+            shapes = [(self.HEADS * D, self.HIDDEN // 32), (self.KV_HEADS * D, self.HIDDEN // 32),
+                      (self.KV_HEADS * D, self.HIDDEN // 32)]
+            k_in = self.HIDDEN
+        else:
+            shapes = [(self.HIDDEN, self.HEADS * D // 32)]
+            k_in = self.HEADS * D
+
+        def q4(n, nb):
+            quant = torch.randint(0, 256, (n, nb, 16), generator=tg, device="cuda", dtype=torch.uint8)
+            scales = torch.rand((n, nb), generator=tg, device="cuda") * 0.02 + 0.01
+            zp = torch.randint(0, 256, ((n * nb + 1) // 2,), generator=tg, device="cuda",
+                               dtype=torch.uint8)
+            return (quant, scales, zp), nw.q4_weight(quant, scales, zp, n, nb)
+
+        self.sets = [[q4(n, nb) for n, nb in shapes] for _ in range(layers)]
+        self.weight_bytes = sum(n * nb * 16 + n * nb * 4 + (n * nb + 1) // 2 for n, nb in shapes)
+        self.x = torch.randn((1, k_in), generator=tg, device="cuda")
+        self.io_bytes = k_in * 4
+        self.cap = 64
+        self.ctx = nw.AttnContext(self.HEADS, self.KV_HEADS, self.cap, q_dtype="f32")
+        if kind == "qkv-append":
+            self.q_out = torch.empty((1, self.HEADS, D), device="cuda")
+            self.kc = torch.zeros((1, self.KV_HEADS, self.cap, D), dtype=torch.float16, device="cuda")
+            self.vc = torch.zeros_like(self.kc)
+            self.pos = torch.arange(self.cap, dtype=torch.int32, device="cuda")
+            self.io_bytes += self.HEADS * D * 4 + 2 * self.KV_HEADS * D * 2
+        else:
+            self.h = torch.zeros((1, self.HIDDEN), device="cuda")
+            self.io_bytes += 2 * self.HIDDEN * 4
+
+    def step(self, s: int, stream, append=True):
+        ws = [w for _, w in self.sets[s % self.layers]]
+        if self.kind == "qkv-append":
+            pos = self.pos.data_ptr() + 4 * ((s // self.layers) % self.cap)
+            self.ctx.qkv_append(self.x, ws[0], ws[1], ws[2], self.q_out, self.kc, self.vc, pos, 1,
+                                stream)
+        else:
+            self.ctx.q4_gemv(self.x, ws[0], self.h, 1, self.nw.NWD_Q4_ACCUMULATE, stream)
+
+    def bytes_per_step(self) -> int:
+        return self.weight_bytes + self.io_bytes
+
+
+def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
+    """The oracle's restatement of kernels/matmul_nbits_sg.wgsl on the host's
+    cores for one layer's projections of the same shapes (random weights)."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    g = np.random.Generator(np.random.PCG64(6))
+    hid, heads, kvh = Q4LayerWorkload.HIDDEN, Q4LayerWorkload.HEADS, Q4LayerWorkload.KV_HEADS
+    shapes = ([(heads * D, hid // 32), (kvh * D, hid // 32), (kvh * D, hid // 32)]
+              if kind == "qkv-append" else [(hid, heads * D // 32)])
+    mats = [(g.integers(0, 256, (n, nb, 16), dtype=np.uint8),
+             g.uniform(0.01, 0.03, (n, nb)).astype(np.float32),
+             g.integers(0, 256, (n * nb + 1) // 2, dtype=np.uint8)) for n, nb in shapes]
+    x = g.standard_normal(32 * shapes[0][1]).astype(np.float32)
+    threads = oracle.max_threads()
+    t0, done = time.perf_counter(), 0
+    while done == 0 or time.perf_counter() - t0 < budget_s:
+        for quant, scales, zp in mats:
+            oracle.q4_gemv_f32(x, quant, scales, zp, threads=threads)
+        done += 1
+    dt = time.perf_counter() - t0
+    wbytes = sum(n * nb * 16 + n * nb * 4 + (n * nb + 1) // 2 for n, nb in shapes)
+    return {"us_per_step": round(dt / done * 1e6, 1), "gbs": round(wbytes * done / dt / 1e9, 3),
+            "cores": threads, "kind": "port", "sample": f"{done} calls, one layer's weights"}
+
+
 def time_graph(torch, wl, steps: int, warmup: int, append=True):
     """Warm up eagerly, capture `steps` steps into a HIP graph, replay it once
     untimed and once timed. Returns (wall seconds, device ms) of the timed replay."""
@@ -250,6 +335,10 @@ EXTRA_WORKLOADS = {
                  "append+attend per step",
     "prefill-512": "prefill-512: B=1, 512 new tokens onto 8192 cached, causal in the chunk, "
                    "kv_append of 512 rows + fp16-MFMA prefill per step",
+    "qkv-append": "qkv-append: B=1, Nano-4B q/k/v 4-bit projections K=3136 -> 5120+1024+1024 "
+                  "with k/v rounded into the fp16 caches, 32 weight sets rotated (461 MB)",
+    "o-proj": "o-proj: B=1, Nano-4B o_proj 4-bit K=5120 -> 3136 with the residual add, "
+              "32 weight sets rotated (266 MB)",
 }
 
 WORKLOADS = {
@@ -291,8 +380,30 @@ def run_workload(torch, nw, name: str, steps: int, warmup: int):
     return res
 
 
-def run_extra(torch, nw, name: str, steps: int, warmup: int):
-    """The ragged batch and the prefill chunk (measured on request)."""
+def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
+    """One 4-bit projection workload: us per call and weight-stream GB/s."""
+    log(f"[bench] {name}: {steps} steps")
+    wl = Q4LayerWorkload(torch, nw, name)
+    wall, ms = time_graph(torch, wl, steps, warmup)
+    us = ms * 1e3 / steps
+    gbs = wl.bytes_per_step() / (us * 1e-6) / 1e9
+    res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us,
+           "bytes_per_step": wl.bytes_per_step(), "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
+           "wall_s": wall}
+    wl.ctx.close()
+    del wl
+    torch.cuda.empty_cache()
+    if cpu:
+        res["cpu_baseline"] = q4_cpu_baseline(name)
+    log(f"[bench] {name}: {res}")
+    return res
+
+
+def run_extra(torch, nw, name: str, steps: int, warmup: int, cpu: bool = False):
+    """The ragged batch, the prefill chunk and the 4-bit projections (measured
+    on request)."""
+    if name in ("qkv-append", "o-proj"):
+        return run_q4(torch, nw, name, steps, warmup, cpu)
     log(f"[bench] {name}: {steps} steps")
     wl = RaggedWorkload(torch, nw) if name == "ragged-64" else PrefillWorkload(torch, nw)
     wall, ms = time_graph(torch, wl, steps, warmup)
@@ -379,7 +490,8 @@ def main():
     nw.load_library()
 
     if args.workload in EXTRA_WORKLOADS:
-        r = run_extra(torch, nw, args.workload, args.steps, args.warmup)
+        r = run_extra(torch, nw, args.workload, args.steps, args.warmup,
+                      cpu=not args.no_cpu_baseline)
         print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
               flush=True)
         return

@@ -314,6 +314,62 @@ napi_value Prefill(napi_env env, napi_callback_info info) {
                                 n_new, max_len, nullptr));
 }
 
+// {quant, scales, zp: BigInt device addresses, n, nBlocks} -> nwd_q4_weight
+bool get_q4(napi_env env, napi_value obj, nwd_q4_weight* w) {
+  napi_valuetype t;
+  if (napi_typeof(env, obj, &t) != napi_ok || t != napi_object) return false;
+  const char* names[3] = {"quant", "scales", "zp"};
+  void* p[3];
+  for (int i = 0; i < 3; ++i) {
+    napi_value v;
+    bool has = false;
+    if (napi_has_named_property(env, obj, names[i], &has) != napi_ok || !has) return false;
+    napi_get_named_property(env, obj, names[i], &v);
+    if (!get_ptr(env, v, &p[i])) return false;
+  }
+  w->quant = p[0];
+  w->scales = static_cast<const float*>(p[1]);
+  w->zp = p[2];
+  w->n = field(env, obj, "n", 0);
+  w->n_blocks = field(env, obj, "nBlocks", 0);
+  return true;
+}
+
+// q4Gemv(ctx, a, w, y, batch, epilogue): matmul_nbits_sg.wgsl, epilogue
+// 0 plain, 1 relu2, 2 accumulate into y (o_proj + residual add)
+napi_value Q4Gemv(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *x, *y;
+  nwd_q4_weight w;
+  int32_t batch, epi;
+  if (!ctx || !get_ptr(env, a[1], &x) || !get_q4(env, a[2], &w) || !get_ptr(env, a[3], &y) ||
+      !get_i32(env, a[4], &batch, 1) || !get_i32(env, a[5], &epi, 0))
+    return throw_error(env, "q4Gemv: bad arguments");
+  return check(env, ctx, "q4Gemv",
+               nwd_q4_gemv(ctx, static_cast<const float*>(x), &w, static_cast<float*>(y), batch,
+                           epi, nullptr));
+}
+
+// qkvAppend(ctx, x, wq, wk, wv, qOut, kCache, vCache, pos, batch): the q/k/v
+// projections and kv_append in one launch
+napi_value QkvAppend(napi_env env, napi_callback_info info) {
+  napi_value a[10];
+  get_args(env, info, 10, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *x, *q, *kc, *vc, *pos;
+  nwd_q4_weight wq, wk, wv;
+  int32_t batch;
+  if (!ctx || !get_ptr(env, a[1], &x) || !get_q4(env, a[2], &wq) || !get_q4(env, a[3], &wk) ||
+      !get_q4(env, a[4], &wv) || !get_ptr(env, a[5], &q) || !get_ptr(env, a[6], &kc) ||
+      !get_ptr(env, a[7], &vc) || !get_ptr(env, a[8], &pos) || !get_i32(env, a[9], &batch, 1))
+    return throw_error(env, "qkvAppend: bad arguments");
+  return check(env, ctx, "qkvAppend",
+               nwd_qkv_append(ctx, static_cast<const float*>(x), &wq, &wk, &wv, q, kc, vc,
+                              static_cast<const int32_t*>(pos), batch, nullptr));
+}
+
 // deviceStatus(ctx) -> 0, or throws with the position error
 napi_value DeviceStatus(napi_env env, napi_callback_info info) {
   napi_value a[1];
@@ -339,6 +395,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"appendDecode", nullptr, AppendDecode, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"prefill", nullptr, Prefill, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"deviceStatus", nullptr, DeviceStatus, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"q4Gemv", nullptr, Q4Gemv, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"qkvAppend", nullptr, QkvAppend, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
   return exports;

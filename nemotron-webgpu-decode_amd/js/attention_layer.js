@@ -16,6 +16,11 @@
 // that the host writes before each step, as the reference writes its
 // uniforms. q/k/v/attnO stay f32, the reference's activation type, so the
 // q/k/v GEMVs and the o_proj GEMV bind unchanged.
+//
+// With the layer's 4-bit weights registered (setLayerWeights), the whole
+// attention layer from the normalised hidden state runs on the library too:
+// the reference's L-q, L-k, L-v, L-kvK, L-kvV, L-attn, L-o, L-add
+// (runtime.js:386-393) become qkvAppend, decode and q4Gemv(accumulate).
 const path = require('path');
 
 const ADDON = path.join(__dirname, '..', 'lib', 'nwd_napi.node');
@@ -23,7 +28,8 @@ const ADDON = path.join(__dirname, '..', 'lib', 'nwd_napi.node');
 const addon = require(ADDON);
 
 // Nemotron-3-Nano-4B attention shapes (engine/config.js:10-12,24,31).
-const NANO4B = { heads: 40, kvHeads: 8, headDim: 128, maxSeq: 256 };
+const NANO4B = { hidden: 3136, heads: 40, kvHeads: 8, headDim: 128, maxSeq: 256 };
+const Q4_ACCUMULATE = 2;  // nwd_q4_gemv epilogue: y = y + W.a (o_proj + residual add)
 const ATTN_LAYERS = [12, 17, 24, 32];
 
 class AttentionSlice {
@@ -49,8 +55,43 @@ class AttentionSlice {
       this.vCache.set(i, addon.malloc(this.cacheBytes));
     }
     this.pos = addon.malloc(4);
+    this.weights = new Map();  // layer -> {q, k, v, o} nwd_q4_weight descriptors
+    this.owned = [];           // device buffers uploadQ4 allocated
     this.seq = 0;
     this.reset();
+  }
+
+  // A host projection in the reference's MatMulNBits format
+  // (engine/weights.js:99-104: quant Uint8Array [n][nBlocks][16], scales
+  // Float32Array [n][nBlocks], zp Uint8Array of packed 4-bit zero points) on
+  // the device, as the descriptor qkvAppend / q4Gemv take.
+  uploadQ4({ quant, scales, zp, n, nBlocks }) {
+    const put = (arr) => {
+      const p = addon.malloc(arr.byteLength);
+      addon.upload(p, arr);
+      this.owned.push(p);
+      return p;
+    };
+    return { quant: put(quant), scales: put(scales), zp: put(zp), n, nBlocks };
+  }
+
+  // runtime.js:321-324: the q4 projections of attention layer i.
+  setLayerWeights(i, { q, k, v, o }) {
+    if (!this.kCache.has(i)) throw new Error(`layer ${i} is not an attention layer`);
+    this.weights.set(i, { q, k, v, o });
+  }
+
+  // runtime.js:386-393 for attention layer i: hNorm (f32 [hidden], device) ->
+  // q / k / v projections with k / v written into the caches, attention, and
+  // o_proj added into the residual stream h (f32 [hidden], device).
+  encodeLayerFromHidden(i, hNorm, h) {
+    const w = this.weights.get(i);
+    if (!w) throw new Error(`layer ${i} has no weights (setLayerWeights)`);
+    addon.qkvAppend(this.ctx, hNorm, w.q, w.k, w.v, this.q, this.kCache.get(i), this.vCache.get(i),
+                    this.pos, 1);
+    addon.decode(this.ctx, this.q, this.kCache.get(i), this.vCache.get(i), this.pos, this.attnO, 1,
+                 this.seq + 1);
+    addon.q4Gemv(this.ctx, this.attnO, w.o, h, 1, Q4_ACCUMULATE);
   }
 
   // runtime.js:615-633 (the KV part of reset)
@@ -102,7 +143,7 @@ class AttentionSlice {
   }
 
   destroy() {
-    for (const p of [this.q, this.k, this.v, this.attnO, this.pos]) addon.free(p);
+    for (const p of [this.q, this.k, this.v, this.attnO, this.pos, ...this.owned]) addon.free(p);
     for (const i of this.layers) {
       addon.free(this.kCache.get(i));
       addon.free(this.vCache.get(i));

@@ -11,6 +11,7 @@ import pytest
 
 import oracle
 from attn_cases import max_abs
+from q4_cases import gemv_f64
 
 ROOT = Path(__file__).resolve().parent.parent
 JS = ROOT / "nemotron-webgpu-decode_amd" / "js"
@@ -51,3 +52,45 @@ def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq):
     assert worst < 2e-3, worst
     if tokens == max_seq:  # engine/runtime.js:448: the next step must throw
         assert "exceeds maxSeq" in man["guard"]
+
+
+def test_node_host_full_layer_from_hidden_state(tmp_path):
+    """js/check_layer.js: one attention layer per token from the normalised
+    hidden state (q/k/v projections + kv_append, attention, o_proj + residual
+    add, engine/runtime.js:386-393) with 4-bit weights. Checked stage by
+    stage against the oracle: the attention output against the chain q4 GEMV
+    -> fp16 cache -> sparse_attn restatement (2e-3), and the residual against
+    h_in + o_proj(attention output) in float64 (1e-6 of sum |w a|, plus one
+    f32 rounding of the add)."""
+    out = tmp_path / "layer"
+    print("node check_layer hidden=512 tokens=12", flush=True)
+    res = subprocess.run(["node", str(JS / "check_layer.js"), str(out), "512", "12"],
+                         capture_output=True, text=True, timeout=180)
+    assert res.returncode == 0, res.stdout + res.stderr
+    man = json.loads((out / "manifest.json").read_text())
+    H, Hkv, D, hid, T = man["heads"], man["kvHeads"], man["headDim"], man["hidden"], man["tokens"]
+
+    def w(name, n, nb):
+        return (np.fromfile(out / f"w{name}.quant", np.uint8).reshape(n, nb, 16),
+                np.fromfile(out / f"w{name}.scales", np.float32).reshape(n, nb),
+                np.fromfile(out / f"w{name}.zp", np.uint8))
+
+    wq, wk, wv = w("q", H * D, hid // 32), w("k", Hkv * D, hid // 32), w("v", Hkv * D, hid // 32)
+    wo = w("o", hid, H * D // 32)
+    hnorm = np.fromfile(out / "hnorm.f32", np.float32).reshape(T, hid)
+    hin = np.fromfile(out / "hin.f32", np.float32).reshape(T, hid)
+    attn = np.fromfile(out / "attn.f32", np.float32).reshape(T, H, D)
+    hout = np.fromfile(out / "hout.f32", np.float32).reshape(T, hid)
+    k_rows, v_rows, worst = [], [], 0.0
+    for t in range(T):
+        q = oracle.q4_gemv_f32(hnorm[t], *wq).reshape(H, D)
+        for rows, wm in ((k_rows, wk), (v_rows, wv)):
+            rows.append(oracle.f16_to_f32(oracle.f32_to_f16(oracle.q4_gemv_f32(hnorm[t], *wm)))
+                        .reshape(Hkv, D))
+        want = oracle.sparse_attn_f32(q, np.stack(k_rows), np.stack(v_rows))
+        worst = max(worst, max_abs(attn[t], want))
+        o64, bound = gemv_f64(attn[t].reshape(-1), *wo)
+        h64 = hin[t].astype(np.float64) + o64
+        slack = 1e-6 * bound + np.abs(h64) * 2.0 ** -23
+        assert np.all(np.abs(hout[t] - h64) <= slack), t
+    assert worst < 2e-3, worst

@@ -25,7 +25,8 @@ def test_addon_exports():
     out = _node("const a = require('../lib/nwd_napi.node'); console.log(JSON.stringify(Object.keys(a)))")
     names = set(json.loads(out))
     assert {"create", "destroy", "cacheBytes", "malloc", "free", "upload", "download", "zero",
-            "sync", "kvAppend", "decode", "appendDecode", "prefill", "deviceStatus"} <= names
+            "sync", "kvAppend", "decode", "appendDecode", "prefill", "deviceStatus",
+            "q4Gemv", "qkvAppend"} <= names
 
 
 def test_create_errors_are_thrown_with_the_library_message():
@@ -37,6 +38,8 @@ for (const d of [{nHeads: 30, nKvHeads: 8, maxSeq: 16}, {nHeads: 24, nKvHeads: 8
   try { a.create(d); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 }
 try { a.decode(null, 0n, 0n, 0n, 0n, 0n, 1, 0); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
+try { a.q4Gemv(null, 0n, {}, 0n, 1, 0); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
+try { a.qkvAppend(null, 0n, {}, {}, {}, 0n, 0n, 0n, 0n, 1); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 console.log(JSON.stringify(msgs));
 """)
     m = json.loads(out)
@@ -44,6 +47,7 @@ console.log(JSON.stringify(msgs));
     assert "group size" in m[1]
     assert "sizes must be positive" in m[2]
     assert m[3].startswith("decode:")
+    assert m[4].startswith("q4Gemv:") and m[5].startswith("qkvAppend:")
 
 
 def test_js_module_parses():
@@ -51,5 +55,8 @@ def test_js_module_parses():
                          text=True, timeout=60)
     assert res.returncode == 0, res.stderr
     res = subprocess.run(["node", "--check", str(JS / "check_attention.js")], capture_output=True,
+                         text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    res = subprocess.run(["node", "--check", str(JS / "check_layer.js")], capture_output=True,
                          text=True, timeout=60)
     assert res.returncode == 0, res.stderr
