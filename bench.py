@@ -389,7 +389,7 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
     gbs = wl.bytes_per_step() / (us * 1e-6) / 1e9
     res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us,
            "bytes_per_step": wl.bytes_per_step(), "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-           "wall_s": wall}
+           "traffic": measured_traffic(name), "wall_s": wall}
     wl.ctx.close()
     del wl
     torch.cuda.empty_cache()
