@@ -172,15 +172,20 @@ class Q4LayerWorkload:
     to 3136). `layers` distinct random weight sets are rotated so the weights
     (14.4 MB / 8.3 MB per layer) come from HBM, not the 256 MB MALL."""
 
-    HIDDEN, HEADS, KV_HEADS = 3136, 40, 8
+    HIDDEN, HEADS, KV_HEADS, VOCAB = 3136, 40, 8, 131072
 
     def __init__(self, torch, nw, kind: str, layers: int = 32, seed: int = 6):
+        if kind == "lm-head":
+            layers = 2  # 2 x 205 MB of weights already exceed the 256 MB MALL
         self.kind, self.layers, self.nw = kind, layers, nw
         tg = torch.Generator(device="cuda")
         tg.manual_seed(seed)
         if kind == "qkv-append":
             shapes = [(self.HEADS * D, self.HIDDEN // 32), (self.KV_HEADS * D, self.HIDDEN // 32),
                       (self.KV_HEADS * D, self.HIDDEN // 32)]
+            k_in = self.HIDDEN
+        elif kind == "lm-head":
+            shapes = [(self.VOCAB, self.HIDDEN // 32)]
             k_in = self.HIDDEN
         else:
             shapes = [(self.HIDDEN, self.HEADS * D // 32)]
@@ -205,6 +210,9 @@ class Q4LayerWorkload:
             self.vc = torch.zeros_like(self.kc)
             self.pos = torch.arange(self.cap, dtype=torch.int32, device="cuda")
             self.io_bytes += self.HEADS * D * 4 + 2 * self.KV_HEADS * D * 2
+        elif kind == "lm-head":
+            self.token = torch.zeros((1,), dtype=torch.int32, device="cuda")
+            self.io_bytes += 4
         else:
             self.h = torch.zeros((1, self.HIDDEN), device="cuda")
             self.io_bytes += 2 * self.HIDDEN * 4
@@ -215,6 +223,8 @@ class Q4LayerWorkload:
             pos = self.pos.data_ptr() + 4 * ((s // self.layers) % self.cap)
             self.ctx.qkv_append(self.x, ws[0], ws[1], ws[2], self.q_out, self.kc, self.vc, pos, 1,
                                 stream)
+        elif self.kind == "lm-head":
+            self.ctx.lm_head_argmax(self.x, ws[0], self.token, None, 1, stream)
         else:
             self.ctx.q4_gemv(self.x, ws[0], self.h, 1, self.nw.NWD_Q4_ACCUMULATE, stream)
 
@@ -231,8 +241,9 @@ def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
 
     g = np.random.Generator(np.random.PCG64(6))
     hid, heads, kvh = Q4LayerWorkload.HIDDEN, Q4LayerWorkload.HEADS, Q4LayerWorkload.KV_HEADS
-    shapes = ([(heads * D, hid // 32), (kvh * D, hid // 32), (kvh * D, hid // 32)]
-              if kind == "qkv-append" else [(hid, heads * D // 32)])
+    shapes = {"qkv-append": [(heads * D, hid // 32), (kvh * D, hid // 32), (kvh * D, hid // 32)],
+              "o-proj": [(hid, heads * D // 32)],
+              "lm-head": [(Q4LayerWorkload.VOCAB, hid // 32)]}[kind]
     mats = [(g.integers(0, 256, (n, nb, 16), dtype=np.uint8),
              g.uniform(0.01, 0.03, (n, nb)).astype(np.float32),
              g.integers(0, 256, (n * nb + 1) // 2, dtype=np.uint8)) for n, nb in shapes]
@@ -241,7 +252,9 @@ def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
     t0, done = time.perf_counter(), 0
     while done == 0 or time.perf_counter() - t0 < budget_s:
         for quant, scales, zp in mats:
-            oracle.q4_gemv_f32(x, quant, scales, zp, threads=threads)
+            y = oracle.q4_gemv_f32(x, quant, scales, zp, threads=threads)
+            if kind == "lm-head":
+                oracle.argmax_ref(y)
         done += 1
     dt = time.perf_counter() - t0
     wbytes = sum(n * nb * 16 + n * nb * 4 + (n * nb + 1) // 2 for n, nb in shapes)
@@ -339,6 +352,8 @@ EXTRA_WORKLOADS = {
                   "with k/v rounded into the fp16 caches, 32 weight sets rotated (461 MB)",
     "o-proj": "o-proj: B=1, Nano-4B o_proj 4-bit K=5120 -> 3136 with the residual add, "
               "32 weight sets rotated (266 MB)",
+    "lm-head": "lm-head: B=1, Nano-4B lm_head 4-bit K=3136 -> 131072 with the greedy pick "
+               "(argmax partial in the GEMV, then the merge), 2 weight sets rotated (410 MB)",
 }
 
 WORKLOADS = {
@@ -402,7 +417,7 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
 def run_extra(torch, nw, name: str, steps: int, warmup: int, cpu: bool = False):
     """The ragged batch, the prefill chunk and the 4-bit projections (measured
     on request)."""
-    if name in ("qkv-append", "o-proj"):
+    if name in ("qkv-append", "o-proj", "lm-head"):
         return run_q4(torch, nw, name, steps, warmup, cpu)
     log(f"[bench] {name}: {steps} steps")
     wl = RaggedWorkload(torch, nw) if name == "ragged-64" else PrefillWorkload(torch, nw)

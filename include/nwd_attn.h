@@ -231,6 +231,26 @@ int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq,
                    void* k_cache, void* v_cache, const int32_t* pos, int32_t batch,
                    void* stream);
 
+/* The greedy token pick: kernels/argmax_partial.wgsl (:16-52) over 256
+ * slices of ceil(n / 256) logits, then kernels/argmax_merge.wgsl (:8-42),
+ * as dispatched at engine/runtime.js:398-399. out[b] gets the index the
+ * reference returns for row b of x [batch][n] f32, including its tie order
+ * (the smaller step within a thread, then the smaller bit-reversed thread
+ * and slice positions of its two reduction trees), NaN never winning, and
+ * 0 when no value exceeds -3.402823466e38. Uses the context's workspace. */
+int nwd_argmax(nwd_ctx* ctx, const float* x, int32_t n, uint32_t* out, int32_t batch,
+               void* stream);
+
+/* lm_head and the greedy pick: the dispatches lm-head, argmax0 and argmax1
+ * of engine/runtime.js:397-399 (matmul_nbits_sg.wgsl then the two argmax
+ * kernels), with the partial argmax in the GEMV's epilogue. h is
+ * [batch][K] f32 (16-byte aligned, the final-norm output), w the 4-bit
+ * lm_head [K -> vocab]; out[b] gets the token index, with nwd_argmax's
+ * semantics over the logits; logits, if not NULL, gets them [batch][vocab]
+ * f32. */
+int nwd_lm_head_argmax(nwd_ctx* ctx, const float* h, const nwd_q4_weight* w, float* logits,
+                       uint32_t* out, int32_t batch, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -388,4 +388,54 @@ int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq, const 
   return NWD_OK;
 }
 
+// The argmax records live in the split-K workspace (calls on a context are
+// stream-ordered, so they never overlap a decode's use of it).
+static unsigned long long* argmax_records(nwd_ctx* ctx, const char* who, int64_t count, int* rc) {
+  const int64_t have = ctx->ws.records * nwd::kHeadDim * (int64_t)sizeof(float) / 8;
+  if (count > have) {
+    *rc = fail(ctx, NWD_ERR_CAPACITY, "%s: %lld partial records exceed the workspace (%lld)", who,
+               (long long)count, (long long)have);
+    return nullptr;
+  }
+  *rc = NWD_OK;
+  return reinterpret_cast<unsigned long long*>(ctx->ws.part_o);
+}
+
+int nwd_argmax(nwd_ctx* ctx, const float* x, int32_t n, uint32_t* out, int32_t batch,
+               void* stream) {
+  const char* who = "nwd_argmax";
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "%s: ctx is NULL", who);
+  if (!x || !out) return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (n < 1) return fail(ctx, NWD_ERR_INVALID, "%s: n %d < 1", who, n);
+  if (batch < 1 || batch > 65535)
+    return fail(ctx, NWD_ERR_INVALID, "%s: batch %d outside [1, 65535]", who, batch);
+  int rc;
+  unsigned long long* rec =
+      argmax_records(ctx, who, (int64_t)nwd::argmax_records_per_row(n) * batch, &rc);
+  if (!rec) return rc;
+  hipError_t e = nwd::launch_argmax(x, n, out, batch, rec, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_argmax: launch", e);
+  return NWD_OK;
+}
+
+int nwd_lm_head_argmax(nwd_ctx* ctx, const float* h, const nwd_q4_weight* w, float* logits,
+                       uint32_t* out, int32_t batch, void* stream) {
+  const char* who = "nwd_lm_head_argmax";
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "%s: ctx is NULL", who);
+  if (int r = check_q4(ctx, who, "w", w, 0)) return r;
+  if (!h || !out) return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (reinterpret_cast<uintptr_t>(h) % 16 != 0)
+    return fail(ctx, NWD_ERR_INVALID, "%s: h must be 16-byte aligned", who);
+  if (batch < 1 || batch > 65535)
+    return fail(ctx, NWD_ERR_INVALID, "%s: batch %d outside [1, 65535]", who, batch);
+  int rc;
+  unsigned long long* rec =
+      argmax_records(ctx, who, (int64_t)nwd::q4_argmax_records_per_row(w->n) * batch, &rc);
+  if (!rec) return rc;
+  hipError_t e = nwd::launch_q4_argmax(h, q4_mat(w), w->n_blocks, logits, out, batch, rec,
+                                       (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(ctx, "nwd_lm_head_argmax: launch", e);
+  return NWD_OK;
+}
+
 }  // extern "C"

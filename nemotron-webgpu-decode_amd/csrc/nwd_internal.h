@@ -86,4 +86,23 @@ hipError_t launch_qkv_append(const Shape& s, const float* x, const Q4Mat& wq, co
                              void* v_cache, const int32_t* pos, int batch, int* status,
                              hipStream_t stream);
 
+// The greedy pick of kernels/argmax_partial.wgsl + argmax_merge.wgsl over
+// x [batch][n]: one 64-bit record per chunk of logits in `records`, then a
+// merge per row into out[b]. records needs argmax_records_per_row(n) * batch
+// entries.
+int argmax_records_per_row(int n);
+hipError_t launch_argmax(const float* x, int n, uint32_t* out, int batch,
+                         unsigned long long* records, hipStream_t stream);
+hipError_t launch_argmax_merge(const unsigned long long* records, int per_row, int n,
+                               uint32_t* out, int batch, hipStream_t stream);
+
+// lm_head (a 4-bit projection of x [batch][K] to w.n logits) with the
+// argmax partial in its epilogue: one record per 16 logits, then the merge.
+// logits (optional) gets the projection. records needs
+// q4_argmax_records_per_row(w.n) * batch entries.
+int q4_argmax_records_per_row(int n);
+hipError_t launch_q4_argmax(const float* x, const Q4Mat& w, int n_blocks, float* logits,
+                            uint32_t* out, int batch, unsigned long long* records,
+                            hipStream_t stream);
+
 }  // namespace nwd

@@ -32,6 +32,7 @@
 // Weight traffic is the roofline: 16.5 bytes per 32 weights (quant, scale,
 // zero point). The activation (12.5 KB at K = 3136) is read by every
 // wavefront from L2.
+#include "nwd_argmax.h"
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
@@ -162,6 +163,42 @@ __global__ __launch_bounds__(kQ4Threads) void q4_gemv_kernel(const float* __rest
   }
 }
 
+// lm_head with the argmax partial in its epilogue (engine/runtime.js:397-
+// 399: the lm-head GEMV, then argmax_partial): each workgroup's 16 logits
+// become one 64-bit record (nwd_argmax.h) for argmax_merge_kernel. No
+// wavefront returns before the barrier: columns past n are computed on the
+// clamped column n - 1 and not recorded.
+template <int kSlots>
+__global__ __launch_bounds__(kQ4Threads) void q4_argmax_kernel(
+    const float* __restrict__ x, const Q4Mat m, int n_blocks, float* __restrict__ logits,
+    unsigned long long* __restrict__ records) {
+  __shared__ unsigned long long best;
+  if (threadIdx.x == 0) best = 0ull;
+  __syncthreads();
+  const int b = blockIdx.y;
+  const int col0 = blockIdx.x * kQ4WgCols + (threadIdx.x >> 6) * kQ4Cols;
+  Q4Act<kSlots> a;
+  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, n_blocks, a);
+  float r[kQ4Cols];
+  q4_columns<kSlots>(m, n_blocks, col0, a, r);
+  if ((threadIdx.x & 63) == 0) {
+    const ArgmaxShape s = argmax_shape(m.n);
+    unsigned long long e = 0ull;
+#pragma unroll
+    for (int c = 0; c < kQ4Cols; ++c) {
+      const int col = col0 + c;
+      if (col < m.n) {
+        if (logits) logits[(int64_t)b * m.n + col] = r[c];
+        const unsigned long long v = argmax_enc(r[c], col, s);
+        e = v > e ? v : e;
+      }
+    }
+    atomicMax(&best, e);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) records[(int64_t)b * gridDim.x + blockIdx.x] = best;
+}
+
 // Columns [0, Nq) are q, [Nq, Nq + Nkv) k, [Nq + Nkv, Nq + 2 Nkv) v; every
 // range is a multiple of 128 (whole heads), so a workgroup's 16 columns lie
 // in one of them.
@@ -264,6 +301,25 @@ hipError_t launch_q4_gemv(const float* x, const Q4Mat& w, int n_blocks, float* y
     case 4: return launch_gemv_slots<4>(x, w, n_blocks, y, batch, epilogue, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+int q4_argmax_records_per_row(int n) { return (n + kQ4WgCols - 1) / kQ4WgCols; }
+
+hipError_t launch_q4_argmax(const float* x, const Q4Mat& w, int n_blocks, float* logits,
+                            uint32_t* out, int batch, unsigned long long* records,
+                            hipStream_t stream) {
+  const int per_row = q4_argmax_records_per_row(w.n);
+  const dim3 grid(per_row, batch);
+  switch (q4_slots(n_blocks)) {
+    case 1: q4_argmax_kernel<1><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
+    case 2: q4_argmax_kernel<2><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
+    case 3: q4_argmax_kernel<3><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
+    case 4: q4_argmax_kernel<4><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_argmax_merge(records, per_row, w.n, out, batch, stream);
 }
 
 hipError_t launch_qkv_append(const Shape& s, const float* x, const Q4Mat& wq, const Q4Mat& wk,

@@ -117,6 +117,9 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_qkv_append": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight),
                                           ctypes.POINTER(NwdQ4Weight), ctypes.POINTER(NwdQ4Weight),
                                           vp, vp, vp, vp, i32, vp]),
+        "nwd_argmax": (ctypes.c_int, [vp, vp, i32, vp, i32, vp]),
+        "nwd_lm_head_argmax": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight), vp, vp, i32,
+                                              vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -254,6 +257,15 @@ class AttnContext:
                                             ctypes.byref(wk), ctypes.byref(wv), _ptr(q_out),
                                             _ptr(k_cache), _ptr(v_cache), _ptr(pos), batch,
                                             _stream(stream)))
+
+    def argmax(self, x, n: int, out, batch: int = 1, stream=None):
+        """kernels/argmax_partial.wgsl + argmax_merge.wgsl (engine/runtime.js:398-399)."""
+        self._check(self.lib.nwd_argmax(self.handle, _ptr(x), n, _ptr(out), batch, _stream(stream)))
+
+    def lm_head_argmax(self, h, w: NwdQ4Weight, out, logits=None, batch: int = 1, stream=None):
+        """lm-head + argmax0 + argmax1 of engine/runtime.js:397-399 in two launches."""
+        self._check(self.lib.nwd_lm_head_argmax(self.handle, _ptr(h), ctypes.byref(w),
+                                                _ptr(logits), _ptr(out), batch, _stream(stream)))
 
     def device_status(self, stream=None) -> int:
         """Synchronises and returns the status code (raises nothing)."""

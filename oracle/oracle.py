@@ -59,6 +59,8 @@ def _load():
     lib.oracle_q4_gemv_f32.restype = ctypes.c_int
     lib.oracle_q4_dequant.argtypes = [u8, f32, u8, f32, u32, u32]
     lib.oracle_q4_dequant.restype = None
+    lib.oracle_argmax_ref.argtypes = [f32, u32]
+    lib.oracle_argmax_ref.restype = ctypes.c_uint32
     _lib = lib
     return lib
 
@@ -158,3 +160,12 @@ def q4_dequant(quant: np.ndarray, scales: np.ndarray, zp: np.ndarray) -> np.ndar
     w = np.empty((N, 32 * n_blocks), np.float32)
     _load().oracle_q4_dequant(quant.reshape(-1), scales.reshape(-1), zp, w, N, n_blocks)
     return w
+
+
+def argmax_ref(x: np.ndarray) -> int:
+    """kernels/argmax_partial.wgsl:16-52 (256 workgroups over ceil(n / 256)
+    slices) then kernels/argmax_merge.wgsl:8-42, op for op: the token index
+    the reference picks from logits x [n]."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    assert x.size >= 1
+    return int(_load().oracle_argmax_ref(x, x.size))

@@ -62,9 +62,18 @@ def dequant_f32(quant, scales, zp) -> np.ndarray:
     return w.reshape(n, n_blocks * 32)
 
 
-def gemv_f64(a, quant, scales, zp):
+def gemv_f64(a, quant, scales, zp, rows: int = 4096):
     """Y = dequant(W) . a in float64, and the bound sum_k |w_k a_k| that the
-    float32 tolerances are stated against."""
-    w = dequant_f64(quant, scales, zp)
+    float32 tolerances are stated against (computed `rows` columns at a
+    time, so a 131072-column lm_head fits in memory)."""
+    n, n_blocks = scales.shape
     a64 = np.asarray(a, np.float64).reshape(-1)
-    return w @ a64, np.abs(w) @ np.abs(a64)
+    z = zero_points(zp, n, n_blocks)
+    y, bound = np.empty(n), np.empty(n)
+    for r0 in range(0, n, rows):
+        r1 = min(n, r0 + rows)
+        w = ((nibbles(quant[r0:r1]).astype(np.float64) - z[r0:r1, :, None])
+             * scales[r0:r1].astype(np.float64)[..., None]).reshape(r1 - r0, -1)
+        y[r0:r1] = w @ a64
+        bound[r0:r1] = np.abs(w) @ np.abs(a64)
+    return y, bound
