@@ -199,6 +199,144 @@ __global__ __launch_bounds__(kQ4Threads) void q4_argmax_kernel(
   if (threadIdx.x == 0) records[(int64_t)b * gridDim.x + blockIdx.x] = best;
 }
 
+// ---------------------------------------------------------------------------
+// Wide form, for projections with many columns (lm_head: 131072). A 128-thread
+// workgroup owns 16 columns, 8 lanes per column; lane j of a column takes
+// blocks j, j+8, ... (kIters of them). The activation row goes to LDS once per
+// workgroup with its block sums, so a lane's registers hold only its weights
+// (all requested at once) and one block of activation at a time: about 40%
+// fewer VALU instructions per weight than the form above. That form wins when
+// the grid is small (a wavefront there has fewer iterations in its chain and
+// each SIMD has few wavefronts to hide it); this one when the grid fills the
+// chip many times over.
+constexpr int kQ4wThreads = 128;
+constexpr int kQ4wLanes = 8;
+constexpr int kQ4wWgCols = kQ4wThreads / kQ4wLanes;  // 16, as the form above
+static_assert(kQ4wWgCols == kQ4WgCols, "both forms write one record per 16 columns");
+constexpr int kQ4wMinCols = 16384;  // below this the form above is used
+
+// A block of activation takes 36 floats of LDS, not 32: the 8 lanes of a
+// column read blocks j, j+8, ... together, and at a 128-byte stride every
+// second one would share LDS banks; at 144 bytes their 16-byte reads land
+// on distinct banks.
+constexpr int kQ4wXStride = 36;
+template <int kIters> struct Q4wLds {
+  static constexpr int kBlocks = kIters * kQ4wLanes;  // >= n_blocks
+  float x[kBlocks * kQ4wXStride];
+  float sum[kBlocks];
+};
+
+// Buffer descriptor word 3 for gfx9-family raw (stride 0) buffers: loads at
+// or past the byte count return zeros without a memory access.
+constexpr int kQ4BufferWord3 = 0x00020000;
+
+// Column `col` (in range) of m dotted with activation row `xrow`; every lane
+// of the column's group of 8 returns the sum. The weights of iteration i of a
+// lane sit at a constant distance from its first block, so each load is one
+// buffer instruction with an immediate offset; blocks past n_blocks read the
+// next column's bytes, or zeros past the matrix, and get no weight.
+template <int kIters>
+__device__ inline float q4w_dot(const Q4Mat& m, int n_blocks, int col,
+                                const float* __restrict__ xrow, Q4wLds<kIters>& lds) {
+  constexpr int kXRounds = (kIters * kQ4wLanes + kQ4wThreads - 1) / kQ4wThreads;
+  const int t = threadIdx.x;
+  const int j = t & (kQ4wLanes - 1);
+  f32x4 xv[kXRounds][8];
+#pragma unroll
+  for (int r = 0; r < kXRounds; ++r) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(xrow + min(t + r * kQ4wThreads, n_blocks - 1) * 32);
+#pragma unroll
+    for (int v = 0; v < 8; ++v) xv[r][v] = p[v];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // activation loads first: waiting for them waits for no weight
+  const int cells = m.n * n_blocks;   // the host keeps 16 * cells < 2^31
+  const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.quant), 0, cells * 16, kQ4BufferWord3);
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m.scales), 0, cells * 4, kQ4BufferWord3);
+  const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.zp), 0, (cells + 1) / 2, kQ4BufferWord3);
+  const int first = col * n_blocks + j;
+  uint4 qv[kIters];
+  float sc[kIters];
+  uint32_t zb[kIters];
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    qv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rq, first * 16 + 128 * i, 0, 0));
+    sc[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, first * 4 + 32 * i, 0, 0));
+    zb[i] = __builtin_amdgcn_raw_buffer_load_b8(rz, (first >> 1) + 4 * i, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // in iteration order: iteration i waits for i's loads only
+  }
+  // Block first + 8 i has the parity of `first`: the same zero-point nibble.
+  const uint32_t zshift = (first & 1) * 4;
+  // Activation to LDS with block sums. Unconditional (a conditional store
+  // lets the compiler sink the activation loads behind the weights): a
+  // thread past n_blocks holds block n_blocks - 1 and stores it to a spare
+  // slot, or to slot n_blocks - 1 itself with the same values.
+#pragma unroll
+  for (int r = 0; r < kXRounds; ++r) {
+    const int slot = min(t + r * kQ4wThreads, Q4wLds<kIters>::kBlocks - 1);
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      *reinterpret_cast<f32x4*>(&lds.x[slot * kQ4wXStride + 4 * v]) = xv[r][v];
+      s += (xv[r][v][0] + xv[r][v][1]) + (xv[r][v][2] + xv[r][v][3]);
+    }
+    lds.sum[slot] = s;
+  }
+  // LDS-only barrier: waits for this thread's LDS writes, not for its
+  // outstanding weight loads (a __syncthreads fence would wait for those).
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  const f32x4* xl = reinterpret_cast<const f32x4*>(&lds.x[j * kQ4wXStride]);
+  const float* sl = &lds.sum[j];
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < kIters; ++i) {
+    const f32x4* xb = xl + (kQ4wXStride / 4) * kQ4wLanes * i;
+    const uint32_t w[4] = {qv[i].x, qv[i].y, qv[i].z, qv[i].w};
+    float d = 0.f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+      asm volatile("" : "+v"(lo), "+v"(hi));  // one v_cvt_f32_ubyteN per nibble
+      const f32x4 xe = xb[2 * k], xo = xb[2 * k + 1];  // elements 8k .. 8k+7
+      d = fmaf((float)(lo & 255u), xe[0], d);
+      d = fmaf((float)(hi & 255u), xe[1], d);
+      d = fmaf((float)((lo >> 8) & 255u), xe[2], d);
+      d = fmaf((float)((hi >> 8) & 255u), xe[3], d);
+      d = fmaf((float)((lo >> 16) & 255u), xo[0], d);
+      d = fmaf((float)((hi >> 16) & 255u), xo[1], d);
+      d = fmaf((float)(lo >> 24), xo[2], d);
+      d = fmaf((float)(hi >> 24), xo[3], d);
+    }
+    const float z = (float)((zb[i] >> zshift) & 15u);
+    const float blk_sum = sc[i] * fmaf(-z, sl[kQ4wLanes * i], d);
+    acc += j + kQ4wLanes * i < n_blocks ? blk_sum : 0.f;
+    // One iteration at a time: otherwise the scheduler hoists every
+    // iteration's activation reads (32 registers each) ahead of the math.
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  return sum8(acc);
+}
+
+// lm_head + argmax partial, wide form: the record of the workgroup's 16
+// columns goes to argmax_merge_kernel like the form above.
+template <int kIters>
+__global__ __launch_bounds__(kQ4wThreads, 2) void q4w_argmax_kernel(
+    const float* __restrict__ x, const Q4Mat m, int n_blocks, float* __restrict__ logits,
+    unsigned long long* __restrict__ records) {
+  __shared__ __attribute__((aligned(16))) Q4wLds<kIters> lds;
+  __shared__ unsigned long long best;
+  if (threadIdx.x == 0) best = 0ull;  // visible after q4w_dot's barrier
+  const int b = blockIdx.y;
+  const int col = blockIdx.x * kQ4wWgCols + (threadIdx.x >> 3);
+  const float r = q4w_dot<kIters>(m, n_blocks, min(col, m.n - 1), x + (int64_t)b * n_blocks * 32, lds);
+  if ((threadIdx.x & (kQ4wLanes - 1)) == 0 && col < m.n) {
+    if (logits) logits[(int64_t)b * m.n + col] = r;
+    atomicMax(&best, argmax_enc(r, col, argmax_shape(m.n)));
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) records[(int64_t)b * gridDim.x + blockIdx.x] = best;
+}
+
 // Columns [0, Nq) are q, [Nq, Nq + Nkv) k, [Nq + Nkv, Nq + 2 Nkv) v; every
 // range is a multiple of 128 (whole heads), so a workgroup's 16 columns lie
 // in one of them.
@@ -255,6 +393,15 @@ namespace {
 
 int q4_slots(int n_blocks) { return (n_blocks + 63) / 64; }
 
+// Iterations per lane of the wide form for n_blocks, rounded up to an
+// instantiated count; 0 if n_blocks is past its limit.
+int q4w_iters(int n_blocks) {
+  const int need = (n_blocks + kQ4wLanes - 1) / kQ4wLanes;
+  for (int k : {1, 2, 3, 4, 6, 8, 10, 13, 16, 20, 24})
+    if (k >= need) return k;
+  return 0;
+}
+
 template <int kSlots>
 hipError_t launch_gemv_slots(const float* x, const Q4Mat& w, int n_blocks, float* y, int batch,
                              int epilogue, hipStream_t stream) {
@@ -310,6 +457,22 @@ hipError_t launch_q4_argmax(const float* x, const Q4Mat& w, int n_blocks, float*
                             hipStream_t stream) {
   const int per_row = q4_argmax_records_per_row(w.n);
   const dim3 grid(per_row, batch);
+  const int iters = q4w_iters(n_blocks);  // 0 past 24 blocks per lane (K > 6144)
+  // byte offsets into the quant array must stay below 2^31
+  if (w.n >= kQ4wMinCols && iters > 0 && (int64_t)w.n * n_blocks * 16 < ((int64_t)1 << 31)) {
+    switch (iters) {
+#define NWD_Q4W_CASE(K) \
+  case K: q4w_argmax_kernel<K><<<grid, kQ4wThreads, 0, stream>>>(x, w, n_blocks, logits, records); break;
+      NWD_Q4W_CASE(1) NWD_Q4W_CASE(2) NWD_Q4W_CASE(3) NWD_Q4W_CASE(4) NWD_Q4W_CASE(6)
+      NWD_Q4W_CASE(8) NWD_Q4W_CASE(10) NWD_Q4W_CASE(13) NWD_Q4W_CASE(16) NWD_Q4W_CASE(20)
+      NWD_Q4W_CASE(24)
+#undef NWD_Q4W_CASE
+      default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_argmax_merge(records, per_row, w.n, out, batch, stream);
+  }
   switch (q4_slots(n_blocks)) {
     case 1: q4_argmax_kernel<1><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
     case 2: q4_argmax_kernel<2><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, logits, records); break;
