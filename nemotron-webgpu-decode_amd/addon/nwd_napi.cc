@@ -370,6 +370,37 @@ napi_value QkvAppend(napi_env env, napi_callback_info info) {
                               static_cast<const int32_t*>(pos), batch, nullptr));
 }
 
+// argmax(ctx, x, n, out, batch): argmax_partial + argmax_merge
+napi_value Argmax(napi_env env, napi_callback_info info) {
+  napi_value a[5];
+  get_args(env, info, 5, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *x, *out;
+  int32_t n, batch;
+  if (!ctx || !get_ptr(env, a[1], &x) || !get_i32(env, a[2], &n, 0) || !get_ptr(env, a[3], &out) ||
+      !get_i32(env, a[4], &batch, 1))
+    return throw_error(env, "argmax: bad arguments");
+  return check(env, ctx, "argmax",
+               nwd_argmax(ctx, static_cast<const float*>(x), n, static_cast<uint32_t*>(out), batch,
+                          nullptr));
+}
+
+// lmHeadArgmax(ctx, h, w, logits (null for none), out, batch): lm-head, argmax0, argmax1
+napi_value LmHeadArgmax(napi_env env, napi_callback_info info) {
+  napi_value a[6];
+  get_args(env, info, 6, a);
+  nwd_ctx* ctx = get_ctx(env, a[0]);
+  void *h, *logits, *out;
+  nwd_q4_weight w;
+  int32_t batch;
+  if (!ctx || !get_ptr(env, a[1], &h) || !get_q4(env, a[2], &w) || !get_ptr(env, a[3], &logits) ||
+      !get_ptr(env, a[4], &out) || !get_i32(env, a[5], &batch, 1))
+    return throw_error(env, "lmHeadArgmax: bad arguments");
+  return check(env, ctx, "lmHeadArgmax",
+               nwd_lm_head_argmax(ctx, static_cast<const float*>(h), &w, static_cast<float*>(logits),
+                                  static_cast<uint32_t*>(out), batch, nullptr));
+}
+
 // deviceStatus(ctx) -> 0, or throws with the position error
 napi_value DeviceStatus(napi_env env, napi_callback_info info) {
   napi_value a[1];
@@ -397,6 +428,8 @@ napi_value Init(napi_env env, napi_value exports) {
       {"deviceStatus", nullptr, DeviceStatus, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"q4Gemv", nullptr, Q4Gemv, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"qkvAppend", nullptr, QkvAppend, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"lmHeadArgmax", nullptr, LmHeadArgmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);
   return exports;

@@ -58,4 +58,14 @@ __device__ inline uint32_t argmax_decode(unsigned long long enc, ArgmaxShape s) 
   return argmax_index(0xFFFFFFFFu - (uint32_t)enc, s);
 }
 
+// Largest encoding over the 64 lanes of a wave, in every lane.
+__device__ inline unsigned long long wave_max_u64(unsigned long long e) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const unsigned long long o = __shfl_xor(e, m, 64);
+    e = o > e ? o : e;
+  }
+  return e;
+}
+
 }  // namespace nwd

@@ -37,22 +37,42 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
       e = c > e ? c : e;
     }
   }
-  atomicMax(&best, e);
+  e = wave_max_u64(e);
+  if ((t & 63) == 0) atomicMax(&best, e);
   __syncthreads();
   if (t == 0) records[(int64_t)blockIdx.y * gridDim.x + blockIdx.x] = best;
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_merge_kernel(
+// One workgroup per row. A 131072-token vocabulary leaves 8192 records per
+// row (64 KiB): 1024 threads each issue all their loads (8 per pass) before
+// the first comparison, so a row costs about one memory round trip. Loads
+// past the row's end return 0 through the buffer descriptor's range, which
+// is the encoding of "no candidate".
+constexpr int kMergeThreads = 1024;
+constexpr int kMergeLoads = 8;
+
+__global__ __launch_bounds__(kMergeThreads) void argmax_merge_kernel(
     const unsigned long long* __restrict__ records, int n_records, uint32_t n,
     uint32_t* __restrict__ out) {
   __shared__ unsigned long long best;
   const int t = threadIdx.x;
   if (t == 0) best = 0ull;
-  __syncthreads();
-  const unsigned long long* r = records + (int64_t)blockIdx.x * n_records;
+  const auto rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<unsigned long long*>(records + (int64_t)blockIdx.x * n_records), 0,
+      n_records * 8, kBufferWord3);
   unsigned long long e = 0ull;
-  for (int k = t; k < n_records; k += kArgmaxThreads) e = r[k] > e ? r[k] : e;
-  atomicMax(&best, e);
+  for (int base = 0; base < n_records; base += kMergeThreads * kMergeLoads) {
+    unsigned long long v[kMergeLoads];
+#pragma unroll
+    for (int u = 0; u < kMergeLoads; ++u)
+      v[u] = __builtin_bit_cast(unsigned long long, __builtin_amdgcn_raw_buffer_load_b64(
+                                   rr, (base + u * kMergeThreads + t) * 8, 0, 0));
+#pragma unroll
+    for (int u = 0; u < kMergeLoads; ++u) e = v[u] > e ? v[u] : e;
+  }
+  e = wave_max_u64(e);
+  __syncthreads();
+  if ((t & 63) == 0) atomicMax(&best, e);
   __syncthreads();
   if (t == 0) out[blockIdx.x] = argmax_decode(best, argmax_shape(n));
 }
@@ -70,7 +90,7 @@ hipError_t launch_argmax(const float* x, int n, uint32_t* out, int batch,
 
 hipError_t launch_argmax_merge(const unsigned long long* records, int per_row, int n,
                                uint32_t* out, int batch, hipStream_t stream) {
-  argmax_merge_kernel<<<batch, kArgmaxThreads, 0, stream>>>(records, per_row, n, out);
+  argmax_merge_kernel<<<batch, kMergeThreads, 0, stream>>>(records, per_row, n, out);
   return hipGetLastError();
 }
 

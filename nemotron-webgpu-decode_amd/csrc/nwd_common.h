@@ -20,6 +20,9 @@ constexpr int kHeadDim = 128;            // D, the only head size built
 constexpr int kMaxSeq = 1 << 22;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kNegBig = -3.4028234663852886e38f;  // finite "minus infinity"
+// Buffer descriptor word 3 for gfx9-family raw (stride 0) buffers: loads at
+// or past the descriptor's byte count return zeros without a memory access.
+constexpr int kBufferWord3 = 0x00020000;
 
 // Status bits written by kernels into the context's device status word.
 constexpr int kStatusBadPos = 1;

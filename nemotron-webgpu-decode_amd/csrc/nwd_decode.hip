@@ -62,8 +62,6 @@ namespace nwd {
 constexpr int kWaves = NWD_DECODE_WAVES;
 constexpr int kThreads = kWaves * 64;
 
-// Buffer descriptor word 3 for gfx9-family raw (stride 0) buffers.
-constexpr int kBufferWord3 = 0x00020000;
 
 template <int G> struct DecodeCfg {
   static constexpr int kLanes = 16;               // lanes per key row

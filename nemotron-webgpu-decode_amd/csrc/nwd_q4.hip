@@ -226,10 +226,6 @@ template <int kIters> struct Q4wLds {
   float sum[kBlocks];
 };
 
-// Buffer descriptor word 3 for gfx9-family raw (stride 0) buffers: loads at
-// or past the byte count return zeros without a memory access.
-constexpr int kQ4BufferWord3 = 0x00020000;
-
 // Column `col` (in range) of m dotted with activation row `xrow`; every lane
 // of the column's group of 8 returns the sum. The weights of iteration i of a
 // lane sit at a constant distance from its first block, so each load is one
@@ -250,9 +246,9 @@ __device__ inline float q4w_dot(const Q4Mat& m, int n_blocks, int col,
   }
   __builtin_amdgcn_sched_barrier(0);  // activation loads first: waiting for them waits for no weight
   const int cells = m.n * n_blocks;   // the host keeps 16 * cells < 2^31
-  const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.quant), 0, cells * 16, kQ4BufferWord3);
-  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m.scales), 0, cells * 4, kQ4BufferWord3);
-  const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.zp), 0, (cells + 1) / 2, kQ4BufferWord3);
+  const auto rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.quant), 0, cells * 16, kBufferWord3);
+  const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(m.scales), 0, cells * 4, kBufferWord3);
+  const auto rz = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(m.zp), 0, (cells + 1) / 2, kBufferWord3);
   const int first = col * n_blocks + j;
   uint4 qv[kIters];
   float sc[kIters];

@@ -153,4 +153,40 @@ class AttentionSlice {
   }
 }
 
-module.exports = { AttentionSlice, NANO4B, ATTN_LAYERS, addon };
+// The end of a decode step (engine/runtime.js:397-399): lm-head GEMV, then
+// argmax_partial and argmax_merge, leaving the token id on the device (the
+// reference's tokenOut, :125-128) for the next step's embedding. Here the
+// lm_head projection and the partial pick are one launch and the merge a
+// second; the index has the reference's exact tie order.
+class GreedyHead {
+  constructor(slice, weight) {
+    this.ctx = slice.ctx;  // shares the attention slice's context (stream order)
+    this.w = weight;       // nwd_q4_weight descriptor of lm_head (slice.uploadQ4)
+    this.tokenOut = addon.malloc(4);
+    this.logits = null;
+  }
+
+  // hNorm: the final norm's output, f32 [hidden] on the device (runtime.js:396).
+  encode(hNorm, keepLogits = false) {
+    if (keepLogits && !this.logits) this.logits = addon.malloc(this.w.n * 4);
+    addon.lmHeadArgmax(this.ctx, hNorm, this.w, keepLogits ? this.logits : null, this.tokenOut, 1);
+  }
+
+  readToken() {
+    const t = new Uint32Array(1);
+    addon.download(t, this.tokenOut);
+    return t[0];
+  }
+
+  readLogits(out = new Float32Array(this.w.n)) {
+    addon.download(out, this.logits);
+    return out;
+  }
+
+  destroy() {
+    addon.free(this.tokenOut);
+    if (this.logits) addon.free(this.logits);
+  }
+}
+
+module.exports = { AttentionSlice, GreedyHead, NANO4B, ATTN_LAYERS, addon };

@@ -94,3 +94,28 @@ def test_node_host_full_layer_from_hidden_state(tmp_path):
         slack = 1e-6 * bound + np.abs(h64) * 2.0 ** -23
         assert np.all(np.abs(hout[t] - h64) <= slack), t
     assert worst < 2e-3, worst
+
+
+def test_node_host_greedy_head(tmp_path):
+    """js/check_head.js: GreedyHead (lm_head GEMV + greedy pick,
+    engine/runtime.js:397-399) on a 32768-token 4-bit lm_head. The logits are
+    within 1e-6 of sum |w a| of the float64 projection, and the token read
+    back equals the oracle's pick on those logits, bit-exact."""
+    out = tmp_path / "head"
+    print("node check_head vocab=32768 hidden=3136 steps=4", flush=True)
+    res = subprocess.run(["node", str(JS / "check_head.js"), str(out), "32768", "3136", "4"],
+                         capture_output=True, text=True, timeout=180)
+    assert res.returncode == 0, res.stdout + res.stderr
+    man = json.loads((out / "manifest.json").read_text())
+    V, hid, T = man["vocab"], man["hidden"], man["steps"]
+    nb = hid // 32
+    quant = np.fromfile(out / "quant.u8", np.uint8).reshape(V, nb, 16)
+    scales = np.fromfile(out / "scales.f32", np.float32).reshape(V, nb)
+    zp = np.fromfile(out / "zp.u8", np.uint8)
+    h = np.fromfile(out / "h.f32", np.float32).reshape(T, hid)
+    logits = np.fromfile(out / "logits.f32", np.float32).reshape(T, V)
+    tokens = np.fromfile(out / "tokens.u32", np.uint32)
+    for t in range(T):
+        y64, bound = gemv_f64(h[t], quant, scales, zp)
+        assert np.all(np.abs(logits[t] - y64) <= 1e-6 * bound), t
+        assert tokens[t] == oracle.argmax_ref(logits[t]), t

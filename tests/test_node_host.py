@@ -26,7 +26,7 @@ def test_addon_exports():
     names = set(json.loads(out))
     assert {"create", "destroy", "cacheBytes", "malloc", "free", "upload", "download", "zero",
             "sync", "kvAppend", "decode", "appendDecode", "prefill", "deviceStatus",
-            "q4Gemv", "qkvAppend"} <= names
+            "q4Gemv", "qkvAppend", "argmax", "lmHeadArgmax"} <= names
 
 
 def test_create_errors_are_thrown_with_the_library_message():
@@ -40,6 +40,8 @@ for (const d of [{nHeads: 30, nKvHeads: 8, maxSeq: 16}, {nHeads: 24, nKvHeads: 8
 try { a.decode(null, 0n, 0n, 0n, 0n, 0n, 1, 0); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 try { a.q4Gemv(null, 0n, {}, 0n, 1, 0); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 try { a.qkvAppend(null, 0n, {}, {}, {}, 0n, 0n, 0n, 0n, 1); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
+try { a.argmax(null, 0n, 16, 0n, 1); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
+try { a.lmHeadArgmax(null, 0n, {}, null, 0n, 1); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 console.log(JSON.stringify(msgs));
 """)
     m = json.loads(out)
@@ -48,6 +50,7 @@ console.log(JSON.stringify(msgs));
     assert "sizes must be positive" in m[2]
     assert m[3].startswith("decode:")
     assert m[4].startswith("q4Gemv:") and m[5].startswith("qkvAppend:")
+    assert m[6].startswith("argmax:") and m[7].startswith("lmHeadArgmax:")
 
 
 def test_js_module_parses():
@@ -57,6 +60,7 @@ def test_js_module_parses():
     res = subprocess.run(["node", "--check", str(JS / "check_attention.js")], capture_output=True,
                          text=True, timeout=60)
     assert res.returncode == 0, res.stderr
-    res = subprocess.run(["node", "--check", str(JS / "check_layer.js")], capture_output=True,
-                         text=True, timeout=60)
-    assert res.returncode == 0, res.stderr
+    for script in ("check_layer.js", "check_head.js"):
+        res = subprocess.run(["node", "--check", str(JS / script)], capture_output=True,
+                             text=True, timeout=60)
+        assert res.returncode == 0, res.stderr
