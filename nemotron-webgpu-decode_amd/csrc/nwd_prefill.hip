@@ -23,7 +23,8 @@
 //     4 consecutive keys of ONE row — its own softmax row;
 //   - causal mask only on tiles that cross a row's limit; online softmax in
 //     log2 units with the scale folded into the exp2 argument (one FMA per
-//     score); O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
+//     score), the row sum taken over the fp16 weights the PV product uses
+//     (v_dot2 with ones, two weights per instruction); O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
 //     registers from the S^T accumulators with no data movement between
 //     lanes, and V^T is read from the row-major V tile with two
 //     ds_read_b64_tr_b16 transpose loads per operand (gfx950): within a
@@ -144,13 +145,22 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   // and of V — 16 lanes cover one 256-byte row — and stores them row-major.
   f16x8 kr[4], vr[4];
   const int k_run = tid & 15, k_row = tid >> 4;
+  // K/V rows come through buffer descriptors that end at key kend: rows
+  // past it (the tail of the last tile, the prefetch after it) read as zeros
+  // without a memory access.
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(kb_ptr), 0,
+                                                    kend * (kHeadDim * 2), kBufferWord3);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(vb_ptr), 0,
+                                                    kend * (kHeadDim * 2), kBufferWord3);
+  const uint32_t stage_off = (uint32_t)k_row * (kHeadDim * 2) + k_run * 16;
   auto load_tile = [&](int kt) {
-    const int k0 = kt * kPBN;
+    const uint32_t t_off = stage_off + (uint32_t)kt * (kPBN * kHeadDim * 2);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t off = (int64_t)min(k0 + k_row + 32 * i, kend - 1) * kHeadDim + k_run * 8;
-      kr[i] = *reinterpret_cast<const f16x8*>(kb_ptr + off);
-      vr[i] = *reinterpret_cast<const f16x8*>(vb_ptr + off);
+      kr[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rk, t_off + i * 32 * (kHeadDim * 2), 0, 0));
+      vr[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
+                                            rv, t_off + i * 32 * (kHeadDim * 2), 0, 0));
     }
   };
   auto store_tile = [&](int buf) {
@@ -176,12 +186,12 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   const float c = qk_scale_log2;
 
   // Prologue: tile 0 into LDS, tile 1 in flight. Loads and stores in the
-  // loop are unconditional (indices clamped to the last tile) so the compiler
-  // can wait for exactly the older loads instead of all of them.
+  // loop are unconditional (past the last tile they read zeros) so the
+  // compiler can wait for exactly the older loads instead of all of them.
   load_tile(0);
   store_tile(0);
   __syncthreads();
-  load_tile(min(1, ntiles - 1));
+  load_tile(1);
 
   for (int kt = 0; kt < ntiles; ++kt) {
     const int buf = kt & 1;
@@ -239,9 +249,12 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float p = fast_exp2(fmaf(st[kb][rb][e], c, -mc));
-          lsum[rb] += p;
           pb[rb][kb * 4 + e] = (f16)p;
         }
+      // the row sum of the fp16 weights the PV product uses
+#pragma unroll
+      for (int e = 0; e < 8; e += 2)
+        lsum[rb] = dot2(f16x2{pb[rb][e], pb[rb][e + 1]}, f16x2{(f16)1.f, (f16)1.f}, lsum[rb]);
     }
 
 #pragma unroll
@@ -255,7 +268,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
 
     store_tile(buf ^ 1);  // tile kt+1; its last readers passed the previous barrier
     __syncthreads();
-    load_tile(min(kt + 2, ntiles - 1));
+    load_tile(kt + 2);
   }
 
   // Row totals of this key quarter, then merge the quarters through LDS:
