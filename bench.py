@@ -44,9 +44,12 @@ def log(*a):
 
 class DecodeWorkload:
     """`layers` distinct caches of `past` random tokens plus `window` tokens
-    of new rows and queries, all on the device."""
+    of new rows and queries, all on the device. K/V are N(0,1), times a
+    per-KV-head scale drawn U[0.5, 2] (`dist="head-scale"`), or with 1% of
+    entries replaced by +-8 (`dist="outliers"`)."""
 
-    def __init__(self, torch, nw, past: int, window: int, layers: int, seed: int):
+    def __init__(self, torch, nw, past: int, window: int, layers: int, seed: int,
+                 dist: str = "normal"):
         self.torch, self.past, self.window, self.layers = torch, past, window, layers
         self.cap = past + window
         g = torch.Generator(device="cuda")
@@ -56,10 +59,24 @@ class DecodeWorkload:
         def rnd(*shape):
             return torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32).to(f16)
 
-        self.kc = [rnd(1, HKV, self.cap, D) for _ in range(layers)]
-        self.vc = [rnd(1, HKV, self.cap, D) for _ in range(layers)]
-        self.knew = rnd(window, 1, HKV, D)
-        self.vnew = rnd(window, 1, HKV, D)
+        # one scale per KV head for K and one for V (caches and new rows alike)
+        hs_k = torch.rand(HKV, generator=g, device="cuda") * 1.5 + 0.5
+        hs_v = torch.rand(HKV, generator=g, device="cuda") * 1.5 + 0.5
+
+        def kv(shape, hs, head_axis):
+            x = torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32)
+            if dist == "head-scale":
+                x *= hs.view(HKV, *([1] * (len(shape) - head_axis - 1)))
+            elif dist == "outliers":
+                hit = torch.rand(*shape, generator=g, device="cuda") < 0.01
+                sign = torch.randint(0, 2, shape, generator=g, device="cuda") * 2 - 1
+                x = torch.where(hit, 8.0 * sign, x)
+            return x.to(f16)
+
+        self.kc = [kv((1, HKV, self.cap, D), hs_k, 1) for _ in range(layers)]
+        self.vc = [kv((1, HKV, self.cap, D), hs_v, 1) for _ in range(layers)]
+        self.knew = kv((window, 1, HKV, D), hs_k, 2)
+        self.vnew = kv((window, 1, HKV, D), hs_v, 2)
         self.q = rnd(window, 1, H, D)
         self.out = torch.empty(1, H, D, dtype=f16, device="cuda")
         self.pos = torch.arange(past, past + window, dtype=torch.int32, device="cuda")
@@ -357,21 +374,22 @@ EXTRA_WORKLOADS = {
 }
 
 WORKLOADS = {
-    # name: (past, window, layers, description)
-    "decode-4k": (4096, 64, 32, "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, append+attend "
-                                "per step, 32 layer caches rotated (545 MB)"),
-    "decode-32k": (32768, 64, 4, "decode-32k: B=1, 32q/8kv/d128, past 32768 (1% +-8 outliers "
-                                 "in the parity tests), append+attend per step, split-K, 4 layer "
-                                 "caches rotated (537 MB)"),
+    # name: (past, window, layers, K/V distribution, description)
+    "decode-4k": (4096, 64, 32, "head-scale",
+                  "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, K/V N(0,1) x per-head "
+                  "U[0.5,2], append+attend per step, 32 layer caches rotated (545 MB)"),
+    "decode-32k": (32768, 64, 4, "outliers",
+                   "decode-32k: B=1, 32q/8kv/d128, past 32768, K/V N(0,1) with 1% +-8 outliers, "
+                   "append+attend per step, split-K, 4 layer caches rotated (537 MB)"),
 }
 
 
 def run_workload(torch, nw, name: str, steps: int, warmup: int):
     """Times `steps` append+attend steps and `steps` decode-only calls of one
     workload from HIP graphs; returns a dict of the measurements."""
-    past, window, layers, desc = WORKLOADS[name]
+    past, window, layers, dist, desc = WORKLOADS[name]
     log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
-    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234)
+    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
     wall, ms = time_graph(torch, wl, steps, warmup)
     us_step = ms * 1e3 / steps
     mean_b = wl.mean_kv_bytes(steps)
@@ -543,7 +561,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "storage_dtype": "f16",
-        "data": "synthetic (seeded N(0,1) fp16 K/V/Q)",
+        "data": "synthetic, seeded: fp16 Q N(0,1), K/V as the workload states",
         "config": {
             "workload": main_res["desc"],
             "batch": 1, "n_heads": H, "n_kv_heads": HKV, "head_dim": D,

@@ -30,12 +30,13 @@
 // — the partial/merge structure of kernels/argmax_partial.wgsl:16-52 and
 // kernels/argmax_merge.wgsl:8-42, with (max, sum, o[D]) records instead of
 // (value, index) pairs. Optionally (nwd_set_decode_merge) the merge runs in
-// the split kernel itself: records are written with device-scope atomic
-// stores and the workgroup that takes the last arrival ticket of its
-// (b, hkv) invalidates its L2 and merges them. That saves the second launch
-// but adds serialised memory round trips at the end of every workgroup. A
-// release fence per workgroup instead of the write-through stores would cost
-// a full L2 write-back each (~0.15 us, serialised on MI355X).
+// the split kernel itself: records are written through to memory (vector
+// stores with the agent-coherent cache policy sc1) and the workgroup that
+// takes the last arrival ticket of its (b, hkv) reads them with sc1 loads
+// and merges them. That saves the second launch but adds serialised memory
+// round trips at the end of every workgroup. A release fence per workgroup
+// instead of the write-through stores would cost a full L2 write-back each
+// (~0.15 us, serialised on MI355X).
 //
 // The key range is partitioned from the host's length bound (max_len), not
 // from the device position, so a workgroup's first K/V loads do not wait for
@@ -115,11 +116,6 @@ __device__ inline f16x8 convert_src_run(const SrcRun& r, bool src16) {
   return h;
 }
 
-// Device-scope relaxed atomic accesses: coherent across the XCDs' L2 caches
-// without the full-L2 write-back a release fence costs.
-__device__ inline void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 // s_waitcnt vmcnt(0): every earlier global access of this thread is complete.
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
@@ -142,7 +138,7 @@ template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) 
 //      weighted by 2^(m - M). The running max M of a head is the same in
 //      every thread, so the 8 thread groups' sums add without rescaling
 //      (xor-32 lane exchange, then LDS across the 4 wavefronts).
-template <int G, bool kO16>
+template <int G, bool kO16, int kPolicy>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
                                    int64_t hrow0, int nsplit, float* lds) {
@@ -157,6 +153,10 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
   float* lds_mp = lds + G * 512 + 2 * kThreads;                 // [G]
   float* lds_lp = lds_mp + G;                                   // [G]
   const int64_t rec0 = hrow0 * nsplit;  // record (g, s) is rec0 + g * nsplit + s
+  const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(part_ml + rec0), 0,
+                                                      G * nsplit * 8, kBufferWord3);
+  const auto r_o = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_o + rec0 * kHeadDim), 0,
+                                                     G * nsplit * kHeadDim * 4, kBufferWord3);
 
   float M[G], Lr[G];
   f32x4 acc[G];
@@ -171,7 +171,8 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
     // 1. Loads (indexes clamped in range; entries past the pass get no weight).
     const int mg = t / kMergeChunk, ms = t % kMergeChunk;
     const bool mvalid = mg < G && ms < ns;
-    const float2 mlv = part_ml[rec0 + min(mg, G - 1) * nsplit + s0 + min(ms, ns - 1)];
+    const float2 mlv = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+        r_ml, (min(mg, G - 1) * nsplit + s0 + min(ms, ns - 1)) * 8, 0, kPolicy));
     __builtin_amdgcn_sched_barrier(0);  // the (m, l) load is waited for first: issue it first
     f32x4 ov[G][kPer];
 #pragma unroll
@@ -179,7 +180,8 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
 #pragma unroll
       for (int k = 0; k < kPer; ++k) {
         const int s = s0 + min(j + 8 * k, ns - 1);
-        ov[g][k] = *reinterpret_cast<const f32x4*>(part_o + (rec0 + g * nsplit + s) * kHeadDim + d4 * 4);
+        ov[g][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+            r_o, ((g * nsplit + s) * kHeadDim + d4 * 4) * 4, 0, kPolicy));
       }
     // 2. Pass max and sum per head.
     lds_ml[t] = mvalid ? mlv : make_float2(kNegBig, 0.f);
@@ -514,35 +516,56 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
 
-  // Merge the wavefronts: one record (or the output) per head.
+  // Merge the wavefronts: one record (or the output) per head; thread t
+  // owns the 4-dim run t % 32 of head t / 32.
   const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
-  for (int idx = tid; idx < G * kHeadDim; idx += kThreads) {
-    const int g = idx / kHeadDim, d = idx - g * kHeadDim;
+  // Record stores of the in-kernel merge write through to memory (agent
+  // coherence, cache policy sc1), so the merging workgroup can read them on
+  // any XCD without an L2 write-back here.
+  constexpr int kRecPolicy = 16;
+  static_assert(G * 32 <= kThreads, "one 4-dim run per thread");
+  if (tid < G * 32) {
+    const int g = tid >> 5, d4 = tid & 31;
     float M = kNegBig;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
-    float o = 0.f, lt = 0.f;
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    float lt = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
       const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
-      o = fmaf(lds_o[(w * G + g) * kHeadDim + d], sc, o);
+      o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
       lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
     }
     if (nsplit == 1) {
-      const float r = o / lt;
-      if constexpr (kO16) static_cast<f16*>(a.out)[(hrow0 + g) * kHeadDim + d] = (f16)r;
-      else static_cast<float*>(a.out)[(hrow0 + g) * kHeadDim + d] = r;
-    } else {
-      const int64_t rec = (hrow0 + g) * nsplit + split;
-      if (a.fused_merge) {
-        st_dev(a.part_o + rec * kHeadDim + d, o);
-        if (d == 0) {
-          st_dev(reinterpret_cast<float*>(a.part_ml + rec), M);
-          st_dev(reinterpret_cast<float*>(a.part_ml + rec) + 1, lt);
-        }
+      const float inv = 1.f / lt;
+      const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
+      if constexpr (kO16) {
+        f16x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
+        *reinterpret_cast<f16x4*>(static_cast<f16*>(a.out) + at) = v;
       } else {
-        a.part_o[rec * kHeadDim + d] = o;
-        if (d == 0) a.part_ml[rec] = make_float2(M, lt);
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + at) = o * inv;
+      }
+    } else {
+      // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
+      const int64_t rec0 = hrow0 * nsplit + split;
+      const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
+                                                         G * nsplit * kHeadDim * 4, kBufferWord3);
+      const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
+                                                          kBufferWord3);
+      const uint32_t off = (g * nsplit * kHeadDim + d4 * 4) * 4;
+      if (a.fused_merge) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, kRecPolicy);
+        if (d4 == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
+                                                g * nsplit * 8, 0, kRecPolicy);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, 0);
+        if (d4 == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
+                                                g * nsplit * 8, 0, 0);
       }
     }
   }
@@ -569,10 +592,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
   if (!lds_last) return;
-  // Acquire at device scope: invalidates this XCD's L2 (no write-back), so
-  // the plain loads of the merge see the records other XCDs wrote through.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  merge_group<G, kO16>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
+  // The records are read with agent-coherent loads (cache policy sc1), so
+  // they see what the other workgroups wrote through before their tickets.
+  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
   if (tid == 0)
     __hip_atomic_store(&a.counters[b * a.n_kv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -584,7 +606,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
     void* __restrict__ out, int n_heads, int nsplit) {
   __shared__ __attribute__((aligned(16))) float lds[merge_lds_floats<G>()];
   const int hkv = blockIdx.x, b = blockIdx.y;
-  merge_group<G, kO16>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
+  merge_group<G, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + hkv * G, nsplit, lds);
 }
 
 template <int G, bool kQ16, bool kO16>
