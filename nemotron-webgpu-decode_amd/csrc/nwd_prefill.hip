@@ -14,10 +14,13 @@
 // K/V fragment read from LDS feeds two MFMAs, which halves LDS traffic per
 // flop against 16-row waves, and two wavefronts share each SIMD so the
 // matrix cores always have a second wavefront to issue from.
-//   - K and V rows are staged in LDS row-major with coalesced 16-byte loads
-//     and stores, padded against bank conflicts and double-buffered: the
-//     next tile's global loads are in flight during the current tile's MFMAs
-//     and one barrier per tile suffices;
+//   - K and V rows go from memory straight into LDS (buffer_load_dwordx4
+//     with the lds flag, gfx950: one instruction writes 1 KB, lane l's 16
+//     bytes at +16l), double-buffered: the next tile's copies land while the
+//     current tile is computed, and one wait plus one barrier per tile
+//     publish them. Rows are unpadded (256 B); the 16-byte chunks of a row
+//     are XOR-swizzled by the row index so the MFMA operand reads hit
+//     distinct banks (each lane fetches the chunk its LDS slot must hold);
 //   - S^T = K Q^T on v_mfma_f32_16x16x32_f16 (K from LDS as the A operand,
 //     the query rows held in registers as the B operand), so each lane holds
 //     4 consecutive keys of ONE row — its own softmax row;
@@ -42,12 +45,16 @@ constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kPBM = 64;                    // rows per workgroup
 constexpr int kPBN = 128;                   // keys per tile
-constexpr int kKsStride = kHeadDim + 8;     // halves per K row in LDS (68 dwords: 16-byte
-                                            // reads of 16 rows hit distinct banks)
-constexpr int kVsStride = kHeadDim + 16;    // halves per V row in LDS (72 dwords: the 4 rows
-                                            // of a transpose load hit distinct banks)
-constexpr int kKsHalves = kPBN * kKsStride;
-constexpr int kVsHalves = kPBN * kVsStride;
+constexpr int kRowBytes = kHeadDim * 2;     // 256: K/V rows are unpadded in LDS
+constexpr int kTileBytes = kPBN * kRowBytes;  // 32 KB
+constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per copy (4)
+// Chunk swizzles (16 chunks of 16 bytes per row): physical chunk p of LDS
+// row r holds logical chunk p ^ kswz(r) of a K row, p ^ vswz(r) of a V row.
+// A K operand read (16 rows, one logical chunk) then covers 16 distinct
+// chunks, and a transpose read (4 rows x 2 chunks per 16 lanes) 8.
+__device__ inline int kswz(int r) { return r & 15; }
+__device__ inline int vswz(int r) { return (r & 7) << 1; }
+typedef __attribute__((address_space(3))) void lds_void;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -87,8 +94,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
     int mtiles, float qk_scale_log2, int* __restrict__ status) {
   constexpr int RB = 2;  // 16-row MFMA blocks per wavefront
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
-  f16* Ks = smem;                       // [2][kPBN][kKsStride]
-  f16* Vs = smem + 2 * kKsHalves;       // [2][kPBN][kVsStride]
+  char* lds = reinterpret_cast<char*>(smem);  // K0 K1 V0 V1, 32 KB each
 
   const int id = blockIdx.x;
   const int hkv = id % n_kv;
@@ -141,37 +147,30 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   const f16* kb_ptr = k_cache + slab;
   const f16* vb_ptr = v_cache + slab;
 
-  // Staging: thread t loads run (t&15) of keys (t>>4) + 32*i, i < 4, of K
-  // and of V — 16 lanes cover one 256-byte row — and stores them row-major.
-  f16x8 kr[4], vr[4];
-  const int k_run = tid & 15, k_row = tid >> 4;
-  // K/V rows come through buffer descriptors that end at key kend: rows
-  // past it (the tail of the last tile, the prefetch after it) read as zeros
-  // without a memory access.
   const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(kb_ptr), 0,
                                                     kend * (kHeadDim * 2), kBufferWord3);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(vb_ptr), 0,
                                                     kend * (kHeadDim * 2), kBufferWord3);
-  const uint32_t stage_off = (uint32_t)k_row * (kHeadDim * 2) + k_run * 16;
-  auto load_tile = [&](int kt) {
-    const uint32_t t_off = stage_off + (uint32_t)kt * (kPBN * kHeadDim * 2);
+  // Wave w copies rows 16w .. 16w+15 of a tile, 4 rows (1 KB) per
+  // instruction: lane l fills physical chunk l & 15 of row 16w + 4i + l/16.
+  // Rows past kend read as zeros (buffer range check), so no LDS row is
+  // ever stale.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int st_row = 16 * wv + (lane >> 4), st_p = lane & 15;
+  auto load_tile = [&](int kt, int bb) {
+    char* kdst = lds + bb * kTileBytes + wv * 16 * kRowBytes;
+    char* vdst = lds + (2 + bb) * kTileBytes + wv * 16 * kRowBytes;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kr[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rk, t_off + i * 32 * (kHeadDim * 2), 0, 0));
-      vr[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(
-                                            rv, t_off + i * 32 * (kHeadDim * 2), 0, 0));
+    for (int i = 0; i < kStageInsts; ++i) {
+      const int row = st_row + 4 * i;
+      const uint32_t rb_off = (uint32_t)(kt * kPBN + row) * kRowBytes;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(kdst + i * 1024), 16,
+                                               rb_off + ((st_p ^ kswz(row)) << 4), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vdst + i * 1024), 16,
+                                               rb_off + ((st_p ^ vswz(row)) << 4), 0, 0, 0);
     }
   };
-  auto store_tile = [&](int buf) {
-    f16* ks = Ks + buf * kKsHalves;
-    f16* vs = Vs + buf * kVsHalves;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *reinterpret_cast<f16x8*>(&ks[(k_row + 32 * i) * kKsStride + k_run * 8]) = kr[i];
-      *reinterpret_cast<f16x8*>(&vs[(k_row + 32 * i) * kVsStride + k_run * 8]) = vr[i];
-    }
-  };
+  auto wait_tile = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
 
   // Running max of the raw scores (log2 units after scaling) and sums.
   float m[RB], lsum[RB];
@@ -185,21 +184,24 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   }
   const float c = qk_scale_log2;
 
-  // Prologue: tile 0 into LDS, tile 1 in flight. Loads and stores in the
-  // loop are unconditional (past the last tile they read zeros) so the
-  // compiler can wait for exactly the older loads instead of all of them.
-  load_tile(0);
-  store_tile(0);
+  // Prologue: tile 0 into LDS, tile 1 in flight.
+  load_tile(0, 0);
+  wait_tile();
   __syncthreads();
-  load_tile(1);
+  load_tile(1, 1);
 
   for (int kt = 0; kt < ntiles; ++kt) {
     const int buf = kt & 1;
-    const f16* ks = Ks + buf * kKsHalves + kq * 32 * kKsStride;
-    // transpose-load addresses: lane 4e+c of a 16-lane group reads dims
-    // 4c..4c+3 (of each 16-dim block) of key row 4*lq + e (+16 for the
-    // second half of the operand)
-    const f16* vs = Vs + buf * kVsHalves + (kq * 32 + 4 * lq + (lr >> 2)) * kVsStride + 4 * (lr & 3);
+    const char* ks = lds + buf * kTileBytes + kq * 32 * kRowBytes;
+    const char* vs = lds + (2 + buf) * kTileBytes + kq * 32 * kRowBytes;
+    // transpose reads: lane 4e+c of a 16-lane group reads dims 4c..4c+3 (of
+    // each 16-dim block) of key row 4*lq + e (+16 for the second half of the
+    // operand); those dims are logical chunk 2*dblk + c/2, bytes 8*(c&1).
+    const int vr0 = 4 * lq + (lr >> 2);
+    auto vaddr = [&](int r, int dblk) {
+      return reinterpret_cast<const f16*>(vs + r * kRowBytes +
+                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz(r)) << 4) + 8 * (lr & 1));
+    };
     const int k0 = kt * kPBN + kq * 32;
 
     // st[kb][rb][e] = raw score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr)
@@ -212,7 +214,8 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&ks[(kb * 16 + lr) * kKsStride + db * 32 + 8 * lq]);
+        const f16x8 a = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
+                                                        (((4 * db + lq) ^ lr) << 4));
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) st[kb][rb] = mfma16x16x32(a, qf[rb][db], st[kb][rb]);
       }
@@ -259,16 +262,16 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
 
 #pragma unroll
     for (int dblk = 0; dblk < 8; ++dblk) {
-      const f16x4 lo = lds_read_tr16(vs + dblk * 16);
-      const f16x4 hi = lds_read_tr16(vs + 16 * kVsStride + dblk * 16);
+      const f16x4 lo = lds_read_tr16(vaddr(vr0, dblk));
+      const f16x4 hi = lds_read_tr16(vaddr(16 + vr0, dblk));
       const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) o[rb][dblk] = mfma16x16x32(a, pb[rb], o[rb][dblk]);
     }
 
-    store_tile(buf ^ 1);  // tile kt+1; its last readers passed the previous barrier
-    __syncthreads();
-    load_tile(kt + 2);
+    wait_tile();      // this wave's part of tile kt+1 is in LDS
+    __syncthreads();  // every part is, and every wave is done with tile kt
+    if (kt + 2 < ntiles) load_tile(kt + 2, buf);  // nothing lands in LDS after the loop
   }
 
   // Row totals of this key quarter, then merge the quarters through LDS:
@@ -333,7 +336,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   }
 }
 
-constexpr size_t kPrefillLds = (size_t)(2 * kKsHalves + 2 * kVsHalves) * sizeof(f16);
+constexpr size_t kPrefillLds = (size_t)4 * kTileBytes;
 static_assert(kPrefillLds >= (size_t)3 * 2 * 64 * 2 * 34 * sizeof(float), "merge exchange fits");
 static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
 
