@@ -12,16 +12,21 @@
 // in order of the flat index col * n_blocks + blk. One weight is
 // (nib - zp) * scale.
 //
-// Mapping: a 256-thread workgroup (4 wavefronts) owns 16 consecutive output
-// columns, 4 per wavefront. Lane l of a wavefront owns the K-blocks l, l+64,
-// l+128, l+192 (kSlots of them) of its 4 columns: it holds the activation of
-// those blocks in registers (32 f32 each, plus their sum) and requests every
-// quant run (16 bytes), scale and zero-point byte of its 4 columns before
-// computing, so a wavefront has all its weight bytes in flight at once. A
-// block contributes scale * (sum_i nib_i * x_i - zp * sum_i x_i): 32 FMAs on
-// nibbles converted with v_cvt_f32_ubyte, then one FMA and one multiply-add.
-// The 64 lanes' partial sums of a column are added with DPP row steps and
-// lane-swap exchanges, and lane 0 writes the 4 columns.
+// Mapping: a 256-thread workgroup (4 wavefronts) owns 16 / kSplit groups of
+// 4 consecutive output columns; kSplit wavefronts share a group, each taking
+// 1/kSplit of the K-blocks (kSplit = 4 at K = 5120, 2 at K = 3136: at least
+// 32 blocks per wavefront). Lane l of a wavefront owns the blocks first + l,
+// first + l + 64, ... (kSlots of them) of its part for the group's 4 columns:
+// it holds the activation of those blocks in registers (32 f32 each, plus
+// their sum) and requests every quant run (16 bytes), scale and zero-point
+// byte before computing, so a wavefront has all its weight bytes in flight
+// at once. A block contributes scale * (sum_i nib_i * x_i - zp * sum_i x_i):
+// 32 FMAs on nibbles converted with v_cvt_f32_ubyte, then one FMA and one
+// multiply-add. The 64 lanes' partial sums of a column are added with DPP
+// row steps and lane-swap exchanges, the parts' sums through LDS in part
+// order, and one lane writes the 4 columns. Splitting K over wavefronts
+// shortens each wavefront's serial chain (the kernels are latency-bound at
+// batch 1): 7.8 -> 7.0 us for q/k/v, 7.5 -> 6.6 us for o_proj.
 //
 // The reference instead gives each of its 4-column workgroups 256 threads
 // striding over the blocks (98 for K = 3136, so 158 threads idle) and
@@ -49,12 +54,14 @@ template <int kSlots> struct Q4Act {
   float sum[kSlots];
 };
 
+// Blocks [first, end) of the row, lane l taking first + l, first + l + 64,
+// ... (clamped in range; slots past end get no weight).
 template <int kSlots>
-__device__ inline void q4_load_act(const float* __restrict__ x, int n_blocks, Q4Act<kSlots>& a) {
+__device__ inline void q4_load_act(const float* __restrict__ x, int first, int end, Q4Act<kSlots>& a) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int j = 0; j < kSlots; ++j) {
-    const int blk = min(lane + 64 * j, n_blocks - 1);  // in range; extra slots get no weight
+    const int blk = min(first + lane + 64 * j, end - 1);
     const f32x4* p = reinterpret_cast<const f32x4*>(x + blk * 32);
 #pragma unroll
     for (int v = 0; v < 8; ++v) {
@@ -84,8 +91,8 @@ __device__ inline void q4_act_sums(Q4Act<kSlots>& a) {
 // activation in `a`; every lane returns the 4 sums. Columns past m.n read
 // column m.n - 1 (their results are not written).
 template <int kSlots>
-__device__ inline void q4_columns(const Q4Mat& m, int n_blocks, int col0, Q4Act<kSlots>& a,
-                                  float (&out)[kQ4Cols]) {
+__device__ inline void q4_columns(const Q4Mat& m, int n_blocks, int first, int end, int col0,
+                                  Q4Act<kSlots>& a, float (&out)[kQ4Cols]) {
   const int lane = threadIdx.x & 63;
   uint4 qv[kQ4Cols][kSlots];
   float sc[kQ4Cols][kSlots];
@@ -96,7 +103,7 @@ __device__ inline void q4_columns(const Q4Mat& m, int n_blocks, int col0, Q4Act<
     const int col = min(col0 + c, m.n - 1);
 #pragma unroll
     for (int j = 0; j < kSlots; ++j) {
-      const int blk = min(lane + 64 * j, n_blocks - 1);
+      const int blk = min(first + lane + 64 * j, end - 1);
       idx[c][j] = (int64_t)col * n_blocks + blk;
       qv[c][j] = *reinterpret_cast<const uint4*>(m.quant + idx[c][j] * 16);
       sc[c][j] = m.scales[idx[c][j]];
@@ -127,24 +134,64 @@ __device__ inline void q4_columns(const Q4Mat& m, int n_blocks, int col0, Q4Act<
       }
       const float z = (float)((idx[c][j] & 1) ? (zb[c][j] >> 4) : (zb[c][j] & 15u));
       const float blk_sum = sc[c][j] * fmaf(-z, a.sum[j], d);
-      acc += lane + 64 * j < n_blocks ? blk_sum : 0.f;
+      acc += first + lane + 64 * j < end ? blk_sum : 0.f;
     }
     out[c] = sum64(acc);
   }
 }
 
-template <int kSlots, int kEpi>
+// kSplit wavefronts share a group of 4 columns, each taking 1/kSplit of
+// the blocks; their sums are added through LDS in part order.
+template <int kSplit> struct Q4Part {
+  static constexpr int kGroups = kQ4Waves / kSplit;  // column groups per workgroup
+  static constexpr int kWgCols = kGroups * kQ4Cols;
+  int col0, first, end, part;
+  __device__ Q4Part(int n_blocks) {
+    const int w = threadIdx.x >> 6;
+    part = w % kSplit;
+    col0 = (blockIdx.x * kGroups + w / kSplit) * kQ4Cols;
+    const int per = (n_blocks + kSplit - 1) / kSplit;
+    first = min(part * per, n_blocks - 1);
+    end = min(part * per + per, n_blocks);
+  }
+  // Adds the parts' sums into part 0's lane 0; true on that lane.
+  __device__ bool reduce(float (&r)[kQ4Cols]) {
+    if constexpr (kSplit == 1) {
+      return (threadIdx.x & 63) == 0;
+    } else {
+      __shared__ float sums[kQ4Waves][kQ4Cols];
+      const int w = threadIdx.x >> 6;
+      if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int c = 0; c < kQ4Cols; ++c) sums[w][c] = r[c];
+      }
+      __syncthreads();
+      if (part != 0 || (threadIdx.x & 63) != 0) return false;
+#pragma unroll
+      for (int c = 0; c < kQ4Cols; ++c) {
+        float v = sums[w][c];
+#pragma unroll
+        for (int p = 1; p < kSplit; ++p) v += sums[w + p][c];
+        r[c] = v;
+      }
+      return true;
+    }
+  }
+};
+
+template <int kSlots, int kSplit, int kEpi>
 __global__ __launch_bounds__(kQ4Threads) void q4_gemv_kernel(const float* __restrict__ x,
                                                              const Q4Mat m, int n_blocks,
                                                              float* __restrict__ y) {
   const int b = blockIdx.y;
-  const int col0 = blockIdx.x * kQ4WgCols + (threadIdx.x >> 6) * kQ4Cols;
-  if (col0 >= m.n) return;  // whole wavefront
+  Q4Part<kSplit> pt(n_blocks);
+  const int col0 = pt.col0;
+  if (kSplit == 1 && col0 >= m.n) return;  // whole wavefront (no barrier follows)
   Q4Act<kSlots> a;
-  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, n_blocks, a);
+  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, pt.first, pt.end, a);
   float r[kQ4Cols];
-  q4_columns<kSlots>(m, n_blocks, col0, a, r);
-  if ((threadIdx.x & 63) != 0) return;
+  q4_columns<kSlots>(m, n_blocks, pt.first, pt.end, col0, a, r);
+  if (!pt.reduce(r) || col0 >= m.n) return;
   float* yb = y + (int64_t)b * m.n;
   float prev[kQ4Cols];
   if constexpr (kEpi == kQ4Accumulate) {
@@ -178,9 +225,9 @@ __global__ __launch_bounds__(kQ4Threads) void q4_argmax_kernel(
   const int b = blockIdx.y;
   const int col0 = blockIdx.x * kQ4WgCols + (threadIdx.x >> 6) * kQ4Cols;
   Q4Act<kSlots> a;
-  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, n_blocks, a);
+  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, 0, n_blocks, a);
   float r[kQ4Cols];
-  q4_columns<kSlots>(m, n_blocks, col0, a, r);
+  q4_columns<kSlots>(m, n_blocks, 0, n_blocks, col0, a, r);
   if ((threadIdx.x & 63) == 0) {
     const ArgmaxShape s = argmax_shape(m.n);
     unsigned long long e = 0ull;
@@ -336,13 +383,14 @@ __global__ __launch_bounds__(kQ4wThreads, 2) void q4w_argmax_kernel(
 // Columns [0, Nq) are q, [Nq, Nq + Nkv) k, [Nq + Nkv, Nq + 2 Nkv) v; every
 // range is a multiple of 128 (whole heads), so a workgroup's 16 columns lie
 // in one of them.
-template <int kSlots, bool kQ16>
+template <int kSlots, int kSplit, bool kQ16>
 __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
     const float* __restrict__ x, const Q4Mat mq, const Q4Mat mk, const Q4Mat mv, int n_blocks,
     void* __restrict__ q_out, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
     const int32_t* __restrict__ pos, int n_kv, int cap, int* __restrict__ status) {
   const int b = blockIdx.y;
-  int col0 = blockIdx.x * kQ4WgCols + (threadIdx.x >> 6) * kQ4Cols;
+  Q4Part<kSplit> pt(n_blocks);
+  int col0 = pt.col0;
   int which = 0;
   if (col0 >= mq.n) {
     col0 -= mq.n;
@@ -354,10 +402,10 @@ __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
   }
   const Q4Mat& m = which == 0 ? mq : (which == 1 ? mk : mv);
   Q4Act<kSlots> a;
-  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, n_blocks, a);
+  q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, pt.first, pt.end, a);
   float r[kQ4Cols];
-  q4_columns<kSlots>(m, n_blocks, col0, a, r);
-  if ((threadIdx.x & 63) != 0) return;
+  q4_columns<kSlots>(m, n_blocks, pt.first, pt.end, col0, a, r);
+  if (!pt.reduce(r)) return;
   if (which == 0) {
     const int64_t at = (int64_t)b * mq.n + col0;
     if constexpr (kQ16) {
@@ -398,51 +446,84 @@ int q4w_iters(int n_blocks) {
   return 0;
 }
 
-template <int kSlots>
+template <int kSlots, int kSplit>
 hipError_t launch_gemv_slots(const float* x, const Q4Mat& w, int n_blocks, float* y, int batch,
                              int epilogue, hipStream_t stream) {
-  const dim3 grid((w.n + kQ4WgCols - 1) / kQ4WgCols, batch);
+  constexpr int kCols = Q4Part<kSplit>::kWgCols;
+  const dim3 grid((w.n + kCols - 1) / kCols, batch);
   switch (epilogue) {
     case kQ4None:
-      q4_gemv_kernel<kSlots, kQ4None><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
+      q4_gemv_kernel<kSlots, kSplit, kQ4None><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
       break;
     case kQ4Relu2:
-      q4_gemv_kernel<kSlots, kQ4Relu2><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
+      q4_gemv_kernel<kSlots, kSplit, kQ4Relu2><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
       break;
     default:
-      q4_gemv_kernel<kSlots, kQ4Accumulate><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
+      q4_gemv_kernel<kSlots, kSplit, kQ4Accumulate><<<grid, kQ4Threads, 0, stream>>>(x, w, n_blocks, y);
       break;
   }
   return hipGetLastError();
 }
 
-template <int kSlots>
+// Waves per column group: enough that each takes at least 32 blocks.
+int q4_split(int n_blocks) {
+#ifdef Q4_SPLIT
+  return Q4_SPLIT;
+#endif
+  return n_blocks >= 128 ? 4 : (n_blocks >= 64 ? 2 : 1);
+}
+
+template <int kSlots, int kSplit>
 hipError_t launch_qkv_slots(const Shape& s, const float* x, const Q4Mat& wq, const Q4Mat& wk,
                             const Q4Mat& wv, int n_blocks, void* q_out, void* k_cache,
                             void* v_cache, const int32_t* pos, int batch, int* status,
                             hipStream_t stream) {
-  const dim3 grid((wq.n + wk.n + wv.n) / kQ4WgCols, batch);
+  const dim3 grid((wq.n + wk.n + wv.n) / Q4Part<kSplit>::kWgCols, batch);
   f16* kc = static_cast<f16*>(k_cache);
   f16* vc = static_cast<f16*>(v_cache);
   if (s.q16)
-    qkv_append_kernel<kSlots, true><<<grid, kQ4Threads, 0, stream>>>(
+    qkv_append_kernel<kSlots, kSplit, true><<<grid, kQ4Threads, 0, stream>>>(
         x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.cap, status);
   else
-    qkv_append_kernel<kSlots, false><<<grid, kQ4Threads, 0, stream>>>(
+    qkv_append_kernel<kSlots, kSplit, false><<<grid, kQ4Threads, 0, stream>>>(
         x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.cap, status);
   return hipGetLastError();
+}
+
+template <int kSplit>
+hipError_t launch_qkv_split(const Shape& s, const float* x, const Q4Mat& wq, const Q4Mat& wk,
+                            const Q4Mat& wv, int n_blocks, void* q_out, void* k_cache,
+                            void* v_cache, const int32_t* pos, int batch, int* status,
+                            hipStream_t stream) {
+  switch (q4_slots((n_blocks + kSplit - 1) / kSplit)) {
+    case 1: return launch_qkv_slots<1, kSplit>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    case 2: return launch_qkv_slots<2, kSplit>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    case 3: return launch_qkv_slots<3, kSplit>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    case 4: return launch_qkv_slots<4, kSplit>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int kSplit>
+hipError_t launch_gemv_split(const float* x, const Q4Mat& w, int n_blocks, float* y, int batch,
+                             int epilogue, hipStream_t stream) {
+  switch (q4_slots((n_blocks + kSplit - 1) / kSplit)) {
+    case 1: return launch_gemv_slots<1, kSplit>(x, w, n_blocks, y, batch, epilogue, stream);
+    case 2: return launch_gemv_slots<2, kSplit>(x, w, n_blocks, y, batch, epilogue, stream);
+    case 3: return launch_gemv_slots<3, kSplit>(x, w, n_blocks, y, batch, epilogue, stream);
+    case 4: return launch_gemv_slots<4, kSplit>(x, w, n_blocks, y, batch, epilogue, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace
 
 hipError_t launch_q4_gemv(const float* x, const Q4Mat& w, int n_blocks, float* y, int batch,
                           int epilogue, hipStream_t stream) {
-  switch (q4_slots(n_blocks)) {
-    case 1: return launch_gemv_slots<1>(x, w, n_blocks, y, batch, epilogue, stream);
-    case 2: return launch_gemv_slots<2>(x, w, n_blocks, y, batch, epilogue, stream);
-    case 3: return launch_gemv_slots<3>(x, w, n_blocks, y, batch, epilogue, stream);
-    case 4: return launch_gemv_slots<4>(x, w, n_blocks, y, batch, epilogue, stream);
-    default: return hipErrorInvalidValue;
+  switch (q4_split(n_blocks)) {
+    case 1: return launch_gemv_split<1>(x, w, n_blocks, y, batch, epilogue, stream);
+    case 2: return launch_gemv_split<2>(x, w, n_blocks, y, batch, epilogue, stream);
+    default: return launch_gemv_split<4>(x, w, n_blocks, y, batch, epilogue, stream);
   }
 }
 
@@ -485,12 +566,10 @@ hipError_t launch_qkv_append(const Shape& s, const float* x, const Q4Mat& wq, co
                              const Q4Mat& wv, int n_blocks, void* q_out, void* k_cache,
                              void* v_cache, const int32_t* pos, int batch, int* status,
                              hipStream_t stream) {
-  switch (q4_slots(n_blocks)) {
-    case 1: return launch_qkv_slots<1>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
-    case 2: return launch_qkv_slots<2>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
-    case 3: return launch_qkv_slots<3>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
-    case 4: return launch_qkv_slots<4>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
-    default: return hipErrorInvalidValue;
+  switch (q4_split(n_blocks)) {
+    case 1: return launch_qkv_split<1>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    case 2: return launch_qkv_split<2>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
+    default: return launch_qkv_split<4>(s, x, wq, wk, wv, n_blocks, q_out, k_cache, v_cache, pos, batch, status, stream);
   }
 }
 
