@@ -61,6 +61,9 @@ def _ctx(H=32, Hkv=8, cap=64, B=1, q="f32"):
     (37, 3, 2),       # ragged column tail, one slot
     (20, 256, 3),     # K = 8192, four slots
     (64, 65, 1),      # 65 blocks: lane 0 holds two
+    (53, 70, 1),      # K split over 2 wavefronts, ragged column tail
+    (37, 130, 2),     # K split over 4 wavefronts (33 + 33 + 33 + 31 blocks), ragged tail
+    (24, 64, 1),      # 2 parts of exactly 32 blocks
 ])
 def test_gemv_matches_float64(n, n_blocks, batch):
     say(f"q4_gemv n={n} n_blocks={n_blocks} batch={batch}")
