@@ -9,6 +9,12 @@
 //   dispatchWorkgroups of kv_append / sparse_attn
 //     (engine/runtime.js:389-391)                  -> kvAppend / decode /
 //                                                      appendDecode / prefill
+// All library calls run on one stream the addon owns (a blocking stream, so
+// the synchronous upload / download / zero, which use the null stream, are
+// ordered with it). captureBegin / captureEnd record the calls in between
+// into a HIP graph that graphLaunch replays with one call: the counterpart of
+// the reference's cached op list, built once and submitted every token
+// (engine/runtime.js:385-429).
 // Device addresses cross into JavaScript as BigInt so the host can offset
 // into a buffer (one position entry per step) the way the reference offsets
 // uniform writes. Every failing call throws an Error naming the operation
@@ -24,6 +30,14 @@
 #include "nwd_attn.h"
 
 namespace {
+
+hipStream_t g_stream = nullptr;
+
+// The addon's stream, created on first use.
+hipStream_t stream() {
+  if (!g_stream && hipStreamCreate(&g_stream) != hipSuccess) g_stream = nullptr;
+  return g_stream;
+}
 
 napi_value throw_error(napi_env env, const std::string& msg) {
   napi_throw_error(env, nullptr, msg.c_str());
@@ -211,6 +225,21 @@ napi_value Upload(napi_env env, napi_callback_info info) {
   return make_i32(env, 0);
 }
 
+// setI32(devPtr, value): stream-ordered write of one int32 (the position
+// before a step, as the reference's queue.writeBuffer of its uniforms,
+// engine/runtime.js:451-452); does not wait for the device.
+napi_value SetI32(napi_env env, napi_callback_info info) {
+  napi_value argv[2];
+  get_args(env, info, 2, argv);
+  void* dst = nullptr;
+  int32_t v = 0;
+  if (!get_ptr(env, argv[0], &dst) || !dst || napi_get_value_int32(env, argv[1], &v) != napi_ok)
+    return throw_error(env, "setI32: expected (devicePtr, int32)");
+  hipError_t e = hipMemsetD32Async(dst, v, 1, stream());
+  if (e != hipSuccess) return throw_error(env, std::string("setI32: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
 // download(typedArray, devPtr): synchronous device -> host copy
 napi_value Download(napi_env env, napi_callback_info info) {
   napi_value argv[2];
@@ -263,7 +292,7 @@ napi_value KvAppend(napi_env env, napi_callback_info info) {
       !get_i32(env, a[7], &n, 1))
     return throw_error(env, "kvAppend: bad arguments");
   return check(env, ctx, "kvAppend",
-               nwd_kv_append(ctx, kn, vn, kc, vc, static_cast<const int32_t*>(pos), batch, n, nullptr));
+               nwd_kv_append(ctx, kn, vn, kc, vc, static_cast<const int32_t*>(pos), batch, n, stream()));
 }
 
 // decode(ctx, q, kCache, vCache, pos, out, batch, maxLen)
@@ -279,7 +308,7 @@ napi_value Decode(napi_env env, napi_callback_info info) {
     return throw_error(env, "decode: bad arguments");
   return check(env, ctx, "decode",
                nwd_decode_attn(ctx, q, kc, vc, static_cast<const int32_t*>(pos), out, batch,
-                               max_len, nullptr));
+                               max_len, stream()));
 }
 
 // appendDecode(ctx, q, kNew, vNew, kCache, vCache, pos, out, batch, maxLen)
@@ -295,7 +324,7 @@ napi_value AppendDecode(napi_env env, napi_callback_info info) {
     return throw_error(env, "appendDecode: bad arguments");
   return check(env, ctx, "appendDecode",
                nwd_append_decode(ctx, q, kn, vn, kc, vc, static_cast<const int32_t*>(pos), out,
-                                 batch, max_len, nullptr));
+                                 batch, max_len, stream()));
 }
 
 // prefill(ctx, q, kCache, vCache, pos0, out, batch, nNew, maxLen)
@@ -311,7 +340,7 @@ napi_value Prefill(napi_env env, napi_callback_info info) {
     return throw_error(env, "prefill: bad arguments");
   return check(env, ctx, "prefill",
                nwd_prefill_attn(ctx, q, kc, vc, static_cast<const int32_t*>(pos), out, batch,
-                                n_new, max_len, nullptr));
+                                n_new, max_len, stream()));
 }
 
 // {quant, scales, zp: BigInt device addresses, n, nBlocks} -> nwd_q4_weight
@@ -349,7 +378,7 @@ napi_value Q4Gemv(napi_env env, napi_callback_info info) {
     return throw_error(env, "q4Gemv: bad arguments");
   return check(env, ctx, "q4Gemv",
                nwd_q4_gemv(ctx, static_cast<const float*>(x), &w, static_cast<float*>(y), batch,
-                           epi, nullptr));
+                           epi, stream()));
 }
 
 // qkvAppend(ctx, x, wq, wk, wv, qOut, kCache, vCache, pos, batch): the q/k/v
@@ -367,7 +396,7 @@ napi_value QkvAppend(napi_env env, napi_callback_info info) {
     return throw_error(env, "qkvAppend: bad arguments");
   return check(env, ctx, "qkvAppend",
                nwd_qkv_append(ctx, static_cast<const float*>(x), &wq, &wk, &wv, q, kc, vc,
-                              static_cast<const int32_t*>(pos), batch, nullptr));
+                              static_cast<const int32_t*>(pos), batch, stream()));
 }
 
 // argmax(ctx, x, n, out, batch): argmax_partial + argmax_merge
@@ -382,7 +411,7 @@ napi_value Argmax(napi_env env, napi_callback_info info) {
     return throw_error(env, "argmax: bad arguments");
   return check(env, ctx, "argmax",
                nwd_argmax(ctx, static_cast<const float*>(x), n, static_cast<uint32_t*>(out), batch,
-                          nullptr));
+                          stream()));
 }
 
 // lmHeadArgmax(ctx, h, w, logits (null for none), out, batch): lm-head, argmax0, argmax1
@@ -398,7 +427,7 @@ napi_value LmHeadArgmax(napi_env env, napi_callback_info info) {
     return throw_error(env, "lmHeadArgmax: bad arguments");
   return check(env, ctx, "lmHeadArgmax",
                nwd_lm_head_argmax(ctx, static_cast<const float*>(h), &w, static_cast<float*>(logits),
-                                  static_cast<uint32_t*>(out), batch, nullptr));
+                                  static_cast<uint32_t*>(out), batch, stream()));
 }
 
 // deviceStatus(ctx) -> 0, or throws with the position error
@@ -407,7 +436,49 @@ napi_value DeviceStatus(napi_env env, napi_callback_info info) {
   get_args(env, info, 1, a);
   nwd_ctx* ctx = get_ctx(env, a[0]);
   if (!ctx) return throw_error(env, "deviceStatus: ctx is null");
-  return check(env, ctx, "deviceStatus", nwd_device_status(ctx, nullptr));
+  return check(env, ctx, "deviceStatus", nwd_device_status(ctx, stream()));
+}
+
+// captureBegin(): the library calls that follow are recorded, not run.
+napi_value CaptureBegin(napi_env env, napi_callback_info) {
+  hipStream_t s = stream();
+  hipError_t e = s ? hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal) : hipErrorInvalidValue;
+  if (e != hipSuccess) return throw_error(env, std::string("captureBegin: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+// captureEnd() -> graph handle (BigInt) of the calls recorded since captureBegin
+napi_value CaptureEnd(napi_env env, napi_callback_info) {
+  hipGraph_t g = nullptr;
+  hipGraphExec_t x = nullptr;
+  hipError_t e = hipStreamEndCapture(stream(), &g);
+  if (e == hipSuccess) e = hipGraphInstantiate(&x, g, nullptr, nullptr, 0);
+  if (g) (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return throw_error(env, std::string("captureEnd: ") + hipGetErrorString(e));
+  napi_value r;
+  napi_create_bigint_uint64(env, static_cast<uint64_t>(reinterpret_cast<uintptr_t>(x)), &r);
+  return r;
+}
+
+// graphLaunch(handle): replays a captured graph on the addon's stream
+napi_value GraphLaunch(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  void* h = nullptr;
+  if (!get_ptr(env, argv[0], &h) || !h) return throw_error(env, "graphLaunch: expected (graph)");
+  hipError_t e = hipGraphLaunch(static_cast<hipGraphExec_t>(h), stream());
+  if (e != hipSuccess) return throw_error(env, std::string("graphLaunch: ") + hipGetErrorString(e));
+  return make_i32(env, 0);
+}
+
+// graphDestroy(handle)
+napi_value GraphDestroy(napi_env env, napi_callback_info info) {
+  napi_value argv[1];
+  get_args(env, info, 1, argv);
+  void* h = nullptr;
+  if (!get_ptr(env, argv[0], &h)) return throw_error(env, "graphDestroy: expected (graph)");
+  if (h) (void)hipGraphExecDestroy(static_cast<hipGraphExec_t>(h));
+  return make_i32(env, 0);
 }
 
 napi_value Init(napi_env env, napi_value exports) {
@@ -420,6 +491,11 @@ napi_value Init(napi_env env, napi_value exports) {
       {"upload", nullptr, Upload, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"download", nullptr, Download, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"zero", nullptr, Zero, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"setI32", nullptr, SetI32, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"captureBegin", nullptr, CaptureBegin, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"captureEnd", nullptr, CaptureEnd, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphLaunch", nullptr, GraphLaunch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
+      {"graphDestroy", nullptr, GraphDestroy, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sync", nullptr, Sync, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"kvAppend", nullptr, KvAppend, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"decode", nullptr, Decode, nullptr, nullptr, nullptr, napi_enumerable, nullptr},

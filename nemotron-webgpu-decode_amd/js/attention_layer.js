@@ -57,6 +57,7 @@ class AttentionSlice {
     this.pos = addon.malloc(4);
     this.weights = new Map();  // layer -> {q, k, v, o} nwd_q4_weight descriptors
     this.owned = [];           // device buffers uploadQ4 allocated
+    this.graphs = [];          // token graphs captureToken made
     this.seq = 0;
     this.reset();
   }
@@ -84,14 +85,37 @@ class AttentionSlice {
   // runtime.js:386-393 for attention layer i: hNorm (f32 [hidden], device) ->
   // q / k / v projections with k / v written into the caches, attention, and
   // o_proj added into the residual stream h (f32 [hidden], device).
-  encodeLayerFromHidden(i, hNorm, h) {
+  // maxLen bounds the keys attended (default: this token's seq + 1).
+  encodeLayerFromHidden(i, hNorm, h, maxLen = this.seq + 1) {
     const w = this.weights.get(i);
     if (!w) throw new Error(`layer ${i} has no weights (setLayerWeights)`);
     addon.qkvAppend(this.ctx, hNorm, w.q, w.k, w.v, this.q, this.kCache.get(i), this.vCache.get(i),
                     this.pos, 1);
     addon.decode(this.ctx, this.q, this.kCache.get(i), this.vCache.get(i), this.pos, this.attnO, 1,
-                 this.seq + 1);
+                 maxLen);
     addon.q4Gemv(this.ctx, this.attnO, w.o, h, 1, Q4_ACCUMULATE);
+  }
+
+  // The reference builds its op list once and submits it every token
+  // (engine/runtime.js:385-429). Here one token's attention layers
+  // (encodeLayerFromHidden for every layer, in order) are captured once into
+  // a HIP graph; runToken replays it between beginStep and endStep with one
+  // call. The position is read from the device at replay, and attention is
+  // sized for the whole capacity (maxSeq), so one graph serves every token.
+  captureToken(hNorm, h) {
+    addon.captureBegin();
+    let graph = null;
+    try {
+      for (const i of this.layers) this.encodeLayerFromHidden(i, hNorm, h, this.maxSeq);
+    } finally {
+      graph = addon.captureEnd();
+    }
+    this.graphs.push(graph);
+    return graph;
+  }
+
+  runToken(graph) {
+    addon.graphLaunch(graph);
   }
 
   // runtime.js:615-633 (the KV part of reset)
@@ -104,9 +128,10 @@ class AttentionSlice {
   }
 
   // runtime.js:448,451-452: guard and position write before the token's ops
+  // (stream-ordered, without waiting for the device, as writeBuffer)
   beginStep() {
     if (this.seq >= this.maxSeq) throw new Error(`seq ${this.seq} exceeds maxSeq ${this.maxSeq}`);
-    addon.upload(this.pos, new Int32Array([this.seq]));
+    addon.setI32(this.pos, this.seq);
   }
 
   // What the q/k/v GEMVs of a layer write (runtime.js:386-388, outputs :120-122).
@@ -143,6 +168,7 @@ class AttentionSlice {
   }
 
   destroy() {
+    for (const g of this.graphs) addon.graphDestroy(g);
     for (const p of [this.q, this.k, this.v, this.attnO, this.pos, ...this.owned]) addon.free(p);
     for (const i of this.layers) {
       addon.free(this.kCache.get(i));

@@ -48,6 +48,7 @@ function main() {
   const outDir = process.argv[2];
   const hidden = Number(process.argv[3] || 512);
   const tokens = Number(process.argv[4] || 12);
+  const useGraph = process.argv[5] === 'graph';  // replay one captured token graph
   const heads = 40;
   const kvHeads = 8;
   const headDim = 128;
@@ -67,6 +68,7 @@ function main() {
 
   const hNormDev = addon.malloc(hidden * 4);
   const hDev = addon.malloc(hidden * 4);
+  const graph = useGraph ? slice.captureToken(hNormDev, hDev) : null;
   const outs = { hnorm: [], hin: [], attn: [], hout: [] };
   for (let t = 0; t < tokens; t++) {
     const hNorm = normals(rand, hidden);
@@ -74,7 +76,8 @@ function main() {
     addon.upload(hNormDev, hNorm);
     addon.upload(hDev, hIn);
     slice.beginStep();
-    slice.encodeLayerFromHidden(layer, hNormDev, hDev);
+    if (graph) slice.runToken(graph);
+    else slice.encodeLayerFromHidden(layer, hNormDev, hDev);
     slice.endStep();
     const hOut = new Float32Array(hidden);
     addon.download(hOut, hDev);
@@ -94,7 +97,7 @@ function main() {
     fs.writeFileSync(path.join(outDir, `w${name}.zp`), bytes(w.zp));
   }
   fs.writeFileSync(path.join(outDir, 'manifest.json'), JSON.stringify({
-    heads, kvHeads, headDim, hidden, tokens,
+    heads, kvHeads, headDim, hidden, tokens, graph: useGraph,
   }));
   addon.free(hNormDev);
   addon.free(hDev);

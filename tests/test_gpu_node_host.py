@@ -54,17 +54,20 @@ def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq):
         assert "exceeds maxSeq" in man["guard"]
 
 
-def test_node_host_full_layer_from_hidden_state(tmp_path):
+@pytest.mark.parametrize("mode", ["eager", "graph"])
+def test_node_host_full_layer_from_hidden_state(tmp_path, mode):
     """js/check_layer.js: one attention layer per token from the normalised
     hidden state (q/k/v projections + kv_append, attention, o_proj + residual
     add, engine/runtime.js:386-393) with 4-bit weights. Checked stage by
     stage against the oracle: the attention output against the chain q4 GEMV
     -> fp16 cache -> sparse_attn restatement (2e-3), and the residual against
     h_in + o_proj(attention output) in float64 (1e-6 of sum |w a|, plus one
-    f32 rounding of the add)."""
+    f32 rounding of the add). `graph`: the token's calls are captured once
+    into a HIP graph and replayed every token (AttentionSlice.captureToken,
+    attention sized for the capacity)."""
     out = tmp_path / "layer"
-    print("node check_layer hidden=512 tokens=12", flush=True)
-    res = subprocess.run(["node", str(JS / "check_layer.js"), str(out), "512", "12"],
+    print(f"node check_layer hidden=512 tokens=12 {mode}", flush=True)
+    res = subprocess.run(["node", str(JS / "check_layer.js"), str(out), "512", "12", mode],
                          capture_output=True, text=True, timeout=180)
     assert res.returncode == 0, res.stdout + res.stderr
     man = json.loads((out / "manifest.json").read_text())

@@ -26,7 +26,8 @@ def test_addon_exports():
     names = set(json.loads(out))
     assert {"create", "destroy", "cacheBytes", "malloc", "free", "upload", "download", "zero",
             "sync", "kvAppend", "decode", "appendDecode", "prefill", "deviceStatus",
-            "q4Gemv", "qkvAppend", "argmax", "lmHeadArgmax"} <= names
+            "q4Gemv", "qkvAppend", "argmax", "lmHeadArgmax", "setI32", "captureBegin",
+            "captureEnd", "graphLaunch", "graphDestroy"} <= names
 
 
 def test_create_errors_are_thrown_with_the_library_message():
@@ -60,7 +61,7 @@ def test_js_module_parses():
     res = subprocess.run(["node", "--check", str(JS / "check_attention.js")], capture_output=True,
                          text=True, timeout=60)
     assert res.returncode == 0, res.stderr
-    for script in ("check_layer.js", "check_head.js"):
+    for script in ("check_layer.js", "check_head.js", "bench_layer.js"):
         res = subprocess.run(["node", "--check", str(JS / script)], capture_output=True,
                              text=True, timeout=60)
         assert res.returncode == 0, res.stderr
