@@ -140,6 +140,12 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   int64_t at_batch = (int64_t)group * 2 * kTargetWorkgroups;
   if ((int64_t)d->max_batch * d->n_heads > at_batch) at_batch = (int64_t)d->max_batch * d->n_heads;
   ctx->ws.records = per_seq > at_batch ? per_seq : at_batch;
+  // Prefill splits a row tile's keys only while its row tiles underfill the
+  // chip (< 256 tiles of 128 rows), so 2 * 256 * 128 records always suffice;
+  // no more than the rows a call can have, times 2 splits.
+  int64_t prefill = (int64_t)2 * d->max_seq * d->n_heads * d->max_batch;
+  if (prefill > (int64_t)2 * kTargetWorkgroups * 128) prefill = (int64_t)2 * kTargetWorkgroups * 128;
+  if (prefill > ctx->ws.records) ctx->ws.records = prefill;
   ctx->ws.part_o = nullptr;
   ctx->ws.part_ml = nullptr;
   ctx->ws.status = nullptr;

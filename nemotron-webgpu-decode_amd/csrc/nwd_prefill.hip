@@ -8,12 +8,15 @@
 //
 // GQA packing: for one KV head the G query heads of the group and the n_new
 // queries form n_new*G rows (row R = query R/G, head R%G) that all share the
-// same K/V stream. A workgroup (8 wavefronts) owns 64 consecutive rows and
-// walks 128-key tiles. Wavefront w computes row group w%2 (32 rows, two
-// 16-row MFMA blocks) against key quarter w/2 (32 keys) of each tile: every
-// K/V fragment read from LDS feeds two MFMAs, which halves LDS traffic per
-// flop against 16-row waves, and two wavefronts share each SIMD so the
-// matrix cores always have a second wavefront to issue from.
+// same K/V stream. A workgroup (8 wavefronts) owns 128 consecutive rows and
+// walks 128-key tiles. Wavefront w computes row group w%4 (32 rows, two
+// 16-row MFMA blocks) against key half w/4 (64 keys) of each tile, as one
+// 64-key online-softmax step: every K/V fragment read from LDS feeds two
+// MFMAs, and two wavefronts share each SIMD. 128 rows per workgroup halve
+// the K/V staging per flop against 64 (one tile copy serves twice the rows);
+// the 64-key step gives each wavefront 8 independent QK^T accumulator chains
+// and one max / rescale per 64 keys (85 us against 103 us for 64-row
+// workgroups with 32-key steps, config 5).
 //   - K and V rows go from memory straight into LDS (buffer_load_dwordx4
 //     with the lds flag, gfx950: one instruction writes 1 KB, lane l's 16
 //     bytes at +16l), double-buffered: the next tile's copies land while the
@@ -27,15 +30,20 @@
 //   - causal mask only on tiles that cross a row's limit; online softmax in
 //     log2 units with the scale folded into the exp2 argument (one FMA per
 //     score), the row sum taken over the fp16 weights the PV product uses
-//     (v_dot2 with ones, two weights per instruction); O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
-//     registers from the S^T accumulators with no data movement between
-//     lanes, and V^T is read from the row-major V tile with two
-//     ds_read_b64_tr_b16 transpose loads per operand (gfx950): within a
-//     16-lane group, output lane j element e comes from position j%4 of the
-//     8 bytes lane 4e + j/4 addresses, so lanes 4e..4e+3 addressing 16
-//     consecutive dims of key row e give lane j V[key_e][d0 + j];
-//   - the four key quarters of a row group are merged through LDS at the
-//     end; accumulation is fp32 throughout and O is normalised once.
+//     (v_dot2 with ones, two weights per instruction); O^T += V^T P^T on the
+//     same MFMA, where P^T (fp16) is built in registers from the S^T
+//     accumulators with no data movement between lanes, and V^T is read from
+//     the row-major V tile with two ds_read_b64_tr_b16 transpose loads per
+//     operand (gfx950): within a 16-lane group, output lane j element e comes
+//     from position j%4 of the 8 bytes lane 4e + j/4 addresses, so lanes
+//     4e..4e+3 addressing 16 consecutive dims of key row e give lane j
+//     V[key_e][d0 + j];
+//   - the two key halves of a row group are merged through LDS at the end;
+//     accumulation is fp32 throughout.
+// With fewer than 256 row tiles, each row tile's key range is split over
+// nsplit workgroups (the decode kernel's split-K): they write (max, sum,
+// o[128]) records to the context's workspace, and prefill_merge_kernel
+// combines them; with one split the workgroup writes O directly.
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
@@ -43,11 +51,13 @@ namespace nwd {
 
 constexpr int kPWaves = 8;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPBM = 64;                    // rows per workgroup
+constexpr int kPBM = 128;                   // rows per workgroup
 constexpr int kPBN = 128;                   // keys per tile
+constexpr int kRB = 2;                      // 16-row MFMA blocks per wavefront
+constexpr int kKB = 4;                      // 16-key blocks per wavefront per tile
 constexpr int kRowBytes = kHeadDim * 2;     // 256: K/V rows are unpadded in LDS
 constexpr int kTileBytes = kPBN * kRowBytes;  // 32 KB
-constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per copy (4)
+constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per load (8)
 // Chunk swizzles (16 chunks of 16 bytes per row): physical chunk p of LDS
 // row r holds logical chunk p ^ kswz(r) of a K row, p ^ vswz(r) of a V row.
 // A K operand read (16 rows, one logical chunk) then covers 16 distinct
@@ -59,7 +69,6 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
-// Transpose load of 4 fp16 values (see the header comment for the lanes).
 __device__ inline f16x4 lds_read_tr16(const f16* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
   return __builtin_bit_cast(f16x4, v);
@@ -83,77 +92,94 @@ __device__ inline f16x8 load_q8(const void* q, int64_t elem) {
   }
 }
 
-// grid: one workgroup per (row tile, kv head, sequence), kv head fastest so
-// that the workgroups the dispatcher sends to one XCD share a KV head and its
-// K/V stream in that XCD's L2.
+template <bool kO16>
+__device__ inline void store_o4(void* out, int64_t at, f32x4 r) {
+  if constexpr (kO16) {
+    f16x4 h;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) h[e] = (f16)r[e];
+    *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = h;
+  } else {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = r;
+  }
+}
+
+struct PrefillArgs {
+  const void* q;
+  const f16* k_cache;
+  const f16* v_cache;
+  const int32_t* pos0;
+  void* out;
+  float* part_o;    // [rows][nsplit][D] (nsplit > 1)
+  float2* part_ml;  // [rows][nsplit] (max in log2 units, sum)
+  int n_heads, n_kv, cap, n_new, mtiles, nsplit;
+  float qk_scale_log2;
+  int* status;
+};
+
 template <int G, bool kQ16, bool kO16>
-__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
-    const void* __restrict__ q, const f16* __restrict__ k_cache,
-    const f16* __restrict__ v_cache, const int32_t* __restrict__ pos0,
-    void* __restrict__ out, int n_heads, int n_kv, int cap, int n_new,
-    int mtiles, float qk_scale_log2, int* __restrict__ status) {
-  constexpr int RB = 2;  // 16-row MFMA blocks per wavefront
+__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
   char* lds = reinterpret_cast<char*>(smem);  // K0 K1 V0 V1, 32 KB each
 
   const int id = blockIdx.x;
-  const int hkv = id % n_kv;
-  const int rest = id / n_kv;
-  const int mt = rest % mtiles;
-  const int b = rest / mtiles;
+  const int hkv = id % a.n_kv;
+  int rest = id / a.n_kv;
+  const int split = rest % a.nsplit;
+  rest /= a.nsplit;
+  const int mt = rest % a.mtiles;
+  const int b = rest / a.mtiles;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 15, lq = lane >> 4;
-  const int rg = wave & 1, kq = wave >> 1;  // row group (32 rows), key quarter (32 keys)
+  const int rh = wave & 3, kh = wave >> 2;  // row group (32 rows), key half (64 keys)
 
-  int P0 = pos0[b];
-  if (P0 < 0 || P0 > cap - n_new) {
-    if (tid == 0 && mt == 0 && hkv == 0) atomicOr(status, kStatusBadPos);
-    P0 = P0 < 0 ? 0 : cap - n_new;
+  int P0 = a.pos0[b];
+  if (P0 < 0 || P0 > a.cap - a.n_new) {
+    if (tid == 0 && mt == 0 && hkv == 0 && split == 0) atomicOr(a.status, kStatusBadPos);
+    P0 = P0 < 0 ? 0 : a.cap - a.n_new;
   }
-  const int total_rows = n_new * G;
+  const int total_rows = a.n_new * G;
   const int r_last = min(mt * kPBM + kPBM, total_rows) - 1;
-  const int kend = P0 + r_last / G + 1;  // keys this workgroup needs
-  const int ntiles = (kend + kPBN - 1) / kPBN;
+  const int kend = P0 + r_last / G + 1;  // keys this row tile needs
+  const int ntiles_all = (kend + kPBN - 1) / kPBN;
+  const int t0 = (int)((int64_t)split * ntiles_all / a.nsplit);
+  const int t1 = (int)((int64_t)(split + 1) * ntiles_all / a.nsplit);
+  const int kend_s = min(kend, t1 * kPBN);  // keys this split may load
 
-  // This wave's rows: R = mt*64 + rg*32 + rb*16 + lr. Query rows are the B
-  // operand of S^T = K Q^T: lane holds Q[row][db*32 + 8*lq .. +7].
-  const int r0 = mt * kPBM + rg * 32;
-  int qi[RB], gq[RB], lim[RB];
-  f16x8 qf[RB][4];
+  const int r0 = mt * kPBM + rh * 32;
+  int qi[kRB], gq[kRB], lim[kRB];
+  f16x8 qf[kRB][4];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < kRB; ++rb) {
     const int R = r0 + rb * 16 + lr;
     const bool ok = R < total_rows;
     qi[rb] = ok ? R / G : 0;
     gq[rb] = ok ? R - qi[rb] * G : 0;
-    lim[rb] = ok ? P0 + qi[rb] : -1;  // last key this row attends
-    const int64_t qrow = ((int64_t)(b * n_new + qi[rb]) * n_heads + hkv * G + gq[rb]) * kHeadDim;
+    lim[rb] = ok ? P0 + qi[rb] : -1;
+    const int64_t qrow = ((int64_t)(b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       if (ok) {
-        qf[rb][db] = load_q8<kQ16>(q, qrow + db * 32 + 8 * lq);
+        qf[rb][db] = load_q8<kQ16>(a.q, qrow + db * 32 + 8 * lq);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[rb][db][e] = (f16)0.f;
       }
     }
   }
-  // Keys at or below every row limit of this wave need no mask.
   const bool wave_has_pad = r0 + 31 >= total_rows;
   const int wave_min_lim = P0 + r0 / G;
 
-  const int64_t slab = (int64_t)(b * n_kv + hkv) * cap * kHeadDim;
-  const f16* kb_ptr = k_cache + slab;
-  const f16* vb_ptr = v_cache + slab;
-
-  const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(kb_ptr), 0,
-                                                    kend * (kHeadDim * 2), kBufferWord3);
-  const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(vb_ptr), 0,
-                                                    kend * (kHeadDim * 2), kBufferWord3);
-  // Wave w copies rows 16w .. 16w+15 of a tile, 4 rows (1 KB) per
-  // instruction: lane l fills physical chunk l & 15 of row 16w + 4i + l/16.
-  // Rows past kend read as zeros (buffer range check), so no LDS row is
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.k_cache + slab), 0,
+                                                    kend_s * (kHeadDim * 2), kBufferWord3);
+  const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.v_cache + slab), 0,
+                                                    kend_s * (kHeadDim * 2), kBufferWord3);
+  // Staging: wave w copies rows 16w .. 16w+15 of a tile, 4 rows (1 KB) per
+  // instruction: lane l fills physical chunk l & 15 of row 16w + 4i + l/16
+  // and so loads the logical chunk the swizzle puts there. Rows past the
+  // split's last key read as zeros (buffer range check), so no LDS row is
   // ever stale.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int st_row = 16 * wv + (lane >> 4), st_p = lane & 15;
@@ -172,72 +198,66 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
   };
   auto wait_tile = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
 
-  // Running max of the raw scores (log2 units after scaling) and sums.
-  float m[RB], lsum[RB];
-  f32x4 o[RB][8];
+  float m[kRB], lsum[kRB];
+  f32x4 o[kRB][8];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < kRB; ++rb) {
     m[rb] = kNegBig;
     lsum[rb] = 0.f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const float c = qk_scale_log2;
+  const float c = a.qk_scale_log2;
 
-  // Prologue: tile 0 into LDS, tile 1 in flight.
-  load_tile(0, 0);
-  wait_tile();
-  __syncthreads();
-  load_tile(1, 1);
-
-  for (int kt = 0; kt < ntiles; ++kt) {
-    const int buf = kt & 1;
-    const char* ks = lds + buf * kTileBytes + kq * 32 * kRowBytes;
-    const char* vs = lds + (2 + buf) * kTileBytes + kq * 32 * kRowBytes;
-    // transpose reads: lane 4e+c of a 16-lane group reads dims 4c..4c+3 (of
-    // each 16-dim block) of key row 4*lq + e (+16 for the second half of the
-    // operand); those dims are logical chunk 2*dblk + c/2, bytes 8*(c&1).
-    const int vr0 = 4 * lq + (lr >> 2);
-    auto vaddr = [&](int r, int dblk) {
-      return reinterpret_cast<const f16*>(vs + r * kRowBytes +
-                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz(r)) << 4) + 8 * (lr & 1));
-    };
-    const int k0 = kt * kPBN + kq * 32;
+  if (t1 > t0) {
+    load_tile(t0, 0);
+    wait_tile();
+    __syncthreads();
+    load_tile(t0 + 1, 1);
+  }
+  for (int kt = t0; kt < t1; ++kt) {
+    const int buf = (kt - t0) & 1;
+    const char* ks = lds + buf * kTileBytes + kh * 64 * kRowBytes;
+    const char* vs = lds + (2 + buf) * kTileBytes + kh * 64 * kRowBytes;
+    const int k0 = kt * kPBN + kh * 64;
 
     // st[kb][rb][e] = raw score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr)
-    f32x4 st[2][RB];
+    f32x4 st[kKB][kRB];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) st[kb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < kRB; ++rb) st[kb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
-                                                        (((4 * db + lq) ^ lr) << 4));
+      for (int kb = 0; kb < kKB; ++kb) {
+        const f16x8 k8 = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
+                                                         (((4 * db + lq) ^ lr) << 4));
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) st[kb][rb] = mfma16x16x32(a, qf[rb][db], st[kb][rb]);
+        for (int rb = 0; rb < kRB; ++rb) st[kb][rb] = mfma16x16x32(k8, qf[rb][db], st[kb][rb]);
       }
     }
-
-    if (wave_has_pad || k0 + 31 > wave_min_lim) {  // this tile crosses a row limit
+    if (wave_has_pad || k0 + 63 > wave_min_lim) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+      for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             if (k0 + kb * 16 + 4 * lq + e > lim[rb]) st[kb][rb][e] = -INFINITY;
     }
-
-    f16x8 pb[RB];
+    // P^T operands, two per row block: pb[rb][h] element e < 4 is key
+    // k0 + 32h + 4*lq + e, e >= 4 is key k0 + 32h + 16 + 4*lq + (e-4).
+    f16x8 pb[kRB][2];
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float mx = fmaxf(fmaxf(fmaxf(st[0][rb][0], st[0][rb][1]), fmaxf(st[0][rb][2], st[0][rb][3])),
-                       fmaxf(fmaxf(st[1][rb][0], st[1][rb][1]), fmaxf(st[1][rb][2], st[1][rb][3])));
+    for (int rb = 0; rb < kRB; ++rb) {
+      float mx = st[0][rb][0];
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][rb][e]);
       mx = max_xor32(max_xor16(mx));
-      if (mx > m[rb]) {  // rescale only when the running max moves
+      if (mx > m[rb]) {
         const float alpha = fast_exp2((m[rb] - mx) * c);
         lsum[rb] *= alpha;
 #pragma unroll
@@ -245,48 +265,52 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
         m[rb] = mx;
       }
       const float mc = m[rb] * c;
-      // P^T operand (32 keys): element e < 4 is key k0 + 4*lq + e, element
-      // e >= 4 is key k0 + 16 + 4*lq + (e-4); V^T is read in the same order.
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p = fast_exp2(fmaf(st[kb][rb][e], c, -mc));
-          pb[rb][kb * 4 + e] = (f16)p;
-        }
-      // the row sum of the fp16 weights the PV product uses
+        for (int e = 0; e < 4; ++e)
+          pb[rb][kb >> 1][(kb & 1) * 4 + e] = (f16)fast_exp2(fmaf(st[kb][rb][e], c, -mc));
 #pragma unroll
-      for (int e = 0; e < 8; e += 2)
-        lsum[rb] = dot2(f16x2{pb[rb][e], pb[rb][e + 1]}, f16x2{(f16)1.f, (f16)1.f}, lsum[rb]);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; e += 2)
+          lsum[rb] = dot2(f16x2{pb[rb][h][e], pb[rb][h][e + 1]}, f16x2{(f16)1.f, (f16)1.f}, lsum[rb]);
     }
-
+    const int vr0 = 4 * lq + (lr >> 2);
+    auto vaddr = [&](int r, int dblk) {
+      return reinterpret_cast<const f16*>(vs + r * kRowBytes +
+                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz(r)) << 4) + 8 * (lr & 1));
+    };
 #pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk) {
-      const f16x4 lo = lds_read_tr16(vaddr(vr0, dblk));
-      const f16x4 hi = lds_read_tr16(vaddr(16 + vr0, dblk));
-      const f16x8 a = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) o[rb][dblk] = mfma16x16x32(a, pb[rb], o[rb][dblk]);
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        const f16x4 lo = lds_read_tr16(vaddr(h * 32 + vr0, dblk));
+        const f16x4 hi = lds_read_tr16(vaddr(h * 32 + 16 + vr0, dblk));
+        const f16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) o[rb][dblk] = mfma16x16x32(v8, pb[rb][h], o[rb][dblk]);
+      }
     }
 
     wait_tile();      // this wave's part of tile kt+1 is in LDS
     __syncthreads();  // every part is, and every wave is done with tile kt
-    if (kt + 2 < ntiles) load_tile(kt + 2, buf);  // nothing lands in LDS after the loop
+    if (kt + 2 < t1) load_tile(kt + 2, buf);  // nothing lands in LDS after the loop
   }
 
-  // Row totals of this key quarter, then merge the quarters through LDS:
-  // quarters 1..3 publish (m, l, o); quarter 0 combines and writes O.
-  constexpr int kX = 2 + 32;  // floats per (rb) state: m, l, o[8][4]
-  float* xch = reinterpret_cast<float*>(smem);  // [3 quarters][2 row groups][64 lanes][RB][kX]
-  auto slot = [&](int qq, int rb) { return xch + ((((qq - 1) * 2 + rg) * 64 + lane) * RB + rb) * kX; };
+  // Merge the two key halves of each row group through LDS: wave (rh, 1)
+  // publishes (m, l, o); wave (rh, 0) combines and writes the output or
+  // this split's records.
+  constexpr int kX = 2 + 32;
+  float* xch = reinterpret_cast<float*>(smem);  // [4 row groups][64 lanes][kRB][kX]
+  auto slot = [&](int rb) { return xch + ((rh * 64 + lane) * kRB + rb) * kX; };
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    lsum[rb] = sum_xor32(sum_xor16(lsum[rb]));
-  }
-  if (kq > 0) {
+  for (int rb = 0; rb < kRB; ++rb) lsum[rb] = sum_xor32(sum_xor16(lsum[rb]));
+  __syncthreads();  // the last tile's LDS reads are done before xch is written
+  if (kh == 1) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      float* x = slot(kq, rb);
+    for (int rb = 0; rb < kRB; ++rb) {
+      float* x = slot(rb);
       x[0] = m[rb];
       x[1] = lsum[rb];
 #pragma unroll
@@ -296,67 +320,112 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(
     }
   }
   __syncthreads();
-  if (kq > 0) return;
+  if (kh == 1) return;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < kRB; ++rb) {
     const int R = r0 + rb * 16 + lr;
     if (R >= total_rows) continue;
-    float M = m[rb];
+    const float* x = slot(rb);
+    const float M = fmaxf(m[rb], x[0]);
+    const float a0 = fast_exp2((m[rb] - M) * c), a1 = fast_exp2((x[0] - M) * c);
+    const float lt = lsum[rb] * a0 + x[1] * a1;
+    const int64_t grow = (int64_t)(b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb];
+    if (a.nsplit == 1) {
+      const float inv = 1.f / lt;
 #pragma unroll
-    for (int qq = 1; qq < 4; ++qq) M = fmaxf(M, slot(qq, rb)[0]);
-    const float a0 = fast_exp2((m[rb] - M) * c);
-    float lt = lsum[rb] * a0;
-    float w[3];
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        f32x4 r = o[rb][dblk] * a0;
 #pragma unroll
-    for (int qq = 1; qq < 4; ++qq) {
-      w[qq - 1] = fast_exp2((slot(qq, rb)[0] - M) * c);
-      lt = fmaf(slot(qq, rb)[1], w[qq - 1], lt);
-    }
-    const float inv = 1.f / lt;
-    // o[rb][dblk][e] = O^T[d = dblk*16 + 4*lq + e][row R]
-    const int64_t orow = ((int64_t)(b * n_new + qi[rb]) * n_heads + hkv * G + gq[rb]) * kHeadDim;
-#pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk) {
-      f32x4 r = o[rb][dblk] * a0;
-#pragma unroll
-      for (int qq = 1; qq < 4; ++qq)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = fmaf(slot(qq, rb)[2 + dblk * 4 + e], w[qq - 1], r[e]);
-      r *= inv;
-      const int64_t at = orow + dblk * 16 + 4 * lq;
-      if constexpr (kO16) {
-        f16x4 h;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = (f16)r[e];
-        *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = h;
-      } else {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = r;
+        for (int e = 0; e < 4; ++e) r[e] = fmaf(x[2 + dblk * 4 + e], a1, r[e]);
+        store_o4<kO16>(a.out, grow * kHeadDim + dblk * 16 + 4 * lq, r * inv);
       }
+    } else {
+      const int64_t rec = grow * a.nsplit + split;
+#pragma unroll
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        f32x4 r = o[rb][dblk] * a0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = fmaf(x[2 + dblk * 4 + e], a1, r[e]);
+        *reinterpret_cast<f32x4*>(a.part_o + rec * kHeadDim + dblk * 16 + 4 * lq) = r;
+      }
+      if (lq == 0) a.part_ml[rec] = make_float2(M * c, lt);
     }
   }
 }
 
+// out[row] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); 32 threads per
+// row, 4 dims each.
+template <bool kO16>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
+                                                            const float2* __restrict__ part_ml,
+                                                            void* __restrict__ out, int64_t rows,
+                                                            int nsplit) {
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = t >> 5;
+  const int d4 = t & 31;
+  if (row >= rows) return;
+  float M = kNegBig;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[row * nsplit + s].x);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  float lt = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float2 ml = part_ml[row * nsplit + s];
+    const float w = fast_exp2(ml.x - M);
+    lt = fmaf(ml.y, w, lt);
+    acc += *reinterpret_cast<const f32x4*>(part_o + (row * nsplit + s) * kHeadDim + d4 * 4) * w;
+  }
+  store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / lt));
+}
+
 constexpr size_t kPrefillLds = (size_t)4 * kTileBytes;
-static_assert(kPrefillLds >= (size_t)3 * 2 * 64 * 2 * 34 * sizeof(float), "merge exchange fits");
+static_assert(kPrefillLds >= (size_t)4 * 64 * kRB * 34 * sizeof(float), "merge exchange fits");
 static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
+
+// Splits of each row tile's key range: enough workgroups to fill the chip
+// (256), at most 8, and as many as the workspace holds records for.
+static int prefill_splits(int64_t row_tiles, int64_t rows, const Workspace& ws) {
+  int n = (int)((256 + row_tiles - 1) / row_tiles);
+  if (n > 8) n = 8;
+  while (n > 1 && rows * n > ws.records) --n;
+  return n < 1 ? 1 : n;
+}
 
 template <int G, bool kQ16, bool kO16>
 static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
                                    const Workspace& ws, hipStream_t stream) {
   auto kern = prefill_kernel<G, kQ16, kO16>;
-  static bool attr_set = false;  // the dynamic LDS size exceeds the 64 KB default
+  static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  const int mtiles = (n_new * G + kPBM - 1) / kPBM;
-  const unsigned blocks = (unsigned)(mtiles * s.n_kv * batch);
-  kern<<<blocks, kPThreads, kPrefillLds, stream>>>(
-      q, static_cast<const f16*>(kc), static_cast<const f16*>(vc), pos0, out, s.n_heads, s.n_kv,
-      s.cap, n_new, mtiles, s.qk_scale * kLog2e, ws.status);
+  PrefillArgs a;
+  a.q = q;
+  a.k_cache = static_cast<const f16*>(kc);
+  a.v_cache = static_cast<const f16*>(vc);
+  a.pos0 = pos0;
+  a.out = out;
+  a.n_heads = s.n_heads;
+  a.n_kv = s.n_kv;
+  a.cap = s.cap;
+  a.n_new = n_new;
+  a.mtiles = (n_new * G + kPBM - 1) / kPBM;
+  a.qk_scale_log2 = s.qk_scale * kLog2e;
+  a.status = ws.status;
+  const int64_t row_tiles = (int64_t)a.mtiles * s.n_kv * batch;
+  const int64_t rows = (int64_t)n_new * s.n_heads * batch;
+  const int nsplit = prefill_splits(row_tiles, rows, ws);
+  a.nsplit = nsplit;
+  a.part_o = ws.part_o;
+  a.part_ml = ws.part_ml;
+  kern<<<(unsigned)(row_tiles * nsplit), kPThreads, kPrefillLds, stream>>>(a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || nsplit == 1) return e;
+  const unsigned blocks = (unsigned)((rows * 32 + 255) / 256);
+  prefill_merge_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows, nsplit);
   return hipGetLastError();
 }
 
