@@ -31,12 +31,15 @@
 
 namespace {
 
-hipStream_t g_stream = nullptr;
+constexpr int kMaxDevices = 64;
+hipStream_t g_streams[kMaxDevices] = {};
 
-// The addon's stream, created on first use.
+// The addon's stream on the current device, created on first use.
 hipStream_t stream() {
-  if (!g_stream && hipStreamCreate(&g_stream) != hipSuccess) g_stream = nullptr;
-  return g_stream;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (!g_streams[dev] && hipStreamCreate(&g_streams[dev]) != hipSuccess) g_streams[dev] = nullptr;
+  return g_streams[dev];
 }
 
 napi_value throw_error(napi_env env, const std::string& msg) {

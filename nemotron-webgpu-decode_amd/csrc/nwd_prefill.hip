@@ -44,6 +44,8 @@
 // nsplit workgroups (the decode kernel's split-K): they write (max, sum,
 // o[128]) records to the context's workspace, and prefill_merge_kernel
 // combines them; with one split the workgroup writes O directly.
+#include <atomic>
+
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
@@ -395,12 +397,18 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
                                    const int32_t* pos0, void* out, int batch, int n_new,
                                    const Workspace& ws, hipStream_t stream) {
   auto kern = prefill_kernel<G, kQ16, kO16>;
-  static bool attr_set = false;
-  if (!attr_set) {
+  // The dynamic LDS size exceeds the 64 KB default: raise the kernel's limit
+  // once per device (the attribute is per device).
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  hipError_t de = hipGetDevice(&dev);
+  if (de != hipSuccess) return de;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr_set.load() & bit)) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPrefillLds);
     if (e != hipSuccess) return e;
-    attr_set = true;
+    attr_set.fetch_or(bit);
   }
   PrefillArgs a;
   a.q = q;
