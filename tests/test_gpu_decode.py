@@ -412,3 +412,38 @@ def test_host_validation_rejects_before_launch():
         with pytest.raises(nw.NwdError) as e:
             ctx.decode(t, 0, t, p, t, 1)
         assert e.value.code == nw.NWD_ERR_INVALID
+
+
+@pytest.mark.parametrize("merge_separate", [True, False])
+def test_max_seq_last_position_fused_append(merge_separate):
+    """The largest supported capacity, max_seq = 2^22, one KV head (a 1 GiB
+    slab per cache): append a dominant key at position 2^22 - 1 and attend
+    over all 2^22 keys. Every other key is zero (score 0) with V = 0.25, so
+    the output is the appended V row up to a weight of 2^22 * exp(-40); the
+    appended rows must land bit-exactly at the end of the slab. The automatic
+    split count is at its maximum here, so the merge takes several passes."""
+    say(f"max_seq 2^22: fused append + decode at the last position, separate merge={merge_separate}")
+    cap = 1 << 22
+    H, Hkv = 4, 1
+    g = rng(4242)
+    u = g.standard_normal(D)
+    u /= np.linalg.norm(u)
+    q = np.tile(u, (1, H, 1)).astype(np.float32)
+    k_new = (40.0 * np.sqrt(D) * u).astype(np.float16)[None, None, :]     # score ~ 40 per query
+    v_new = g.standard_normal((1, 1, D)).astype(np.float16)
+    with nw.AttnContext(H, Hkv, cap, q_dtype="f32", o_dtype="f32") as ctx:
+        ctx.set_decode_merge(merge_separate)
+        kc = torch.zeros((1, Hkv, cap, D), dtype=torch.float16, device="cuda")
+        vc = torch.full((1, Hkv, cap, D), 0.25, dtype=torch.float16, device="cuda")
+        out = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+        ctx.append_decode(dev(q), dev(k_new), dev(v_new), kc, vc, pos_tensor([cap - 1]), out, 1)
+        assert ctx.device_status() == nw.NWD_OK
+        o = host(out)
+        np.testing.assert_array_equal(host(kc[0, 0, cap - 1]).view(np.uint16),
+                                      k_new[0, 0].view(np.uint16))
+        np.testing.assert_array_equal(host(vc[0, 0, cap - 1]).view(np.uint16),
+                                      v_new[0, 0].view(np.uint16))
+        assert host(kc[0, 0, cap - 2]).max() == 0 and host(vc[0, 0, cap - 2]).min() == np.float16(0.25)
+    want = v_new[0, 0].astype(np.float32)
+    for h in range(H):
+        assert max_abs(o[0, h], want) < 1e-4, h
