@@ -148,3 +148,35 @@ def test_prefill_matches_sequential_decode():
         torch.cuda.synchronize()
     stepwise = torch.stack(seq, dim=1).cpu().numpy()
     assert max_abs(out.cpu().numpy(), stepwise) < TOL
+
+
+def test_prefill_at_max_seq():
+    """A 64-token chunk appended at the end of the largest capacity (max_seq =
+    2^22, one KV head, 1 GiB slabs): each query attends ~2^22 keys, so every
+    row tile's key range is split (and merged) over several workgroups. Old
+    keys are zero (score 0) with V = 0.25; the new keys are a dominant
+    direction u (score 40 against every query), so query i averages the new
+    V rows 0..i up to a weight of 2^22 * exp(-40)."""
+    say("prefill 64 new tokens at the end of max_seq = 2^22")
+    cap, n_new, H, Hkv = 1 << 22, 64, 4, 1
+    p0 = cap - n_new
+    g = rng(4343)
+    u = g.standard_normal(D)
+    u /= np.linalg.norm(u)
+    q = np.tile(u, (1, n_new, H, 1)).astype(np.float16)
+    knew = np.tile((40.0 * np.sqrt(D) * u).astype(np.float16), (1, n_new, Hkv, 1))
+    vnew = g.standard_normal((1, n_new, Hkv, D)).astype(np.float16)
+    with nw.AttnContext(H, Hkv, cap) as ctx:
+        kc = torch.zeros((1, Hkv, cap, D), dtype=torch.float16, device="cuda")
+        vc = torch.full((1, Hkv, cap, D), 0.25, dtype=torch.float16, device="cuda")
+        pos = pos_tensor([p0])
+        ctx.kv_append(dev(knew), dev(vnew), kc, vc, pos, 1, n_new)
+        out = torch.empty((1, n_new, H, D), dtype=torch.float16, device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos, out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        o = out.float().cpu().numpy()
+    v = vnew[0, :, 0].astype(np.float64)
+    for i in range(n_new):
+        want = v[:i + 1].mean(axis=0)
+        for h in range(H):
+            assert max_abs(o[0, i, h], want) < 2e-3, (i, h)
