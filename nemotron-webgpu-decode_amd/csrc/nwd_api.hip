@@ -24,6 +24,7 @@ struct nwd_ctx {
   int device;
   int forced_splits;
   int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 default (separate)
+  int* status_host;    // pinned copy target of the device status word
   std::string err;
 };
 
@@ -155,6 +156,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->ws.part_ml = nullptr;
   ctx->ws.status = nullptr;
   ctx->ws.counters = nullptr;
+  ctx->status_host = nullptr;
   const size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
   e = hipMalloc(&ctx->ws.part_o, ctx->ws.records * nwd::kHeadDim * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
@@ -162,6 +164,8 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.status, sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.status, 0, sizeof(int));
+  // Pinned, so the per-step status read is one small DMA, not a staged copy.
+  if (e == hipSuccess) e = hipHostMalloc(reinterpret_cast<void**>(&ctx->status_host), sizeof(int));
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     nwd_destroy(ctx);
@@ -180,6 +184,7 @@ void nwd_destroy(nwd_ctx* ctx) {
   if (ctx->ws.part_ml) (void)hipFree(ctx->ws.part_ml);
   if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
   if (ctx->ws.status) (void)hipFree(ctx->ws.status);
+  if (ctx->status_host) (void)hipHostFree(ctx->status_host);
   if (prev >= 0) (void)hipSetDevice(prev);
   delete ctx;
 }
@@ -316,10 +321,10 @@ int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const voi
 int nwd_device_status(nwd_ctx* ctx, void* stream) {
   if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_device_status: ctx is NULL");
   hipStream_t s = (hipStream_t)stream;
-  int host = 0;
-  hipError_t e = hipMemcpyAsync(&host, ctx->ws.status, sizeof(int), hipMemcpyDeviceToHost, s);
+  hipError_t e = hipMemcpyAsync(ctx->status_host, ctx->ws.status, sizeof(int), hipMemcpyDeviceToHost, s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(ctx, "nwd_device_status", e);
+  const int host = *ctx->status_host;
   if (host == 0) return NWD_OK;
   e = hipMemsetAsync(ctx->ws.status, 0, sizeof(int), s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
