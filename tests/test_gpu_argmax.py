@@ -70,8 +70,10 @@ def test_argmax_special_values():
         assert got[b] == oracle.argmax_ref(x[b]), b
 
 
-@pytest.mark.parametrize("vocab,batch", [(8191, 2), (131072, 1)])
+@pytest.mark.parametrize("vocab,batch", [(8191, 2), (131072, 1), (20001, 3)])
 def test_lm_head_argmax(vocab, batch):
+    """8191: the per-slot GEMV form; 131072 and 20001 (>= 16384 columns) the
+    wide form, 20001 with a ragged last workgroup and three rows."""
     say(f"lm_head_argmax vocab={vocab} batch={batch}")
     g = rng(600 + vocab)
     nb = HIDDEN // 32
