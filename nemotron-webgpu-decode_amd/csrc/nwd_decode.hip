@@ -52,15 +52,17 @@
 
 namespace nwd {
 
-// Build-time tuning constants (the defaults are the measured best on MI355X).
-#ifndef NWD_DECODE_WAVES
-#define NWD_DECODE_WAVES 4
-#endif
+// Keys per row per iteration, a build-time tuning constant: 2 is the
+// measured best on MI355X (append + attend per step, 4 and 8 keys: 7.07 and
+// 8.23 us at 153 keys against 6.29, 11.3 and 13.3 at 4K against 10.2, 31.1
+// and 32.7 at 32K against 29.9).
 #ifndef NWD_DECODE_KEYS_PER_ROW
 #define NWD_DECODE_KEYS_PER_ROW 2
 #endif
 
-constexpr int kWaves = NWD_DECODE_WAVES;
+// Four wavefronts per workgroup (eight measured slower at 4K and 32K);
+// merge_group's thread mapping assumes these 256 threads.
+constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 
 
