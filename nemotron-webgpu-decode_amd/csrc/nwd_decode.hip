@@ -8,7 +8,10 @@
 //
 // Here one 256-thread workgroup (4 wavefronts) owns (sequence b, KV head
 // hkv, split s): it loads each K/V row of its key range once and serves all G
-// query heads of the group from it.
+// query heads of the group from it. When one split and few sequences leave
+// the chip nearly idle, the launch instead gives each query head its own
+// workgroup (kQsub = G workgroups per KV head, each serving one head), which
+// shortens every workgroup's serial chain G-fold.
 //
 // Mapping inside a wavefront: 4 rows of 16 lanes; a row owns one key at a
 // time and each lane holds 8 of its 128 dims (one 16-byte run), so one load
@@ -267,7 +270,9 @@ struct DecodeArgs {
   int* status;
 };
 
-template <int G, bool kQ16, bool kO16>
+// kQsub workgroups per KV head, each serving G of its query heads (kQsub = 1:
+// one workgroup serves the whole group).
+template <int G, bool kQ16, bool kO16, int kQsub>
 __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeArgs a) {
   using C = DecodeCfg<G>;
   constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
@@ -281,7 +286,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   float* lds_o = lds;                                 // [kWaves][G][D]
   float* lds_ml = lds + kWaves * G * kHeadDim;         // [kWaves][G][2]
 
-  const int split = blockIdx.x, hkv = blockIdx.y, b = blockIdx.z;
+  const int split = blockIdx.x, hkv = blockIdx.y / kQsub, b = blockIdx.z;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int row = lane / kLanes, col = lane % kLanes;
@@ -349,7 +354,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
 
   // Query registers: this lane's dims of each of the G heads.
-  const int h0 = hkv * G;
+  const int h0 = blockIdx.y * G;
   const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kHeadDim + col * 8;
   f16x8 q16[kQ16 ? G : 1][kRuns];
   float q32[kQ16 ? 1 : G][kDims];
@@ -573,7 +578,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   // The new rows go to the caches last: lanes 0-15 hold the 16 runs of the
   // new K row in nk, lanes 16-31 those of the new V row in nv.
-  if (owns_new && tid < 32) {
+  if (owns_new && tid < 32 && blockIdx.y % kQsub == 0) {
     f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim + col * 8;
     *reinterpret_cast<f16x8*>(dst) = tid < 16 ? nk[0] : nv[0];
   }
@@ -614,10 +619,13 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
   merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds);
 }
 
-template <int G, bool kQ16, bool kO16>
+// Largest grid the one-workgroup-per-query-head form is used for (one per CU).
+constexpr int kSubSplitMaxWorkgroups = 256;
+
+template <int G, bool kQ16, bool kO16, int kQsub>
 static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
-  dim3 grid((unsigned)a.nsplit, (unsigned)a.n_kv, (unsigned)batch);
-  decode_split_kernel<G, kQ16, kO16><<<grid, kThreads, 0, stream>>>(a);
+  dim3 grid((unsigned)a.nsplit, (unsigned)(a.n_kv * kQsub), (unsigned)batch);
+  decode_split_kernel<G, kQ16, kO16, kQsub><<<grid, kThreads, 0, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
   decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kThreads, 0, stream>>>(
@@ -625,10 +633,11 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <int G>
+template <int G, int kQsub = 1>
 static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, int batch, hipStream_t st) {
-  if (s.q16) return s.o16 ? launch_g<G, true, true>(a, batch, st) : launch_g<G, true, false>(a, batch, st);
-  return s.o16 ? launch_g<G, false, true>(a, batch, st) : launch_g<G, false, false>(a, batch, st);
+  if (s.q16)
+    return s.o16 ? launch_g<G, true, true, kQsub>(a, batch, st) : launch_g<G, true, false, kQsub>(a, batch, st);
+  return s.o16 ? launch_g<G, false, true, kQsub>(a, batch, st) : launch_g<G, false, false, kQsub>(a, batch, st);
 }
 
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
@@ -653,6 +662,21 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.fused_merge = c.fused_merge;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
+  // One split over few (sequence, KV head) pairs: the chip is nearly idle
+  // and each workgroup's time is its serial chain of key iterations, whose
+  // compute grows with the heads it serves. Then one workgroup per query
+  // head (each reads its group's K/V rows, G-fold traffic that is small at
+  // these sizes): 4.5 against 6.3 us per step at 153 keys, B = 1, G = 4,
+  // the same bits.
+  if (a.nsplit == 1 && (int64_t)c.batch * s.n_heads <= kSubSplitMaxWorkgroups) {
+    switch (s.group) {
+      case 2: return launch_qo<1, 2>(s, a, c.batch, stream);
+      case 4: return launch_qo<1, 4>(s, a, c.batch, stream);
+      case 5: return launch_qo<1, 5>(s, a, c.batch, stream);
+      case 8: return launch_qo<1, 8>(s, a, c.batch, stream);
+      default: break;  // group 1 is already one workgroup per query head
+    }
+  }
   switch (s.group) {
     case 1: return launch_qo<1>(s, a, c.batch, stream);
     case 2: return launch_qo<2>(s, a, c.batch, stream);

@@ -294,6 +294,44 @@ def test_append_decode_equals_two_launches(G, src):
         assert max_abs(want[b], oracle.sparse_attn_f32(f32(q[b]), kk, vv)) < TOL
 
 
+@pytest.mark.parametrize("G", [2, 4, 5, 8])
+def test_one_workgroup_per_query_head_same_bits(G):
+    """A single-split decode of few sequences (batch x heads <= 256) runs one
+    workgroup per query head; more sequences run one per KV head. Each
+    sequence of a batch too large for the first form, run alone, must give
+    the same bits (output and fused-append cache rows), and the oracle's
+    result."""
+    say(f"per-query-head form G={G}")
+    Hkv, L = 8, 200
+    H = G * Hkv
+    B = 256 // H + 1
+    g = rng(350 + G)
+    rows = [kv_rows(g, L - 1, Hkv) for _ in range(B)]
+    newk = normal_f16(g, (B, Hkv, D))
+    newv = normal_f16(g, (B, Hkv, D))
+    q = normal_f16(g, (B, H, D))
+    with nw.AttnContext(H, Hkv, L, max_batch=B) as ctx:
+        base_k = to_cache([r[0] for r in rows], Hkv, L)
+        base_v = to_cache([r[1] for r in rows], Hkv, L)
+        assert ctx.decode_splits(B, L) == 1 and ctx.decode_splits(1, L) == 1
+        kc, vc = dev(base_k), dev(base_v)
+        out = torch.empty((B, H, D), dtype=torch.float16, device="cuda")
+        ctx.append_decode(dev(q), dev(newk), dev(newv), kc, vc, pos_tensor([L - 1] * B), out, B)
+        kc1, vc1 = dev(base_k), dev(base_v)
+        for b in range(B):  # the same sequences one at a time
+            o1 = torch.empty((1, H, D), dtype=torch.float16, device="cuda")
+            ctx.append_decode(dev(q[b:b + 1]), dev(newk[b:b + 1]), dev(newv[b:b + 1]), kc1[b:b + 1],
+                              vc1[b:b + 1], pos_tensor([L - 1]), o1, 1)
+            assert torch.equal(o1[0], out[b]), b
+        assert torch.equal(kc1, kc) and torch.equal(vc1, vc)
+        assert ctx.device_status() == nw.NWD_OK
+        got = out.float().cpu().numpy()
+    for b in range(B):
+        kk = f32(from_cache(host(kc), b, L))
+        vv = f32(from_cache(host(vc), b, L))
+        assert max_abs(got[b], oracle.sparse_attn_f32(f32(q[b]), kk, vv)) < TOL, b
+
+
 def test_fused_merge_repeated_calls_and_batches():
     """Many back-to-back calls with changing inputs, batch sizes and split
     counts: the in-kernel merge (arrival tickets) must give the separate-kernel
