@@ -61,14 +61,18 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
   return max_len <= 0 ? ctx->desc.max_seq : max_len;
 }
 
-// Up to 256 keys one workgroup per (sequence, KV head) is fastest (no merge
-// launch: 6.5 against 7.9 us per step at 153 keys). Beyond, fill the chip
-// even where that leaves splits with no 128-key unit (an empty split costs
-// less than the unused CUs: 8.0-8.9 against 8.5-9.7 us per step from 384 to
-// 2048 keys, measured on MI355X).
+// Short contexts take one split (no merge launch). With few sequences
+// (batch x heads <= kSubSplitMaxWorkgroups) the decode then runs one
+// workgroup per query head, which pays up to 512 keys (per append + attend
+// step: 5.6 against 8.0 us at 320 keys, 7.9 against 8.1 at 576, 10.2 against
+// 8.2 at 832); otherwise up to 256 (6.5 against 7.9 us at 153 keys). Beyond,
+// fill the chip even where that leaves splits with no 128-key unit (an empty
+// split costs less than the unused CUs: 8.0-8.9 against 8.5-9.7 us per step
+// from 384 to 2048 keys). Measured on MI355X at B = 1, 32 query heads.
 int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
   const int units = (max_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
-  if (units <= 2) return 1;
+  const bool per_head = (int64_t)batch * ctx->desc.n_heads <= nwd::kSubSplitMaxWorkgroups;
+  if (units <= (per_head ? 4 : 2)) return 1;
   const int per_wave = batch * ctx->desc.n_kv_heads;
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
   const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work

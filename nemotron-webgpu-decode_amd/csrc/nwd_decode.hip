@@ -619,9 +619,6 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
   merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds);
 }
 
-// Largest grid the one-workgroup-per-query-head form is used for (one per CU).
-constexpr int kSubSplitMaxWorkgroups = 256;
-
 template <int G, bool kQ16, bool kO16, int kQsub>
 static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
   dim3 grid((unsigned)a.nsplit, (unsigned)(a.n_kv * kQsub), (unsigned)batch);

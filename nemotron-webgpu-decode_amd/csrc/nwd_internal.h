@@ -52,6 +52,10 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                          hipStream_t stream);
 
+// Largest batch x query heads for which a single-split decode runs one
+// workgroup per query head (one per CU); the split rule uses it too.
+constexpr int kSubSplitMaxWorkgroups = 256;
+
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,
                           int batch, int n_new, int max_len, const Workspace& ws,
