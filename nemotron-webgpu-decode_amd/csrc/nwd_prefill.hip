@@ -384,10 +384,13 @@ static_assert(kPrefillLds >= (size_t)4 * 64 * kRB * 34 * sizeof(float), "merge e
 static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
 
 // Splits of each row tile's key range: enough workgroups to fill the chip
-// (256), at most 8, and as many as the workspace holds records for.
-static int prefill_splits(int64_t row_tiles, int64_t rows, const Workspace& ws) {
+// (256), at most 8, no more than the key tiles a row tile can have (keys
+// are bounded by max_len), and as many as the workspace holds records for.
+static int prefill_splits(int64_t row_tiles, int64_t rows, int max_len, const Workspace& ws) {
   int n = (int)((256 + row_tiles - 1) / row_tiles);
   if (n > 8) n = 8;
+  const int key_tiles = (max_len + kPBN - 1) / kPBN;
+  if (n > key_tiles) n = key_tiles;
   while (n > 1 && rows * n > ws.records) --n;
   return n < 1 ? 1 : n;
 }
@@ -395,7 +398,7 @@ static int prefill_splits(int64_t row_tiles, int64_t rows, const Workspace& ws) 
 template <int G, bool kQ16, bool kO16>
 static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
-                                   const Workspace& ws, hipStream_t stream) {
+                                   int max_len, const Workspace& ws, hipStream_t stream) {
   auto kern = prefill_kernel<G, kQ16, kO16>;
   // The dynamic LDS size exceeds the 64 KB default: raise the kernel's limit
   // once per device (the attribute is per device).
@@ -425,7 +428,7 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
   a.status = ws.status;
   const int64_t row_tiles = (int64_t)a.mtiles * s.n_kv * batch;
   const int64_t rows = (int64_t)n_new * s.n_heads * batch;
-  const int nsplit = prefill_splits(row_tiles, rows, ws);
+  const int nsplit = prefill_splits(row_tiles, rows, max_len, ws);
   a.nsplit = nsplit;
   a.part_o = ws.part_o;
   a.part_ml = ws.part_ml;
@@ -440,25 +443,24 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
 template <int G>
 static hipError_t launch_prefill_g(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
-                                   const Workspace& ws, hipStream_t stream) {
+                                   int max_len, const Workspace& ws, hipStream_t stream) {
   if (s.q16)
-    return s.o16 ? launch_prefill_t<G, true, true>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream)
-                 : launch_prefill_t<G, true, false>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
-  return s.o16 ? launch_prefill_t<G, false, true>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream)
-               : launch_prefill_t<G, false, false>(s, q, kc, vc, pos0, out, batch, n_new, ws, stream);
+    return s.o16 ? launch_prefill_t<G, true, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
+                 : launch_prefill_t<G, true, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+  return s.o16 ? launch_prefill_t<G, false, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
+               : launch_prefill_t<G, false, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
 }
 
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,
                           int batch, int n_new, int max_len, const Workspace& ws,
                           hipStream_t stream) {
-  (void)max_len;
   switch (s.group) {
-    case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
-    case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
-    case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
-    case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
-    case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, ws, stream);
+    case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
+    case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
+    case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
+    case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
+    case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
     default: return hipErrorInvalidValue;
   }
 }

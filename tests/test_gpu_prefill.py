@@ -67,6 +67,16 @@ def test_prefill_small_all_queries(G):
     assert _check_rows(out, q16, rows, pos0s, range(n_new)) < TOL
 
 
+@pytest.mark.parametrize("G", [4, 5])
+def test_prefill_short_prompt_one_split(G):
+    """A prompt of 60 tokens from an empty cache: every row tile has one
+    key tile, so its keys are not split and the output is written directly."""
+    say(f"prefill short prompt G={G}")
+    Hkv = 8
+    out, q16, rows = _run_prefill(G * Hkv, Hkv, [0], 60, 95 + G)
+    assert _check_rows(out, q16, rows, [0], range(60)) < TOL
+
+
 def test_prefill_batch_ragged_f32_io():
     say("prefill batch=3 f32 io")
     pos0s, n_new = [0, 65, 300], 70
