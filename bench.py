@@ -381,6 +381,9 @@ WORKLOADS = {
     "decode-32k": (32768, 64, 4, "outliers",
                    "decode-32k: B=1, 32q/8kv/d128, past 32768, K/V N(0,1) with 1% +-8 outliers, "
                    "append+attend per step, split-K, 4 layer caches rotated (537 MB)"),
+    "decode-153": (152, 1, 64, "normal",
+                   "decode-153: B=1, 32q/8kv/d128, past 152, one token appended at 152 and 153 "
+                   "keys attended per step, K/V N(0,1), 64 layer caches rotated (40 MB)"),
 }
 
 
@@ -502,7 +505,7 @@ def main():
                     default="decode-4k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-32k", action="store_true",
-                    help="skip the secondary decode-32k measurement")
+                    help="skip the secondary decode-32k and decode-153 measurements")
     ap.add_argument("--copy-only", action="store_true",
                     help="only run 4 copies of 256 MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -529,12 +532,15 @@ def main():
               flush=True)
         return
     main_res = run_workload(torch, nw, args.workload, args.steps, args.warmup)
-    extra = None
+    extra = short = None
     if args.workload == "decode-4k" and not args.no_32k:
         r = run_workload(torch, nw, "decode-32k", 256, 16)
         extra = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
                  if k not in ("desc", "mean_kv_bytes")}
         extra["hbm_frac"] = round(r["decode_gbs"] / HBM_PEAK_GBS, 4)
+        r = run_workload(torch, nw, "decode-153", 1024, 64)
+        short = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
+                 if k not in ("desc", "mean_kv_bytes")}
     copy_gbs = copy_bandwidth(torch)
     log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
@@ -583,6 +589,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "decode_32k": extra,
+        "decode_153": short,
         "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(main_res["wall_s"], 4),
     }
