@@ -279,9 +279,11 @@ def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
             "cores": threads, "kind": "port", "sample": f"{done} calls, one layer's weights"}
 
 
-def time_graph(torch, wl, steps: int, warmup: int, append=True):
+def time_graph(torch, wl, steps: int, warmup: int, append=True, reps: int = 1):
     """Warm up eagerly, capture `steps` steps into a HIP graph, replay it once
-    untimed and once timed. Returns (wall seconds, device ms) of the timed replay."""
+    untimed and `reps` times timed. Returns (wall seconds, device ms) of the
+    timed replay, the median one when reps > 1 (the first replays after a
+    capture can run at lower clocks)."""
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for s in range(warmup):
@@ -292,16 +294,19 @@ def time_graph(torch, wl, steps: int, warmup: int, append=True):
         for s in range(steps):
             wl.step(s, stream, append)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    runs = []
     with torch.cuda.stream(stream):  # replay() launches on the current stream
         graph.replay()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    return wall, start.elapsed_time(end)
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
+            torch.cuda.synchronize()
+            runs.append((time.perf_counter() - t0, start.elapsed_time(end)))
+    runs.sort(key=lambda r: r[1])
+    return runs[len(runs) // 2]
 
 
 def time_eager(torch, wl, steps: int):
@@ -420,7 +425,7 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
     """One 4-bit projection workload: us per call and weight-stream GB/s."""
     log(f"[bench] {name}: {steps} steps")
     wl = Q4LayerWorkload(torch, nw, name)
-    wall, ms = time_graph(torch, wl, steps, warmup)
+    wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
     us = ms * 1e3 / steps
     gbs = wl.bytes_per_step() / (us * 1e-6) / 1e9
     res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us,
@@ -442,8 +447,8 @@ def run_extra(torch, nw, name: str, steps: int, warmup: int, cpu: bool = False):
         return run_q4(torch, nw, name, steps, warmup, cpu)
     log(f"[bench] {name}: {steps} steps")
     wl = RaggedWorkload(torch, nw) if name == "ragged-64" else PrefillWorkload(torch, nw)
-    wall, ms = time_graph(torch, wl, steps, warmup)
-    _, ms_main = time_graph(torch, wl, steps, 0, append=False)
+    wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
+    _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
     us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
     res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us_step,
            "main_us": us_main, "wall_s": wall, "mean_kv_bytes": wl.mean_kv_bytes(steps)}
