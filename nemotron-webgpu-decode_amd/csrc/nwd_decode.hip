@@ -56,9 +56,10 @@
 namespace nwd {
 
 // Keys per row per iteration, a build-time tuning constant: 2 is the
-// measured best on MI355X (append + attend per step, 4 and 8 keys: 7.07 and
-// 8.23 us at 153 keys against 6.29, 11.3 and 13.3 at 4K against 10.2, 31.1
-// and 32.7 at 32K against 29.9).
+// measured best on MI355X (append + attend per step with one workgroup per
+// KV head; 4 and 8 keys: 7.07 and 8.23 us at 153 keys against 6.29, 11.3
+// and 13.3 at 4K against 10.2, 31.1 and 32.7 at 32K against 29.9; 1 key:
+// 10.4 at 4K against 10.1, 34.6 at 32K against 29.4).
 #ifndef NWD_DECODE_KEYS_PER_ROW
 #define NWD_DECODE_KEYS_PER_ROW 2
 #endif
