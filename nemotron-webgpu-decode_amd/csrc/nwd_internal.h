@@ -53,7 +53,10 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
                          hipStream_t stream);
 
 // Largest batch x query heads for which a single-split decode runs one
-// workgroup per query head (one per CU); the split rule uses it too.
+// workgroup per query head (one per CU); the split rule uses it too. Beyond
+// it the G-fold K/V reads cost more than the shorter chains save: 153 keys,
+// 32 query heads, per append + attend step, B = 16: 8.4 against 6.7 us,
+// B = 32: 13.4 against 7.2 (B = 1-8 gain or tie).
 constexpr int kSubSplitMaxWorkgroups = 256;
 
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
