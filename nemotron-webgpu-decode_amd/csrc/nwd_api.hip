@@ -61,18 +61,26 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
   return max_len <= 0 ? ctx->desc.max_seq : max_len;
 }
 
-// Short contexts take one split (no merge launch). With few sequences
-// (batch x heads <= kSubSplitMaxWorkgroups) the decode then runs one
-// workgroup per query head, which pays up to 512 keys (per append + attend
-// step: 5.6 against 8.0 us at 320 keys, 7.9 against 8.1 at 576, 10.2 against
-// 8.2 at 832); otherwise up to 256 (6.5 against 7.9 us at 153 keys). Beyond,
-// fill the chip even where that leaves splits with no 128-key unit (an empty
-// split costs less than the unused CUs: 8.0-8.9 against 8.5-9.7 us per step
-// from 384 to 2048 keys). Measured on MI355X at B = 1, 32 query heads.
+// Split count for nwd_decode_attn. With few sequences (batch x query heads
+// <= kSubSplitMaxWorkgroups) the decode runs one workgroup per query head
+// and split; there one split (no merge launch) pays up to 384 keys, and
+// kSubSplitMaxWorkgroups / (batch x heads) splits up to 2048 (per append +
+// attend step at B = 1, 32 heads: 5.4 against 5.8 us at 320 keys, 5.8
+// against 6.6 at 448, 6.1 against 8.1 with the per-KV-head form at 832,
+// 7.0 against 8.2 at 1600, a tie at 2112, 12.2 against 10.1 at 4160).
+// Otherwise one split up to 256 keys (6.5 against 7.9 us at 153 keys), and
+// beyond, enough splits to fill the chip, even where that leaves splits with
+// no 128-key unit (an empty split costs less than the unused CUs: 8.0-8.9
+// against 8.5-9.7 us per step from 384 to 2048 keys). Measured on MI355X.
 int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
   const int units = (max_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
-  const bool per_head = (int64_t)batch * ctx->desc.n_heads <= nwd::kSubSplitMaxWorkgroups;
-  if (units <= (per_head ? 4 : 2)) return 1;
+  const int64_t heads = (int64_t)batch * ctx->desc.n_heads;
+  if (heads <= nwd::kSubSplitMaxWorkgroups) {
+    if (units <= 3) return 1;
+    if (units <= 16) return (int)(nwd::kSubSplitMaxWorkgroups / heads);
+  } else if (units <= 2) {
+    return 1;
+  }
   const int per_wave = batch * ctx->desc.n_kv_heads;
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
   const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work
@@ -161,7 +169,10 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->ws.status = nullptr;
   ctx->ws.counters = nullptr;
   ctx->status_host = nullptr;
-  const size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
+  // Merge tickets: one per (sequence, KV head), or per (sequence, query
+  // head) in the per-query-head form (at most kSubSplitMaxWorkgroups).
+  size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
+  if (n_counters < (size_t)nwd::kSubSplitMaxWorkgroups) n_counters = nwd::kSubSplitMaxWorkgroups;
   e = hipMalloc(&ctx->ws.part_o, ctx->ws.records * nwd::kHeadDim * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));

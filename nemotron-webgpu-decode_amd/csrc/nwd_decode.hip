@@ -389,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
 
   const int pos_raw = a.pos[b];
   const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
-  if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
+  if (!pos_ok && tid == 0 && split == 0 && blockIdx.y == 0) atomicOr(a.status, kStatusBadPos);
   const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
   // Keys this split attends: [t0, t1); the last split also takes any keys
   // past the host bound.
@@ -594,17 +594,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   if (nsplit == 1 || !a.fused_merge) return;
 
-  // The workgroup that takes the last arrival ticket of this (b, hkv)
-  // merges. Each thread's record stores are complete (device-coherent)
+  // The workgroup that takes the last arrival ticket of this (b, head
+  // group) merges: one counter per (b, blockIdx.y), i.e. per (b, hkv), or per
+  // (b, query head) in the per-query-head form, where batch x n_heads fits
+  // the counters (the host keeps at least kSubSplitMaxWorkgroups of them).
+  // Each thread's record stores are complete (device-coherent)
   // before the barrier, and the ticket is taken after it; the merging
   // workgroup reads the records with device-scope loads. Nothing waits on
   // another workgroup.
   __shared__ int lds_last;
+  int* const counter = &a.counters[b * (a.n_kv * kQsub) + blockIdx.y];
   wait_vm();
   __syncthreads();
   if (tid == 0) {
-    const int ticket = __hip_atomic_fetch_add(&a.counters[b * a.n_kv + hkv], 1, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+    const int ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     lds_last = ticket == nsplit - 1;
   }
   __syncthreads();
@@ -613,7 +616,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // they see what the other workgroups wrote through before their tickets.
   merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
   if (tid == 0)
-    __hip_atomic_store(&a.counters[b * a.n_kv + hkv], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Separate merge: one 256-thread workgroup per (query head, sequence), the
@@ -669,13 +672,14 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.fused_merge = c.fused_merge;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
-  // One split over few (sequence, KV head) pairs: the chip is nearly idle
-  // and each workgroup's time is its serial chain of key iterations, whose
-  // compute grows with the heads it serves. Then one workgroup per query
-  // head (each reads its group's K/V rows, G-fold traffic that is small at
-  // these sizes): 4.5 against 6.3 us per step at 153 keys, B = 1, G = 4,
-  // the same bits.
-  if (a.nsplit == 1 && (int64_t)c.batch * s.n_heads <= kSubSplitMaxWorkgroups) {
+  // When one workgroup per (sequence, query head, split) fits the chip, each
+  // query head gets its own workgroups: a workgroup's time is its serial
+  // chain of key iterations, whose compute grows with the heads it serves,
+  // and the G-fold K/V reads are small at the lengths the split rule sends
+  // here (per append + attend step, B = 1, G = 4: 4.5 against 6.3 us at 153
+  // keys with one split; 6.1 against 8.1 at 832 keys and 6.8 against 8.3 at
+  // 1088 with 8 splits). Same bits.
+  if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
     switch (s.group) {
       case 2: return launch_qo<1, 2>(s, a, c.batch, stream);
       case 4: return launch_qo<1, 4>(s, a, c.batch, stream);
