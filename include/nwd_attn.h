@@ -175,7 +175,8 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 /* Chooses where split-K records are merged: 1 in a separate merge kernel
  * launched after the split kernel (the two-dispatch shape of argmax_partial /
  * argmax_merge, engine/runtime.js:398-399); 0 inside the split kernel, by the
- * last workgroup of each (sequence, kv head) to finish; negative restores the
+ * last workgroup of each (sequence, kv head) to finish (of each (sequence,
+ * query head) when the call runs one workgroup per query head); negative restores the
  * default, the separate kernel (measured faster on MI355X at 4K and 32K
  * keys). Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
