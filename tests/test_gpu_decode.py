@@ -332,6 +332,34 @@ def test_one_workgroup_per_query_head_same_bits(G):
         assert max_abs(got[b], oracle.sparse_attn_f32(f32(q[b]), kk, vv)) < TOL, b
 
 
+@pytest.mark.parametrize("G,B,L", [(5, 3, 900), (4, 1, 1500), (8, 2, 600)])
+def test_per_query_head_form_with_splits(G, B, L):
+    """Up to 2048 keys few sequences run one workgroup per query head and
+    split (256 / (batch x heads) splits); both merge forms give the same
+    bits, and the oracle's result."""
+    say(f"per-query-head form with splits G={G} B={B} L={L}")
+    Hkv = 8
+    H = G * Hkv
+    g = rng(400 + G)
+    rows = [kv_rows(g, L - 29 * b, Hkv) for b in range(B)]
+    q = normal_f16(g, (B, H, D))
+    with nw.AttnContext(H, Hkv, L, max_batch=B, o_dtype="f32") as ctx:
+        n = ctx.decode_splits(B, L)
+        assert n == 256 // (B * H) and n > 1, n
+        kc = dev(to_cache([r[0] for r in rows], Hkv, L))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, L))
+        pos = pos_tensor([L - 1 - 29 * b for b in range(B)])
+        outs = []
+        for sep in (True, False):
+            ctx.set_decode_merge(sep)
+            outs.append(_decode(ctx, dev(q), kc, vc, pos, B, torch.float32))
+        assert ctx.device_status() == nw.NWD_OK
+    assert np.array_equal(outs[0], outs[1])
+    for b in range(B):
+        want = oracle.sparse_attn_f32(f32(q[b]), f32(rows[b][0]), f32(rows[b][1]))
+        assert max_abs(outs[0][b], want) < TOL, b
+
+
 def test_fused_merge_repeated_calls_and_batches():
     """Many back-to-back calls with changing inputs, batch sizes and split
     counts: the in-kernel merge (arrival tickets) must give the separate-kernel
