@@ -384,13 +384,13 @@ static_assert(kPrefillLds >= (size_t)4 * 64 * kRB * 34 * sizeof(float), "merge e
 static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
 
 // Splits of each row tile's key range: enough workgroups to fill the chip
-// (256), at most 8, no more than the key tiles a row tile can have (keys
-// are bounded by max_len), and as many as the workspace holds records for.
+// (256), at most 16, at least 3 key tiles per split (keys are bounded by
+// max_len), and as many as the workspace holds records for.
 static int prefill_splits(int64_t row_tiles, int64_t rows, int max_len, const Workspace& ws) {
   int n = (int)((256 + row_tiles - 1) / row_tiles);
-  if (n > 8) n = 8;
+  if (n > 16) n = 16;
   const int key_tiles = (max_len + kPBN - 1) / kPBN;
-  if (n > key_tiles) n = key_tiles;
+  if (n > key_tiles / 3) n = key_tiles / 3;
   while (n > 1 && rows * n > ws.records) --n;
   return n < 1 ? 1 : n;
 }
