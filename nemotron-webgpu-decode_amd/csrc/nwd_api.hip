@@ -64,7 +64,8 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
 // Split count for nwd_decode_attn. With few sequences (batch x query heads
 // <= kSubSplitMaxWorkgroups) the decode runs one workgroup per query head
 // and split; there one split (no merge launch) pays up to 384 keys, and
-// kSubSplitMaxWorkgroups / (batch x heads) splits up to 2048 (per append +
+// n = kSubSplitMaxWorkgroups / (batch x heads) splits while they hold at
+// most 256 keys each (up to 2048 keys at B = 1, 32 heads; per append +
 // attend step at B = 1, 32 heads: 5.4 against 5.8 us at 320 keys, 5.8
 // against 6.6 at 448, 6.1 against 8.1 with the per-KV-head form at 832,
 // 7.0 against 8.2 at 1600, a tie at 2112, 12.2 against 10.1 at 4160).
@@ -77,7 +78,8 @@ int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
   const int64_t heads = (int64_t)batch * ctx->desc.n_heads;
   if (heads <= nwd::kSubSplitMaxWorkgroups) {
     if (units <= 3) return 1;
-    if (units <= 16) return (int)(nwd::kSubSplitMaxWorkgroups / heads);
+    const int n = (int)(nwd::kSubSplitMaxWorkgroups / heads);
+    if (units <= 2 * n) return n;  // at most two 128-key units per split
   } else if (units <= 2) {
     return 1;
   }
