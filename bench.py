@@ -2,23 +2,32 @@
 
 One "step" is one attention-layer step of the reference engine
 (engine/runtime.js:389-391: kv_append for K, for V, then sparse_attn): here
-one nwd_append_decode launch that writes the new token's K and V rows and
-attends over pos+1 keys. Default workload: 32 query heads, 8 KV heads, head_dim
-128, fp16 cache, 4096 cached tokens, 64 generated tokens per window. To keep
-the 256 MB Infinity Cache from serving the KV reads, each step uses the next
-of 32 distinct layer caches (545 MB in total), the way a model walks its
-layers; step s uses layer s % 32 and token (s // 32) % 64, at position
-4096 + token.
+one nwd_append_decode call that writes the new token's K and V rows and
+attends over pos+1 keys.
 
-Inputs are resident in HBM before timing starts and the steps are replayed
-from a HIP graph (captured once), so the timed region is device work plus the
-graph's launch gaps. Prints ONE JSON line.
+The headline (the JSON line's `value`, `ms_per_step`, `roofline`,
+`cpu_baseline`) is the decode-32k workload: batch 1, 32 query heads, 8 KV
+heads, head_dim 128, fp16 cache, 32768 cached tokens with 1% of K/V entries
+at +-8, one token appended and attended per step. To keep the 256 MB
+Infinity Cache from serving the KV reads, step s uses layer cache s % 4 of 4
+distinct caches (537 MB), the way a model walks its layers, and token
+(s // 4) % 64 of a 64-token window. The other four workloads of the
+benchmark specification (decode-153, decode-4k, ragged-64, prefill-512) and
+the read ceiling of the same access pattern (stream-read) are measured in the
+same run and reported under `configs` and `stream_read`, each with its own
+roofline block.
+
+Inputs are resident in HBM before timing starts and steps are replayed from
+HIP graphs (captured once), timed with hipEvents on the stream the kernels
+run on. Prints ONE JSON line.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+       python bench.py --workload NAME    (one workload, for profiling)
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -29,8 +38,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "nemotron-webgpu-decode_amd"))
 
 METRIC = "µs/attention-layer step + achieved KV-read GB/s (% of HBM peak), 1×MI355X"
-HBM_PEAK_GBS = 8000.0
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 H, HKV, D = 32, 8, 128
+BENCH_LIB = ROOT / "nemotron-webgpu-decode_amd" / "lib" / "libnwd_bench.so"
 
 
 def kv_bytes(L: int) -> int:
@@ -40,6 +51,36 @@ def kv_bytes(L: int) -> int:
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+class Hip:
+    """The few HIP runtime calls bench.py makes directly (events around the
+    split kernel, see nwd_set_kernel_events)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+
+    def event(self) -> int:
+        e = ctypes.c_void_p()
+        if self.lib.hipEventCreate(ctypes.byref(e)) != 0:
+            raise RuntimeError("hipEventCreate failed")
+        return e.value
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        if self.lib.hipEventSynchronize(b) != 0:
+            raise RuntimeError("hipEventSynchronize failed")
+        ms = ctypes.c_float()
+        if self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, e: int):
+        self.lib.hipEventDestroy(e)
 
 
 class DecodeWorkload:
@@ -321,10 +362,33 @@ def time_eager(torch, wl, steps: int):
     return start.elapsed_time(end)
 
 
-def cpu_baseline(past: int, window: int, budget_s: float = 20.0):
+def split_kernel_us(torch, hip: Hip, wl, calls: int):
+    """Duration of the decode split kernel alone (decode_split_kernel, the
+    dominant kernel of a decode call), from HIP events the runtime records
+    at its start and end (nwd_set_kernel_events); eager decode-only calls
+    over the same rotation of layer caches. Returns the mean in us."""
+    stream = torch.cuda.Stream()
+    e0, e1 = hip.event(), hip.event()
+    wl.ctx.set_kernel_events(e0, e1)
+    tot = []
+    try:
+        for s in range(calls + 8):
+            wl.step(s, stream, append=False)
+            ms = hip.elapsed_ms(e0, e1)
+            if s >= 8:
+                tot.append(ms * 1e3)
+    finally:
+        wl.ctx.set_kernel_events(None, None)
+        torch.cuda.synchronize()
+        hip.destroy(e0)
+        hip.destroy(e1)
+    return sum(tot) / len(tot)
+
+
+def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "normal"):
     """The oracle (op-for-op CPU restatement of kernels/sparse_attn.wgsl +
     kv_append.wgsl, f32, per-head workgroups over OpenMP threads) on the same
-    workload, for as many steps of the window as fit in `budget_s`."""
+    workload shape, for as many steps of the window as fit in `budget_s`."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -333,8 +397,15 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0):
     threads = oracle.max_threads()
     g = np.random.Generator(np.random.PCG64(7))
     cap = past + window
-    k = g.standard_normal((cap, HKV, D), dtype=np.float32)
-    v = g.standard_normal((cap, HKV, D), dtype=np.float32)
+
+    def kv():
+        x = g.standard_normal((cap, HKV, D), dtype=np.float32)
+        if dist == "outliers":
+            hit = g.random((cap, HKV, D)) < 0.01
+            x[hit] = np.where(g.random(int(hit.sum())) < 0.5, -8.0, 8.0)
+        return x
+
+    k, v = kv(), kv()
     q = g.standard_normal((window, H, D), dtype=np.float32)
     kc = np.zeros(cap * HKV * D, np.float32)
     vc = np.zeros(cap * HKV * D, np.float32)
@@ -365,11 +436,25 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0):
     }
 
 
+WORKLOADS = {
+    # name: (past, window, layers, K/V distribution, description)
+    "decode-32k": (32768, 64, 4, "outliers",
+                   "decode-32k: B=1, 32q/8kv/d128, past 32768, K/V N(0,1) with 1% +-8 outliers, "
+                   "append+attend per step, split-K, 4 layer caches rotated (537 MB)"),
+    "decode-4k": (4096, 64, 32, "head-scale",
+                  "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, K/V N(0,1) x per-head "
+                  "U[0.5,2], append+attend per step, 32 layer caches rotated (545 MB)"),
+    "decode-153": (152, 1, 64, "normal",
+                   "decode-153: B=1, 32q/8kv/d128, past 152, one token appended at 152 and 153 "
+                   "keys attended per step, K/V N(0,1), 64 layer caches rotated (40 MB)"),
+}
 EXTRA_WORKLOADS = {
     "ragged-64": "ragged-64: 64 sequences, past U{512..16384} (seed 4), one query each, "
                  "append+attend per step",
     "prefill-512": "prefill-512: B=1, 512 new tokens onto 8192 cached, causal in the chunk, "
                    "kv_append of 512 rows + fp16-MFMA prefill per step",
+    "stream-read": "stream-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
+                   "rotated) read with the split kernel's access pattern and nothing else",
     "qkv-append": "qkv-append: B=1, Nano-4B q/k/v 4-bit projections K=3136 -> 5120+1024+1024 "
                   "with k/v rounded into the fp16 caches, 32 weight sets rotated (461 MB)",
     "o-proj": "o-proj: B=1, Nano-4B o_proj 4-bit K=5120 -> 3136 with the residual add, "
@@ -377,46 +462,134 @@ EXTRA_WORKLOADS = {
     "lm-head": "lm-head: B=1, Nano-4B lm_head 4-bit K=3136 -> 131072 with the greedy pick "
                "(argmax partial in the GEMV, then the merge), 2 weight sets rotated (527 MB)",
 }
-
-WORKLOADS = {
-    # name: (past, window, layers, K/V distribution, description)
-    "decode-4k": (4096, 64, 32, "head-scale",
-                  "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, K/V N(0,1) x per-head "
-                  "U[0.5,2], append+attend per step, 32 layer caches rotated (545 MB)"),
-    "decode-32k": (32768, 64, 4, "outliers",
-                   "decode-32k: B=1, 32q/8kv/d128, past 32768, K/V N(0,1) with 1% +-8 outliers, "
-                   "append+attend per step, split-K, 4 layer caches rotated (537 MB)"),
-    "decode-153": (152, 1, 64, "normal",
-                   "decode-153: B=1, 32q/8kv/d128, past 152, one token appended at 152 and 153 "
-                   "keys attended per step, K/V N(0,1), 64 layer caches rotated (40 MB)"),
-}
+# Step counts of the secondary measurements (fixed, so a short --steps only
+# shortens the headline's timed region).
+SECONDARY_STEPS = {"decode-32k": 256, "decode-4k": 512, "decode-153": 1024, "ragged-64": 64,
+                   "prefill-512": 32, "stream-read": 64}
 
 
-def run_workload(torch, nw, name: str, steps: int, warmup: int):
+def hbm_roofline(achieved_gbs: float, kernel: str, algorithmic_bytes: float, traffic):
+    return {"bound": "hbm", "kernel": kernel, "achieved": round(achieved_gbs, 1),
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(achieved_gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic, "algorithmic_bytes": int(algorithmic_bytes)}
+
+
+def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, headline: bool = False):
     """Times `steps` append+attend steps and `steps` decode-only calls of one
-    workload from HIP graphs; returns a dict of the measurements."""
+    workload from HIP graphs, and the split kernel alone from eager calls;
+    returns a dict of the measurements."""
     past, window, layers, dist, desc = WORKLOADS[name]
     log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
-    wall, ms = time_graph(torch, wl, steps, warmup)
+    # median of 3 timed replays, each of exactly `steps` steps
+    wall, ms = time_graph(torch, wl, steps, warmup, reps=3)
     us_step = ms * 1e3 / steps
     mean_b = wl.mean_kv_bytes(steps)
-    # the dominant work alone: one nwd_decode_attn call per step, same rotation
-    _, ms_dec = time_graph(torch, wl, steps, 0, append=False)
-    dec_us = ms_dec * 1e3 / steps
+    # the decode call alone (split + merge kernels), same rotation
+    n_dec = max(steps, SECONDARY_STEPS[name])
+    _, ms_dec = time_graph(torch, wl, n_dec, 0, append=False, reps=3)
+    dec_us = ms_dec * 1e3 / n_dec
+    dec_b = wl.mean_kv_bytes(n_dec)
+    split_us = split_kernel_us(torch, hip, wl, 128)
     n_eager = min(steps, 512)
     eager_us = time_eager(torch, wl, n_eager) * 1e3 / n_eager
+    splits = wl.ctx.decode_splits(1, wl.cap)
     res = {
         "workload": name, "desc": desc, "past": past, "window": window, "layers": layers,
-        "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
-        "decode_us": dec_us, "decode_gbs": mean_b / (dec_us * 1e-6) / 1e9,
-        "eager_us_per_step": eager_us, "mean_kv_bytes": mean_b, "wall_s": wall,
-        "splits": wl.ctx.decode_splits(1, wl.cap),
+        "steps": steps, "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
+        "decode_us": dec_us, "decode_gbs": dec_b / (dec_us * 1e-6) / 1e9,
+        "split_kernel_us": split_us, "eager_us_per_step": eager_us, "mean_kv_bytes": mean_b,
+        "wall_s": wall, "splits": splits,
     }
-    log(f"[bench] {name}: step {us_step:.3f} us ({res['gbs']:.1f} GB/s), decode {dec_us:.3f} us "
-        f"({res['decode_gbs']:.1f} GB/s), eager step {eager_us:.3f} us")
+    kernel = ("decode_split_kernel (duration from HIP events at its start and end); the call "
+              "adds decode_merge_kernel" if splits > 1 else "decode_split_kernel (one split, no merge)")
+    res["roofline"] = hbm_roofline(dec_b / (split_us * 1e-6) / 1e9, kernel, dec_b,
+                                   measured_traffic(name))
+    res["call_roofline"] = {"achieved": round(res["decode_gbs"], 1),
+                            "frac": round(res["decode_gbs"] / HBM_PEAK_GBS, 4),
+                            "us": round(dec_us, 3)}
+    log(f"[bench] {name}: step {us_step:.3f} us ({res['gbs']:.1f} GB/s), decode call {dec_us:.3f} us "
+        f"({res['decode_gbs']:.1f} GB/s), split kernel {split_us:.3f} us, eager step {eager_us:.3f} us")
     wl.ctx.close()
     del wl
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_ragged(torch, nw, steps: int, warmup: int):
+    log(f"[bench] ragged-64: {steps} steps")
+    wl = RaggedWorkload(torch, nw)
+    wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
+    _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
+    us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
+    b = wl.mean_kv_bytes(steps)
+    res = {"workload": "ragged-64", "desc": EXTRA_WORKLOADS["ragged-64"], "us_per_step": us_step,
+           "decode_us": us_main, "wall_s": wall, "mean_kv_bytes": b,
+           "splits": wl.ctx.decode_splits(wl.batch, wl.cap),
+           "gbs": b / (us_step * 1e-6) / 1e9, "decode_gbs": b / (us_main * 1e-6) / 1e9}
+    res["roofline"] = hbm_roofline(res["decode_gbs"],
+                                   "nwd_decode_attn (split + merge kernels, one call)", b,
+                                   measured_traffic("ragged-64"))
+    log(f"[bench] ragged-64: step {us_step:.1f} us, decode {us_main:.1f} us "
+        f"({res['decode_gbs']:.1f} GB/s)")
+    wl.ctx.close()
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_prefill(torch, nw, steps: int, warmup: int):
+    log(f"[bench] prefill-512: {steps} steps")
+    wl = PrefillWorkload(torch, nw)
+    wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
+    _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
+    us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
+    tflops = wl.flops() / (us_main * 1e-6) / 1e12
+    res = {"workload": "prefill-512", "desc": EXTRA_WORKLOADS["prefill-512"],
+           "us_per_step": us_step, "prefill_us": us_main, "wall_s": wall, "flops": wl.flops(),
+           "roofline": {"bound": "mfma", "kernel": "nwd_prefill_attn (prefill + split merge)",
+                        "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                        "traffic": None, "algorithmic_flops": wl.flops()}}
+    log(f"[bench] prefill-512: step {us_step:.1f} us (kv_append + prefill), prefill {us_main:.1f} us "
+        f"({tflops:.1f} TFLOP/s)")
+    wl.ctx.close()
+    del wl
+    torch.cuda.empty_cache()
+    return res
+
+
+def run_stream_read(torch, nw, launches: int):
+    """The read ceiling of the decode-32k access pattern (csrc/bench/
+    nwd_stream_read.hip): the same 4 layer caches, 32 splits per KV head,
+    graph-replayed back to back."""
+    lib = ctypes.CDLL(str(BENCH_LIB))
+    lib.nwd_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                          ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_void_p, ctypes.c_void_p]
+    past, window, layers, dist, _ = WORKLOADS["decode-32k"]
+    log(f"[bench] stream-read: {launches} launches")
+    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
+    keys, splits = past + 1, wl.ctx.decode_splits(1, wl.cap)
+    out = torch.empty(HKV * splits * 256, dtype=torch.float32, device="cuda")
+
+    class Reader:
+        def step(self, s, stream, append=True):
+            rc = lib.nwd_bench_stream_read(wl.kc[s % layers].data_ptr(), wl.vc[s % layers].data_ptr(),
+                                           HKV, wl.cap, keys, splits, out.data_ptr(),
+                                           stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"nwd_bench_stream_read: hip error {rc}")
+
+    _, ms = time_graph(torch, Reader(), launches, 8, reps=3)
+    us = ms * 1e3 / launches
+    b = kv_bytes(keys)
+    res = {"workload": "stream-read", "desc": EXTRA_WORKLOADS["stream-read"], "us_per_launch": us,
+           "bytes": b, "gbs": b / (us * 1e-6) / 1e9, "frac": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "splits": splits}
+    log(f"[bench] stream-read: {us:.3f} us per 134 MB launch ({res['gbs']:.1f} GB/s)")
+    wl.ctx.close()
+    del wl, out
     torch.cuda.empty_cache()
     return res
 
@@ -440,36 +613,10 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
     return res
 
 
-def run_extra(torch, nw, name: str, steps: int, warmup: int, cpu: bool = False):
-    """The ragged batch, the prefill chunk and the 4-bit projections (measured
-    on request)."""
-    if name in ("qkv-append", "o-proj", "lm-head"):
-        return run_q4(torch, nw, name, steps, warmup, cpu)
-    log(f"[bench] {name}: {steps} steps")
-    wl = RaggedWorkload(torch, nw) if name == "ragged-64" else PrefillWorkload(torch, nw)
-    wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
-    _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
-    us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
-    res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us_step,
-           "main_us": us_main, "wall_s": wall, "mean_kv_bytes": wl.mean_kv_bytes(steps)}
-    if name == "prefill-512":
-        res["tflops"] = wl.flops() / (us_main * 1e-6) / 1e12
-        res["flops"] = wl.flops()
-    else:
-        res["splits"] = wl.ctx.decode_splits(wl.batch, wl.cap)
-        res["gbs"] = res["mean_kv_bytes"] / (us_step * 1e-6) / 1e9
-        res["decode_gbs"] = res["mean_kv_bytes"] / (us_main * 1e-6) / 1e9
-    log(f"[bench] {name}: {res}")
-    wl.ctx.close()
-    del wl
-    torch.cuda.empty_cache()
-    return res
-
-
 def measured_traffic(name: str):
-    """HBM bytes per nwd_decode_attn call of `name` from the committed
-    counter summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled by
-    the plain-copy calibration), or None if it has not been profiled."""
+    """HBM bytes per call of `name` from the committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs, scaled by the plain-copy
+    calibration), or None if it has not been profiled."""
     f = ROOT / "profiles" / f"{name}_pmc.md"
     if not f.exists():
         return None
@@ -501,16 +648,23 @@ def copy_bandwidth(torch, nbytes: int = 1 << 30, reps: int = 10):
     return round(gbs, 1)
 
 
+def rounded(d):
+    if isinstance(d, dict):
+        return {k: rounded(v) for k, v in d.items() if k not in ("desc",)}
+    if isinstance(d, float):
+        return round(d, 3)
+    return d
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2048)
-    ap.add_argument("--warmup", type=int, default=256)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + sorted(EXTRA_WORKLOADS),
-                    default="decode-4k")
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--workload", choices=["all"] + sorted(WORKLOADS) + sorted(EXTRA_WORKLOADS),
+                    default="all", help="all (default): the headline and every configuration; "
+                    "a name: that workload alone (profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-32k", action="store_true",
-                    help="skip the secondary decode-32k and decode-153 measurements")
     ap.add_argument("--copy-only", action="store_true",
                     help="only run 4 copies of 256 MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -529,34 +683,40 @@ def main():
         log(f"[bench] copy 256 MiB x4: {copy_bandwidth(torch, 1 << 28, 4)} GB/s")
         return
     nw.load_library()
+    hip = Hip()
 
-    if args.workload in EXTRA_WORKLOADS:
-        r = run_extra(torch, nw, args.workload, args.steps, args.warmup,
-                      cpu=not args.no_cpu_baseline)
-        print(json.dumps({k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()}),
-              flush=True)
+    if args.workload != "all":
+        w = args.workload
+        if w in WORKLOADS:
+            r = run_decode(torch, nw, hip, w, args.steps, args.warmup)
+        elif w == "ragged-64":
+            r = run_ragged(torch, nw, args.steps, args.warmup)
+        elif w == "prefill-512":
+            r = run_prefill(torch, nw, args.steps, args.warmup)
+        elif w == "stream-read":
+            r = run_stream_read(torch, nw, args.steps)
+        else:
+            r = run_q4(torch, nw, w, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
+        print(json.dumps(rounded(r)), flush=True)
         return
-    main_res = run_workload(torch, nw, args.workload, args.steps, args.warmup)
-    extra = short = None
-    if args.workload == "decode-4k" and not args.no_32k:
-        r = run_workload(torch, nw, "decode-32k", 256, 16)
-        extra = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
-                 if k not in ("desc", "mean_kv_bytes")}
-        extra["hbm_frac"] = round(r["decode_gbs"] / HBM_PEAK_GBS, 4)
-        r = run_workload(torch, nw, "decode-153", 1024, 64)
-        short = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in r.items()
-                 if k not in ("desc", "mean_kv_bytes")}
+
+    head = run_decode(torch, nw, hip, "decode-32k", args.steps, args.warmup, headline=True)
+    configs = {
+        "decode-153": run_decode(torch, nw, hip, "decode-153", SECONDARY_STEPS["decode-153"], 64),
+        "decode-4k": run_decode(torch, nw, hip, "decode-4k", SECONDARY_STEPS["decode-4k"], 32),
+        "ragged-64": run_ragged(torch, nw, SECONDARY_STEPS["ragged-64"], 8),
+        "prefill-512": run_prefill(torch, nw, SECONDARY_STEPS["prefill-512"], 4),
+    }
+    stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
     copy_gbs = copy_bandwidth(torch)
     log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline(main_res["past"], main_res["window"])
+        log("[bench] cpu baseline (decode-32k)")
+        cpu = cpu_baseline(head["past"], head["window"], dist="outliers")
         log(f"[bench] cpu: {cpu}")
 
-    us_step, gbs = main_res["us_per_step"], main_res["gbs"]
-    achieved = main_res["decode_gbs"]
-    traffic = measured_traffic(args.workload)
+    us_step, gbs = head["us_per_step"], head["gbs"]
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -574,29 +734,24 @@ def main():
         "storage_dtype": "f16",
         "data": "synthetic, seeded: fp16 Q N(0,1), K/V as the workload states",
         "config": {
-            "workload": main_res["desc"],
+            "workload": head["desc"],
             "batch": 1, "n_heads": H, "n_kv_heads": HKV, "head_dim": D,
-            "past": main_res["past"], "window": main_res["window"],
-            "layers": main_res["layers"], "decode_splits": main_res["splits"],
-            "timing": "one HIP graph replay of `steps` steps, hipEvents",
+            "past": head["past"], "window": head["window"],
+            "layers": head["layers"], "decode_splits": head["splits"],
+            "timing": "median of 3 HIP graph replays of exactly `steps` append+attend steps "
+                      "each, hipEvents on the launching stream",
         },
-        "eager_us_per_step": round(main_res["eager_us_per_step"], 3),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "nwd_decode_attn = decode_split_kernel + decode_merge_kernel",
-            "achieved": round(achieved, 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes": int(main_res["mean_kv_bytes"]),
-            "decode_us": round(main_res["decode_us"], 3),
-        },
+        "eager_us_per_step": round(head["eager_us_per_step"], 3),
+        "roofline": rounded(head["roofline"]),
+        "decode_call": {"us": round(head["decode_us"], 3), "gbs": round(head["decode_gbs"], 1),
+                        "frac": round(head["decode_gbs"] / HBM_PEAK_GBS, 4),
+                        "split_kernel_us": round(head["split_kernel_us"], 3)},
         "cpu_baseline": cpu,
-        "decode_32k": extra,
-        "decode_153": short,
+        "configs": {k: rounded({kk: vv for kk, vv in v.items() if kk != "mean_kv_bytes"})
+                    for k, v in configs.items()},
+        "stream_read": rounded(stream),
         "device_copy_gbs": copy_gbs,
-        "wall_s_timed": round(main_res["wall_s"], 4),
+        "wall_s_timed": round(head["wall_s"], 4),
     }
     print(json.dumps(line), flush=True)
 

@@ -181,6 +181,15 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * keys). Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
+/* Measurement hook (no counterpart in the reference, whose split/merge
+ * kernels are timed only as a whole step, bench/engine.js:70-137): while set,
+ * the split kernel of every decode call on ctx is launched so that the HIP
+ * runtime records start_event when it begins and stop_event when it ends
+ * (hipEvent_t handles created by the caller with timing enabled), which
+ * separates its duration from the merge kernel's. NULL, NULL turns it off.
+ * Not for calls under HIP graph capture. */
+int nwd_set_kernel_events(nwd_ctx* ctx, void* start_event, void* stop_event);
+
 /* ---------------------------------------------------------------------
  * 4-bit projections around the path: the producer of q / k / v and the
  * consumer of the attention output.

@@ -20,6 +20,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libnwd_attn.so"
+BENCH_LIB = PKG / "lib" / "libnwd_bench.so"  # measurement kernels for bench.py
 ADDON = PKG / "lib" / "nwd_napi.node"
 INCLUDE = PKG.parent / "include"
 NODE_INCLUDE = Path(os.environ.get("NODE_INCLUDE", "/usr/include/node"))
@@ -73,7 +74,21 @@ def build(jobs: int | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
     os.replace(tmp, LIB)
+    build_bench()
     return LIB
+
+
+def build_bench() -> Path:
+    """Links lib/libnwd_bench.so from csrc/bench/*.hip: kernels that only
+    bench.py uses (the stream-read ceiling), kept out of the product ABI."""
+    objs = [_compile(src) for src in sorted((CSRC / "bench").glob("*.hip"))]
+    tmp = BENCH_LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"bench library link failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, BENCH_LIB)
+    return BENCH_LIB
 
 
 def build_addon() -> Path | None:

@@ -24,6 +24,8 @@ struct nwd_ctx {
   int device;
   int forced_splits;
   int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 default (separate)
+  void* ev_start;      // hipEvent_t pair recorded around decode split kernels, or NULL
+  void* ev_stop;
   int* status_host;    // pinned copy target of the device status word
   std::string err;
 };
@@ -143,6 +145,8 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->desc = *d;
   ctx->forced_splits = 0;
   ctx->separate_merge = -1;
+  ctx->ev_start = nullptr;
+  ctx->ev_stop = nullptr;
   ctx->shape.n_heads = d->n_heads;
   ctx->shape.n_kv = d->n_kv_heads;
   ctx->shape.group = group;
@@ -287,6 +291,8 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   // 32K keys (its one launch costs less than the in-kernel merge's serialised
   // store, ticket and record round trips).
   c.fused_merge = ctx->separate_merge == 0 ? 1 : 0;
+  c.ev_start = ctx->ev_start;
+  c.ev_stop = ctx->ev_stop;
   hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, who, e);
   return NWD_OK;
@@ -311,6 +317,15 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new, const void
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel) {
   if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_merge: ctx is NULL");
   ctx->separate_merge = separate_kernel < 0 ? -1 : (separate_kernel ? 1 : 0);
+  return NWD_OK;
+}
+
+int nwd_set_kernel_events(nwd_ctx* ctx, void* start_event, void* stop_event) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_kernel_events: ctx is NULL");
+  if ((start_event == nullptr) != (stop_event == nullptr))
+    return fail(ctx, NWD_ERR_INVALID, "nwd_set_kernel_events: give both events or neither");
+  ctx->ev_start = start_event;
+  ctx->ev_stop = stop_event;
   return NWD_OK;
 }
 

@@ -38,20 +38,22 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(
     const int32_t* __restrict__ pos, int n_tokens, int n_kv, int cap,
     int* __restrict__ status) {
   const int b = blockIdx.y;
-  const int runs_per_token = n_kv * kRunsPerRow;
-  const int i = blockIdx.x * kAppendThreads + threadIdx.x;
-  if (i >= n_tokens * runs_per_token) return;
-  const int j = i / runs_per_token;
-  const int rem = i - j * runs_per_token;
+  // 64-bit run index: n_tokens * n_kv * 16 can exceed 2^31 at the largest
+  // capacities.
+  const int64_t runs_per_token = (int64_t)n_kv * kRunsPerRow;
+  const int64_t i = (int64_t)blockIdx.x * kAppendThreads + threadIdx.x;
+  if (i >= (int64_t)n_tokens * runs_per_token) return;
+  const int j = (int)(i / runs_per_token);
+  const int rem = (int)(i - j * runs_per_token);
   const int h = rem / kRunsPerRow;
   const int run = rem - h * kRunsPerRow;
-  const int p = pos[b] + j;
+  const int64_t p = (int64_t)pos[b] + j;
   if (p < 0 || p >= cap) {  // the reference host throws here (runtime.js:448)
     atomicOr(status, kStatusBadPos);
     return;
   }
-  const int64_t src = ((int64_t)(b * n_tokens + j) * n_kv + h) * kHeadDim + run * 8;
-  const int64_t dst = cache_index(b, p, h, run * 8, n_kv, cap);
+  const int64_t src = (((int64_t)b * n_tokens + j) * n_kv + h) * kHeadDim + run * 8;
+  const int64_t dst = cache_index(b, (int)p, h, run * 8, n_kv, cap);
   f16x8 kr = load_run<kSrc16>(k_new, src);
   f16x8 vr = load_run<kSrc16>(v_new, src);
   *reinterpret_cast<f16x8*>(k_cache + dst) = kr;
@@ -63,7 +65,9 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
                             int batch, int n_tokens, int* status,
                             hipStream_t stream) {
   const int64_t runs = (int64_t)n_tokens * s.n_kv * kRunsPerRow;
-  dim3 grid((unsigned)((runs + kAppendThreads - 1) / kAppendThreads), (unsigned)batch);
+  const int64_t blocks = (runs + kAppendThreads - 1) / kAppendThreads;
+  if (blocks > 0x7FFFFFFF) return hipErrorInvalidValue;  // beyond the grid's x range
+  dim3 grid((unsigned)blocks, (unsigned)batch);
   if (s.kv16) {
     kv_append_kernel<true><<<grid, kAppendThreads, 0, stream>>>(
         k_new, v_new, static_cast<f16*>(k_cache), static_cast<f16*>(v_cache), pos,

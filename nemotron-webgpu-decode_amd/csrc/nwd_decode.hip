@@ -6,27 +6,28 @@
 // thread streaming one whole key row (uncoalesced), and it caps the context
 // at 256 keys (:29).
 //
-// Here one 256-thread workgroup (4 wavefronts) owns (sequence b, KV head
-// hkv, split s): it loads each K/V row of its key range once and serves all G
-// query heads of the group from it. When one split and few sequences leave
-// the chip nearly idle, the launch instead gives each query head its own
-// workgroup (kQsub = G workgroups per KV head, each serving one head), which
-// shortens every workgroup's serial chain G-fold.
+// Here one workgroup owns (sequence b, KV head hkv, split s): it loads each
+// K/V row of its key range once and serves all G query heads of the group
+// from it. When few sequences leave the chip nearly idle, the launch instead
+// gives each query head its own workgroups (kQsub = G workgroups per KV head,
+// each serving one head), which shortens every workgroup's serial chain
+// G-fold.
 //
-// Mapping inside a wavefront: 4 rows of 16 lanes; a row owns one key at a
-// time and each lane holds 8 of its 128 dims (one 16-byte run), so one load
-// instruction reads 1 KB of consecutive keys. q.k is a packed fp16 dot
-// (v_dot2_f32_f16) or an fp32 FMA chain, summed over the row's lanes with DPP
-// moves, so every lane of the row holds the score. Each row runs its own
-// online softmax (running max and sum in log2 units, exp2 on the hardware)
-// and accumulates p * V for its dims in fp32 with no cross-lane traffic. The
-// next iteration's K/V loads are issued before the current one is computed,
-// unconditionally, so the wait before the compute only waits for the older
-// loads; they go through buffer descriptors that end at the split's last key,
-// so the prefetch past the end reads zeros without a memory round trip. At
-// the end the row states are merged
-// (shuffles inside a wave, LDS across waves) into one record (m, l, o[128])
-// per query head.
+// Mapping inside a wavefront: rows of kLanes lanes (16 or 8); a row owns one
+// key at a time and each lane holds 128 / kLanes of its dims (one or two
+// 16-byte runs), so one load instruction reads 1 KB of consecutive keys. q.k
+// is a packed fp16 dot (v_dot2_f32_f16) or an fp32 FMA chain, summed over the
+// row's lanes with DPP moves, so every lane of the row holds the score. Each
+// row runs its own online softmax (running max and sum in log2 units, exp2
+// on the hardware) and accumulates p * V for its dims in fp32 with no
+// cross-lane traffic. The next iteration's K/V loads are issued before the
+// current one is computed, unconditionally, so the wait before the compute
+// only waits for the older loads; they go through buffer descriptors that
+// end at the split's last key, so the prefetch past the end reads zeros
+// without a memory round trip, and they are marked non-temporal (each byte
+// is read once). At the end the row states are merged (DPP and lane swaps
+// inside a wave, LDS across waves) into one record (m, l, o[128]) per query
+// head.
 //
 // With one split the record is normalised and written to `out`. With
 // several, records go to the workspace and decode_merge_kernel combines them
@@ -36,10 +37,7 @@
 // the split kernel itself: records are written through to memory (vector
 // stores with the agent-coherent cache policy sc1) and the workgroup that
 // takes the last arrival ticket of its (b, hkv) reads them with sc1 loads
-// and merges them. That saves the second launch but adds serialised memory
-// round trips at the end of every workgroup. A release fence per workgroup
-// instead of the write-through stores would cost a full L2 write-back each
-// (~0.15 us, serialised on MI355X).
+// and merges them.
 //
 // The key range is partitioned from the host's length bound (max_len), not
 // from the device position, so a workgroup's first K/V loads do not wait for
@@ -50,38 +48,35 @@
 // the new position writes them into the caches and uses them from registers,
 // so an attention-layer step (kv_append x2 + attention in the reference,
 // engine/runtime.js:389-391) is one launch.
+#include <hip/hip_ext.h>
+
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
 namespace nwd {
 
-// Keys per row per iteration, a build-time tuning constant: 2 is the
-// measured best on MI355X (append + attend per step with one workgroup per
-// KV head; 4 and 8 keys: 7.07 and 8.23 us at 153 keys against 6.29, 11.3
-// and 13.3 at 4K against 10.2, 31.1 and 32.7 at 32K against 29.9; 1 key:
-// 10.4 at 4K against 10.1, 34.6 at 32K against 29.4).
-#ifndef NWD_DECODE_KEYS_PER_ROW
-#define NWD_DECODE_KEYS_PER_ROW 2
-#endif
-
-// Four wavefronts per workgroup (eight measured slower at 4K and 32K);
-// merge_group's thread mapping assumes these 256 threads.
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
-
-
-template <int G> struct DecodeCfg {
-  static constexpr int kLanes = 16;               // lanes per key row
-  static constexpr int kRows = 64 / kLanes;       // key rows per wavefront
-  static constexpr int kRuns = 16 / kLanes;       // 16-byte runs per lane per key
-  static constexpr int kDims = 8 * kRuns;          // dims per lane
-  static constexpr int kKpr = NWD_DECODE_KEYS_PER_ROW;  // keys per row per iteration
-  static constexpr int kBlockKeys = kWaves * kRows * kKpr;
+// Shape of one split workgroup: kW wavefronts, rows of kL lanes per key,
+// kKpr keys per row per iteration, kT iterations' tiles in flight.
+template <int kW, int kL, int kKpr_, int kT>
+struct DecodeCfg {
+  static constexpr int kTiles = kT;
+  static constexpr int kWaves = kW;
+  static constexpr int kThreads = kW * 64;
+  static constexpr int kLanes = kL;               // lanes per key row
+  static constexpr int kRows = 64 / kL;           // key rows per wavefront
+  static constexpr int kRuns = 16 / kL;           // 16-byte runs per lane per key
+  static constexpr int kDims = 8 * kRuns;         // dims per lane
+  static constexpr int kKpr = kKpr_;              // keys per row per iteration
+  static constexpr int kWaveKeys = kRows * kKpr;  // keys per wavefront per iteration
+  static constexpr int kBlockKeys = kW * kWaveKeys;
+  static_assert(kL == 8 || kL == 16, "rows of 8 or 16 lanes");
 };
 
-// Units the key range is split in (the largest block size, 128 keys).
+// Units the key range is split in (128 keys).
 constexpr int kUnitKeys = 128;
 
+// Sum over each aligned group of N lanes (N = 8 or 16); every lane of the
+// group gets it.
 template <int N>
 __device__ inline float sum_lanes(float x) {
   x += dpp_mov<kDppQuadXor1>(x);
@@ -89,6 +84,19 @@ __device__ inline float sum_lanes(float x) {
   x += dpp_mov<kDppHalfMirror>(x);
   if constexpr (N == 16) x += dpp_mov<kDppRowMirror>(x);
   return x;
+}
+
+// Max / sum of the lanes holding the same dims in every row of a wavefront
+// (rows of N lanes: lanes l, l ^ N, ... up to l ^ 32).
+template <int N>
+__device__ inline float max_rows(float x) {
+  if constexpr (N == 8) x = fmaxf(x, dpp_mov<kDppRowRor8>(x));
+  return max_xor32(max_xor16(x));
+}
+template <int N>
+__device__ inline float sum_rows(float x) {
+  if constexpr (N == 8) x += dpp_mov<kDppRowRor8>(x);
+  return sum_xor32(sum_xor16(x));
 }
 
 // One 16-byte run (8 values) of a new K/V row, fp16 or fp32, loaded as raw
@@ -129,14 +137,18 @@ __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 // Splits the merge reads per pass: all loads of a pass are issued together,
 // one memory round trip (one pass for the usual 32 splits or fewer).
 constexpr int kMergeChunk = 32;
+// Threads that take part in a merge (the first 256 of the workgroup).
+constexpr int kMergeThreads = 256;
 
 // LDS floats merge_group uses: the per-wave partial outputs [4][G][32] x 4,
 // one (m, l) pair per thread and the pass's head max / sum [G] each.
-template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) + 2 * kThreads; }
+template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) + 2 * kMergeThreads; }
 
 // Merges the nsplit records of the G heads of one (b, hkv) and writes the
-// normalised outputs. Thread t owns the 4-dim run d4 = t % 32 of every head,
-// for the splits s = j, j + 8, ... of a pass (j = t / 32). Per pass:
+// normalised outputs. Called by every thread of the workgroup (256 or
+// more); threads t < 256 do the work. Thread t owns the 4-dim run
+// d4 = t % 32 of every head, for the splits s = j, j + 8, ... of a pass
+// (j = t / 32). Per pass:
 //   1. every (m, l) pair and every o run of the pass is requested at once;
 //   2. the (m, l) pairs go to LDS, and two heads per wavefront reduce their
 //      32 entries to the pass max Mp and sum Lp = sum l * 2^(m - Mp);
@@ -148,15 +160,15 @@ template <int G, bool kO16, int kPolicy>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
                                    int64_t hrow0, int nsplit, float* lds) {
-  static_assert(kThreads == 256, "merge_group maps 8 groups of 32 threads");
-  static_assert(G * kMergeChunk <= kThreads, "one (m, l) pair per thread per pass");
+  static_assert(G * kMergeChunk <= kMergeThreads, "one (m, l) pair per thread per pass");
   constexpr int kPer = kMergeChunk / 8;  // splits per thread per head per pass
   const int t = threadIdx.x;
+  const bool act = t < kMergeThreads;
   const int lane = t & 63, wave = t >> 6;
-  const int d4 = t & 31, j = t >> 5;
+  const int d4 = t & 31, j = (t >> 5) & 7;
   f32x4* lds_acc = reinterpret_cast<f32x4*>(lds);               // [4][G][32]
-  float2* lds_ml = reinterpret_cast<float2*>(lds + G * 512);     // [kThreads]: [G][kMergeChunk], unused
-  float* lds_mp = lds + G * 512 + 2 * kThreads;                 // [G]
+  float2* lds_ml = reinterpret_cast<float2*>(lds + G * 512);     // [kMergeThreads]: [G][kMergeChunk], unused
+  float* lds_mp = lds + G * 512 + 2 * kMergeThreads;            // [G]
   float* lds_lp = lds_mp + G;                                   // [G]
   const int64_t rec0 = hrow0 * nsplit;  // record (g, s) is rec0 + g * nsplit + s
   const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(part_ml + rec0), 0,
@@ -175,7 +187,7 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
   for (int s0 = 0; s0 < nsplit; s0 += kMergeChunk) {
     const int ns = min(kMergeChunk, nsplit - s0);
     // 1. Loads (indexes clamped in range; entries past the pass get no weight).
-    const int mg = t / kMergeChunk, ms = t % kMergeChunk;
+    const int mg = (t & (kMergeThreads - 1)) / kMergeChunk, ms = t % kMergeChunk;
     const bool mvalid = mg < G && ms < ns;
     const float2 mlv = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
         r_ml, (min(mg, G - 1) * nsplit + s0 + min(ms, ns - 1)) * 8, 0, kPolicy));
@@ -190,11 +202,11 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
             r_o, ((g * nsplit + s) * kHeadDim + d4 * 4) * 4, 0, kPolicy));
       }
     // 2. Pass max and sum per head.
-    lds_ml[t] = mvalid ? mlv : make_float2(kNegBig, 0.f);
+    if (act) lds_ml[t] = mvalid ? mlv : make_float2(kNegBig, 0.f);
     __syncthreads();
     {
       const int g = 2 * wave + (lane >> 5);
-      if (g < G) {
+      if (act && g < G) {
         const float2 e = lds_ml[g * kMergeChunk + (lane & 31)];
         const float mp = max32(e.x);
         const float lp = sum32(e.y * fast_exp2(e.x - mp));
@@ -228,7 +240,7 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
   for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[g][i] = sum_xor32(acc[g][i]);
-    if (lane < 32) lds_acc[(wave * G + g) * 32 + d4] = acc[g];
+    if (act && lane < 32) lds_acc[(wave * G + g) * 32 + d4] = acc[g];
   }
   __syncthreads();
   if (t < G * 32) {
@@ -273,12 +285,13 @@ struct DecodeArgs {
 
 // kQsub workgroups per KV head, each serving G of its query heads (kQsub = 1:
 // one workgroup serves the whole group).
-template <int G, bool kQ16, bool kO16, int kQsub>
-__global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeArgs a) {
-  using C = DecodeCfg<G>;
+template <int G, bool kQ16, bool kO16, int kQsub, class C>
+__global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeArgs a) {
+  constexpr int kWaves = C::kWaves, kThreads = C::kThreads;
   constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
-  constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys;
-  constexpr int kWaveKeys = kRows * kKpr;
+  constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
+  constexpr int kTiles = C::kTiles;
+  static_assert(kThreads >= kMergeThreads, "merge_group needs 256 threads");
   constexpr int kMergeFloats = merge_lds_floats<G>();
   constexpr int kWaveFloats = kWaves * G * (kHeadDim + 2);
   constexpr int kLdsFloats = kMergeFloats > kWaveFloats ? kMergeFloats : kWaveFloats;
@@ -336,9 +349,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
         tl.k[j][i] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + i * kLanes * 16, 0, 0));
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + i * kLanes * 16, 0, kStreamPolicy));
         tl.v[j][i] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off + i * kLanes * 16, 0, 0));
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off + i * kLanes * 16, 0, kStreamPolicy));
       }
     }
   };
@@ -347,20 +360,28 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // raw) before its first tile, and before the position says which split
   // owns them, so that converting them later never waits for a tile.
   const bool has_new = a.k_new != nullptr;
-  SrcRun nk_raw, nv_raw;
+  SrcRun nk_raw[kRuns], nv_raw[kRuns];
   if (has_new) {
-    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim + col * 8;
-    nk_raw = load_src_run_raw(a.k_new, src, a.new16);
-    nv_raw = load_src_run_raw(a.v_new, src, a.new16);
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim + (col + i * kLanes) * 8;
+      nk_raw[i] = load_src_run_raw(a.k_new, src, a.new16);
+      nv_raw[i] = load_src_run_raw(a.v_new, src, a.new16);
+    }
   }
 
-  // The first tile is requested before the position is known, over the keys
-  // this split can own: up to the host bound, or up to the capacity for the
-  // last split (which absorbs keys past the bound).
-  Tile ta, tb;
+  // The first kTiles - 1 tiles are requested before the position is known,
+  // over the keys this split can own: up to the host bound, or up to the
+  // capacity for the last split (which absorbs keys past the bound). They may
+  // therefore hold cache rows at or past L, which the reference never reads;
+  // their V runs are zeroed before use (a stale Inf or NaN times a zero
+  // weight would be NaN). Later tiles are bounded by the split's last key.
+  Tile tr[kTiles];
   {
     const int own_end = split == nsplit - 1 ? a.cap : t1h;
-    load_tile(ta, slab_rsrc(a.k_cache, own_end), slab_rsrc(a.v_cache, own_end), 0);
+    const auto ek = slab_rsrc(a.k_cache, own_end), ev = slab_rsrc(a.v_cache, own_end);
+#pragma unroll
+    for (int t = 0; t < kTiles - 1; ++t) load_tile(tr[t], ek, ev, t);
   }
 
   // Query registers: this lane's dims of each of the G heads.
@@ -402,11 +423,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // end of the kernel.
   const int pnew = L - 1;
   const bool owns_new = has_new && pos_ok && t0 <= pnew && pnew < t1;
-  static_assert(kRuns == 1, "one 16-byte run per lane");
+  // Only the iteration whose tile holds the new key substitutes it: a
+  // substitution in every tile lengthened the owning workgroup's chain, the
+  // critical path of the whole launch (32K keys: 28.8 against 25.8 us per
+  // step with and without the append).
+  const int it_new = owns_new ? (pnew - t0) / kBlockKeys : -1;
   f16x8 nk[kRuns], nv[kRuns];
   if (owns_new) {
-    nk[0] = convert_src_run(nk_raw, a.new16);
-    nv[0] = convert_src_run(nv_raw, a.new16);
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      nk[i] = convert_src_run(nk_raw[i], a.new16);
+      nv[i] = convert_src_run(nv_raw[i], a.new16);
+    }
   }
 
   auto qk = [&](const Tile& tl, int j, int g) -> float {
@@ -438,7 +466,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
 
   auto compute_tile = [&](Tile& tl, int it) {
     const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
-    if (owns_new) {
+    if (it == it_new) {
 #pragma unroll
       for (int j = 0; j < kKpr; ++j) {
         const bool sub = base + j * kRows == pnew;
@@ -446,6 +474,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
         for (int i = 0; i < kRuns; ++i) {
           tl.k[j][i] = sub ? nk[i] : tl.k[j][i];
           tl.v[j][i] = sub ? nv[i] : tl.v[j][i];
+        }
+      }
+    }
+    if (it < kTiles - 1) {  // early tiles' rows at or past t1 may be stale cache rows
+#pragma unroll
+      for (int j = 0; j < kKpr; ++j) {
+        const bool valid = base + j * kRows < t1;
+#pragma unroll
+        for (int i = 0; i < kRuns; ++i) {
+          const u32x4 w = __builtin_bit_cast(u32x4, tl.v[j][i]);
+          tl.v[j][i] = __builtin_bit_cast(f16x8, valid ? w : u32x4{0u, 0u, 0u, 0u});
         }
       }
     }
@@ -493,28 +532,27 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
     }
   };
 
-  // Two register tiles; the loads of iteration it+1 are in flight while
-  // iteration it is computed. The first tile is requested before the
-  // position arrives.
+  // A ring of kTiles register tiles: the loads of iterations it+1 ..
+  // it+kTiles-1 are in flight while iteration it is computed.
   if (n_it > 0) {
-    for (int it = 0; it < n_it; it += 2) {
-      load_tile(tb, rk, rv, it + 1);
-      compute_tile(ta, it);
-      load_tile(ta, rk, rv, it + 2);
-      if (it + 1 < n_it) compute_tile(tb, it + 1);
+    for (int it0 = 0; it0 < n_it; it0 += kTiles) {
+#pragma unroll
+      for (int t = 0; t < kTiles; ++t) {
+        load_tile(tr[(t + kTiles - 1) % kTiles], rk, rv, it0 + t + kTiles - 1);
+        if (t == 0 || it0 + t < n_it) compute_tile(tr[t], it0 + t);
+      }
     }
   }
 
-  // Merge the 4 row states of this wavefront (rows of 16 lanes: lane ^ 16
-  // and lane ^ 32 hold the same dims of the other rows).
-  static_assert(kLanes == 16, "row merge assumes 16-lane rows");
+  // Merge the row states of this wavefront: the lanes l, l ^ kLanes, ...
+  // hold the same dims of the other rows.
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float M = max_xor32(max_xor16(m[g]));
+    const float M = max_rows<kLanes>(m[g]);
     const float sc = fast_exp2(m[g] - M);
-    l[g] = sum_xor32(sum_xor16(l[g] * sc));
+    l[g] = sum_rows<kLanes>(l[g] * sc);
 #pragma unroll
-    for (int i = 0; i < kDims; ++i) acc[g][i] = sum_xor32(sum_xor16(acc[g][i] * sc));
+    for (int i = 0; i < kDims; ++i) acc[g][i] = sum_rows<kLanes>(acc[g][i] * sc);
     m[g] = M;
   }
   if (row == 0) {
@@ -586,11 +624,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
       }
     }
   }
-  // The new rows go to the caches last: lanes 0-15 hold the 16 runs of the
-  // new K row in nk, lanes 16-31 those of the new V row in nv.
-  if (owns_new && tid < 32 && blockIdx.y % kQsub == 0) {
-    f16* dst = (tid < 16 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim + col * 8;
-    *reinterpret_cast<f16x8*>(dst) = tid < 16 ? nk[0] : nv[0];
+  // The new rows go to the caches last: the lanes of row 0 of wavefront 0
+  // hold the 16 runs of the new K row in nk, those of row 1 the V row's.
+  if (owns_new && wave == 0 && row < 2 && blockIdx.y % kQsub == 0) {
+#pragma unroll
+    for (int i = 0; i < kRuns; ++i) {
+      f16* dst = (row == 0 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim +
+                 (col + i * kLanes) * 8;
+      *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
+    }
   }
   if (nsplit == 1 || !a.fused_merge) return;
 
@@ -598,10 +640,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   // group) merges: one counter per (b, blockIdx.y), i.e. per (b, hkv), or per
   // (b, query head) in the per-query-head form, where batch x n_heads fits
   // the counters (the host keeps at least kSubSplitMaxWorkgroups of them).
-  // Each thread's record stores are complete (device-coherent)
-  // before the barrier, and the ticket is taken after it; the merging
-  // workgroup reads the records with device-scope loads. Nothing waits on
-  // another workgroup.
+  //
+  // Ordering (the AMDGPU memory model for gfx942-family targets, which
+  // gfx950 follows): an agent-scope release is "write back dirty L2 lines,
+  // wait for the stores", an agent-scope acquire is "agent-scope load, then
+  // invalidate L2". The records are the only data handed over, and they are
+  // stored and loaded with the agent-scope cache policy sc1 itself, so they
+  // leave no dirty L2 line behind and no stale L2 line can serve them: the
+  // release reduces to waiting for this thread's record stores (vmcnt(0))
+  // before the barrier that precedes the ticket, and the acquire to the sc1
+  // loads in merge_group, which are issued only after the ticket has
+  // returned (they depend on it through lds_last).
   __shared__ int lds_last;
   int* const counter = &a.counters[b * (a.n_kv * kQsub) + blockIdx.y];
   wait_vm();
@@ -612,8 +661,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
   if (!lds_last) return;
-  // The records are read with agent-coherent loads (cache policy sc1), so
-  // they see what the other workgroups wrote through before their tickets.
   merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
   if (tid == 0)
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -622,9 +669,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_split_kernel(const DecodeA
 // Separate merge: one 256-thread workgroup per (query head, sequence), the
 // head's records being those of a group of one. Four times the workgroups
 // of a per-KV-head merge, each with a quarter of the loads: 9.7 against
-// 10.8 us per 4K decode.
+// 10.8 us per 4K decode. (One thread per output dim looping over the splits,
+// with no LDS or barrier, measured slower: 9.9 against 9.35 us at 4K.)
 template <bool kO16>
-__global__ __launch_bounds__(kThreads) void decode_merge_kernel(
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float2* __restrict__ part_ml,
     void* __restrict__ out, int n_heads, int nsplit) {
   __shared__ __attribute__((aligned(16))) float lds[merge_lds_floats<1>()];
@@ -632,22 +680,50 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(
   merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds);
 }
 
+// The split workgroup's shape, from sweeps on MI355X (decode-only, per call,
+// 32K / 4K / 153 keys): 4 wavefronts, 16-lane rows, 2 keys per row, 2 tiles
+// in flight: 26.5-27.5 / 9.2-9.4 / 4.6 us. Eight wavefronts (two per SIMD):
+// 28.5 / 10.6 / 5.0; 8-lane rows (fewer reduction and softmax instructions
+// per key, twice the accumulators): 28.0-28.5 / 10.5-10.7 / 4.9-5.0; 3 or 4
+// tiles in flight: 27.4-27.5 / 9.9-10.3 / 4.7-4.9. The loop is bound by HBM
+// (the K/V stream alone, with the compute removed, runs at the rate of a
+// plain read of the same pattern, ~6.2 TB/s), so more work in flight only
+// lengthens the latency of each load.
+using SplitCfg = DecodeCfg<4, 16, 2, 2>;
+
 template <int G, bool kQ16, bool kO16, int kQsub>
-static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream) {
+static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, void* ev_start,
+                           void* ev_stop) {
+  using C = SplitCfg;
   dim3 grid((unsigned)a.nsplit, (unsigned)(a.n_kv * kQsub), (unsigned)batch);
-  decode_split_kernel<G, kQ16, kO16, kQsub><<<grid, kThreads, 0, stream>>>(a);
-  hipError_t e = hipGetLastError();
+  hipError_t e;
+  if (ev_start || ev_stop) {
+    // Measurement: the runtime records the events when the split kernel
+    // starts and when it ends.
+    DecodeArgs arg = a;
+    void* args[] = {&arg};
+    e = hipExtLaunchKernel(reinterpret_cast<const void*>(&decode_split_kernel<G, kQ16, kO16, kQsub, C>),
+                           grid, dim3(C::kThreads), args, 0, stream, (hipEvent_t)ev_start,
+                           (hipEvent_t)ev_stop, 0);
+  } else {
+    decode_split_kernel<G, kQ16, kO16, kQsub, C><<<grid, C::kThreads, 0, stream>>>(a);
+    e = hipGetLastError();
+  }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
-  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kThreads, 0, stream>>>(
+  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kMergeThreads, 0, stream>>>(
       a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit);
   return hipGetLastError();
 }
 
 template <int G, int kQsub = 1>
-static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, int batch, hipStream_t st) {
+static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
+                            hipStream_t st) {
+  const int B = c.batch;
   if (s.q16)
-    return s.o16 ? launch_g<G, true, true, kQsub>(a, batch, st) : launch_g<G, true, false, kQsub>(a, batch, st);
-  return s.o16 ? launch_g<G, false, true, kQsub>(a, batch, st) : launch_g<G, false, false, kQsub>(a, batch, st);
+    return s.o16 ? launch_g<G, true, true, kQsub>(a, B, st, c.ev_start, c.ev_stop)
+                 : launch_g<G, true, false, kQsub>(a, B, st, c.ev_start, c.ev_stop);
+  return s.o16 ? launch_g<G, false, true, kQsub>(a, B, st, c.ev_start, c.ev_stop)
+               : launch_g<G, false, false, kQsub>(a, B, st, c.ev_start, c.ev_stop);
 }
 
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
@@ -681,19 +757,19 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   // 1088 with 8 splits). Same bits.
   if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
     switch (s.group) {
-      case 2: return launch_qo<1, 2>(s, a, c.batch, stream);
-      case 4: return launch_qo<1, 4>(s, a, c.batch, stream);
-      case 5: return launch_qo<1, 5>(s, a, c.batch, stream);
-      case 8: return launch_qo<1, 8>(s, a, c.batch, stream);
+      case 2: return launch_qo<1, 2>(s, a, c, stream);
+      case 4: return launch_qo<1, 4>(s, a, c, stream);
+      case 5: return launch_qo<1, 5>(s, a, c, stream);
+      case 8: return launch_qo<1, 8>(s, a, c, stream);
       default: break;  // group 1 is already one workgroup per query head
     }
   }
   switch (s.group) {
-    case 1: return launch_qo<1>(s, a, c.batch, stream);
-    case 2: return launch_qo<2>(s, a, c.batch, stream);
-    case 4: return launch_qo<4>(s, a, c.batch, stream);
-    case 5: return launch_qo<5>(s, a, c.batch, stream);
-    case 8: return launch_qo<8>(s, a, c.batch, stream);
+    case 1: return launch_qo<1>(s, a, c, stream);
+    case 2: return launch_qo<2>(s, a, c, stream);
+    case 4: return launch_qo<4>(s, a, c, stream);
+    case 5: return launch_qo<5>(s, a, c, stream);
+    case 8: return launch_qo<8>(s, a, c, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -41,6 +41,8 @@ struct DecodeCall {
   int nsplit;
   int span;  // host bound on the keys attended (max_len), partitions the splits
   int fused_merge;  // merge in the split kernel (else a separate merge kernel)
+  void* ev_start;   // optional hipEvent_t pair recorded around the split kernel
+  void* ev_stop;
 };
 
 hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new,

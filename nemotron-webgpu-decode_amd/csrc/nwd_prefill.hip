@@ -159,7 +159,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     qi[rb] = ok ? R / G : 0;
     gq[rb] = ok ? R - qi[rb] * G : 0;
     lim[rb] = ok ? P0 + qi[rb] : -1;
-    const int64_t qrow = ((int64_t)(b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * kHeadDim;
+    const int64_t qrow = (((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       if (ok) {
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     const float M = fmaxf(m[rb], x[0]);
     const float a0 = fast_exp2((m[rb] - M) * c), a1 = fast_exp2((x[0] - M) * c);
     const float lt = lsum[rb] * a0 + x[1] * a1;
-    const int64_t grow = (int64_t)(b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb];
+    const int64_t grow = ((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb];
     if (a.nsplit == 1) {
       const float inv = 1.f / lt;
 #pragma unroll

@@ -486,9 +486,6 @@ hipError_t launch_gemv_slots(const float* x, const Q4Mat& w, int n_blocks, float
 
 // Waves per column group: enough that each takes at least 32 blocks.
 int q4_split(int n_blocks) {
-#ifdef Q4_SPLIT
-  return Q4_SPLIT;
-#endif
   return n_blocks >= 128 ? 4 : (n_blocks >= 64 ? 2 : 1);
 }
 

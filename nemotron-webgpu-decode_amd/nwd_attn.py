@@ -113,6 +113,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_decode_splits": (i32, [vp, i32, i32]),
         "nwd_set_decode_splits": (ctypes.c_int, [vp, i32]),
         "nwd_set_decode_merge": (ctypes.c_int, [vp, i32]),
+        "nwd_set_kernel_events": (ctypes.c_int, [vp, vp, vp]),
         "nwd_q4_gemv": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight), vp, i32, i32, vp]),
         "nwd_qkv_append": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight),
                                           ctypes.POINTER(NwdQ4Weight), ctypes.POINTER(NwdQ4Weight),
@@ -213,6 +214,11 @@ class AttnContext:
         kernel's last workgroup; None: the default (the separate kernel)."""
         v = -1 if separate_kernel is None else int(bool(separate_kernel))
         self._check(self.lib.nwd_set_decode_merge(self.handle, v))
+
+    def set_kernel_events(self, start, stop):
+        """hipEvent_t handles (ints) recorded around every later decode call's
+        split kernel; None, None turns it off."""
+        self._check(self.lib.nwd_set_kernel_events(self.handle, start, stop))
 
     # ------------------------------------------------------------ operations
     def kv_append(self, k_new, v_new, k_cache, v_cache, pos, batch: int, n_tokens: int = 1,

@@ -209,7 +209,11 @@ def test_config3_past32768_outliers_split_k():
 
 
 def test_config4_ragged_batch64():
-    """64 sequences, past lengths U{512..16384}, one query each."""
+    """64 sequences, past lengths U{512..16384}, one query each: one new token
+    per sequence appended at pos = past and attended, both as nwd_kv_append +
+    nwd_decode_attn and as the fused nwd_append_decode the benchmark times.
+    The fused path writes the same cache bits and gives the same output bits;
+    every sequence matches the oracle."""
     H, Hkv, B = 32, 8, 64
     g = rng(4)
     past = g.integers(512, 16385, size=B)
@@ -218,9 +222,20 @@ def test_config4_ragged_batch64():
     kc = randn_f16((B, Hkv, cap, D), 40)
     vc = randn_f16((B, Hkv, cap, D), 41)
     q = randn_f16((B, H, D), 42)
+    kn = randn_f16((B, Hkv, D), 43)
+    vn = randn_f16((B, Hkv, D), 44)
+    pos = pos_tensor(past.tolist())
     with nw.AttnContext(H, Hkv, cap, max_batch=B) as ctx:
-        out = _decode(ctx, q, kc, vc, pos_tensor(past.tolist()), B, max_len=cap)
+        kc2, vc2 = kc.clone(), vc.clone()
+        ctx.kv_append(kn[:, None], vn[:, None], kc, vc, pos, B, 1)
+        out = _decode(ctx, q, kc, vc, pos, B, max_len=cap)
+        say("config4 fused append_decode B=64")
+        fused = torch.empty((B, H, D), dtype=torch.float16, device="cuda")
+        ctx.append_decode(q, kn, vn, kc2, vc2, pos, fused, B, cap)
         assert ctx.device_status() == nw.NWD_OK
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc)  # appended rows bit-exact
+        fused = fused.float().cpu().numpy()
+    assert np.array_equal(fused, out)
     qh = q.float().cpu().numpy()
     worst = 0.0
     for b in range(B):
@@ -229,6 +244,55 @@ def test_config4_ragged_batch64():
                                       threads=0)
         worst = max(worst, max_abs(out[b], want))
     assert worst < TOL, worst
+
+
+@pytest.mark.parametrize("fill", [0x7E00, 0x7C00, 0xFC00])
+def test_stale_rows_past_length_do_not_leak(fill):
+    """Cache rows at or past L are never read by the reference (it loops
+    t < seq, kernels/sparse_attn.wgsl:45-113) and may hold anything, e.g.
+    NaN or Inf in an uncleared cache. The output must be bit-identical to
+    that of a zero-filled cache, for every decode form: one split (one
+    workgroup per query head), several splits, per-KV-head workgroups (B=9),
+    both merge forms, and the fused append, with L - t0 < 32 for the split
+    holding the last key."""
+    Hkv, H, cap = 8, 32, 1100
+    g = rng(500 + fill % 97)
+    for L in (1, 5, 31, 129, 150, 257, 1025, 1057):
+        for B in (1, 9):
+            rows = [kv_rows(g, L, Hkv) for _ in range(B)]
+            q = normal_f16(g, (B, H, D))
+            kn = normal_f16(g, (B, Hkv, D))
+            vn = normal_f16(g, (B, Hkv, D))
+            base_k = to_cache([r[0] for r in rows], Hkv, cap)
+            base_v = to_cache([r[1] for r in rows], Hkv, cap)
+            stale_k, stale_v = base_k.copy(), base_v.copy()
+            stale_k[:, :, L:, :] = np.uint16(fill).view(np.float16)
+            stale_v[:, :, L:, :] = np.uint16(fill).view(np.float16)
+            pos = pos_tensor([L - 1] * B)
+            caches = [(dev(base_k), dev(base_v)), (dev(stale_k), dev(stale_v))]
+            with nw.AttnContext(H, Hkv, cap, max_batch=B, o_dtype="f32") as ctx:
+                for n in (0, 1, 3, 8):
+                    for sep in (True, False):
+                        for max_len in (L, 0):
+                            say(f"stale rows fill={fill:#06x} L={L} B={B} splits={n} "
+                                f"separate={sep} max_len={max_len}")
+                            ctx.set_decode_splits(n)
+                            ctx.set_decode_merge(sep)
+                            outs = []
+                            for kcd, vcd in caches:
+                                o1 = _decode(ctx, dev(q), kcd, vcd, pos, B, torch.float32,
+                                             max_len=max_len)
+                                o2 = torch.empty((B, H, D), dtype=torch.float32, device="cuda")
+                                ctx.append_decode(dev(q), dev(kn), dev(vn), kcd.clone(), vcd.clone(),
+                                                  pos, o2, B, max_len)
+                                outs.append((o1, host(o2)))
+                            assert np.all(np.isfinite(outs[0][0])) and np.all(np.isfinite(outs[0][1]))
+                            key = (L, B, n, sep, max_len)
+                            assert np.array_equal(outs[0][0], outs[1][0]), key
+                            assert np.array_equal(outs[0][1], outs[1][1]), key
+                assert ctx.device_status() == nw.NWD_OK
+            want = oracle.sparse_attn_f32(f32(q[0]), f32(rows[0][0]), f32(rows[0][1]))
+            assert max_abs(outs[1][0][0], want) < TOL, L
 
 
 @pytest.mark.parametrize("L", [1, 2, 63, 64, 65, 127, 128, 129, 1000, 5000])
