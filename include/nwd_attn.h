@@ -145,6 +145,27 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new,
                       const int32_t* pos, void* out, int32_t batch,
                       int32_t max_len, void* stream);
 
+/* Allocation-free form of nwd_append_decode, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc. It has no counterpart in the reference,
+ * whose engine allocates everything once up front (engine/runtime.js:109-211).
+ * It takes the descriptor instead of a context and needs no nwd_create: the
+ * split-K records live in a static 16 MiB device array of the library (one
+ * per GPU, held until the process ends), so a call whose records would not
+ * fit (batch * n_heads * splits > 32262 when it splits) fails with
+ * NWD_ERR_CAPACITY before any launch. The merge always runs as a separate
+ * kernel. Results are bit-identical to nwd_append_decode on a context made
+ * from the same descriptor (default merge form, automatic split count).
+ * status, if not NULL, is a caller-owned device int32 that gets bit 1 OR-ed
+ * in when a position is outside [0, max_seq) (nothing is written there and
+ * attention is clamped, as in nwd_append_decode); with NULL such a position
+ * is not reported. All calls on one GPU share its scratch: calls that may
+ * run at the same time on one GPU (on different streams) race. */
+int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k_new,
+                              const void* v_new, void* k_cache, void* v_cache,
+                              const int32_t* pos, void* out, int32_t batch,
+                              int32_t max_len, int32_t* status, void* stream);
+
 /* Causal chunked prefill; replaces the token-by-token prefill of
  * engine/runtime.js:640-643 (each prompt token runs kv_append then
  * sparse_attn). The n_new new rows must already be in the caches at tokens

@@ -11,11 +11,21 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/nwd_attn.h"
 #include "nwd_common.h"
 #include "nwd_internal.h"
+
+// Device scratch of nwd_append_decode_noalloc: a status word, then the
+// split-K records (m, l) and o[128] of the calls that split. It is a static
+// device array, so each GPU that loads the library holds its own copy until
+// the process ends; the entry point allocates nothing. Host code never uses
+// the name `scratch` as an address (on the host it only names the symbol):
+// the device address comes from hipGetSymbolAddress, once per device.
+constexpr size_t kScratchBytes = (size_t)16 << 20;
+static __device__ __attribute__((aligned(256))) unsigned char scratch[kScratchBytes];
 
 struct nwd_ctx {
   nwd_desc desc;
@@ -78,9 +88,9 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
 // beyond, enough splits to fill the chip, even where that leaves splits with
 // no 128-key unit (an empty split costs less than the unused CUs: 8.0-8.9
 // against 8.5-9.7 us per step from 384 to 2048 keys). Measured on MI355X.
-int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
+int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   const int units = (max_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
-  const int64_t heads = (int64_t)batch * ctx->desc.n_heads;
+  const int64_t heads = (int64_t)batch * n_heads;
   if (heads <= nwd::kSubSplitMaxWorkgroups) {
     if (units <= 3) return 1;
     const int n = (int)(nwd::kSubSplitMaxWorkgroups / heads);
@@ -88,11 +98,61 @@ int auto_splits(const nwd_ctx* ctx, int batch, int max_len) {
   } else if (units <= 2) {
     return 1;
   }
-  const int per_wave = batch * ctx->desc.n_kv_heads;
+  const int per_wave = batch * n_kv_heads;
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
   const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work
   if (by_len > n) n = by_len;
   return n < 1 ? 1 : n;
+}
+
+// Validates a descriptor (the checks nwd_create and the allocation-free
+// entry point share); failures name `who`.
+int check_desc(const nwd_desc* d, const char* who) {
+  if (!d) return fail(nullptr, NWD_ERR_INVALID, "%s: desc is NULL", who);
+  if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->head_dim <= 0 || d->max_seq <= 0 ||
+      d->max_batch <= 0)
+    return fail(nullptr, NWD_ERR_INVALID,
+                "%s: sizes must be positive (n_heads=%d n_kv_heads=%d head_dim=%d "
+                "max_seq=%d max_batch=%d)",
+                who, d->n_heads, d->n_kv_heads, d->head_dim, d->max_seq, d->max_batch);
+  if (d->n_heads % d->n_kv_heads != 0)
+    return fail(nullptr, NWD_ERR_INVALID, "%s: n_heads %d is not a multiple of n_kv_heads %d",
+                who, d->n_heads, d->n_kv_heads);
+  const int group = d->n_heads / d->n_kv_heads;
+  if (!group_supported(group))
+    return fail(nullptr, NWD_ERR_UNSUPPORTED,
+                "%s: group size n_heads/n_kv_heads = %d is not one of 1, 2, 4, 5, 8", who, group);
+  if (d->head_dim != nwd::kHeadDim)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "%s: head_dim %d is not supported (only 128)", who,
+                d->head_dim);
+  for (int t : {d->q_dtype, d->o_dtype, d->kv_dtype})
+    if (t != NWD_F16 && t != NWD_F32)
+      return fail(nullptr, NWD_ERR_INVALID, "%s: dtype %d is neither NWD_F16 nor NWD_F32", who, t);
+  if (!(d->scale >= 0.f) || std::isinf(d->scale))
+    return fail(nullptr, NWD_ERR_INVALID, "%s: scale must be finite and >= 0", who);
+  if (d->max_seq > nwd::kMaxSeq)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "%s: max_seq %d exceeds %d tokens", who, d->max_seq,
+                nwd::kMaxSeq);
+  // Largest element index of a cache and of the query/output buffers must
+  // fit the kernels' 64-bit index math; keep the per-slab token index in int.
+  if ((int64_t)d->max_batch * d->n_kv_heads * (int64_t)d->max_seq > ((int64_t)1 << 40))
+    return fail(nullptr, NWD_ERR_INVALID, "%s: cache too large", who);
+  if ((int64_t)d->max_batch * d->n_kv_heads > (1 << 30))
+    return fail(nullptr, NWD_ERR_INVALID, "%s: max_batch * n_kv_heads too large", who);
+  return NWD_OK;
+}
+
+nwd::Shape shape_of(const nwd_desc* d) {
+  nwd::Shape sh;
+  sh.n_heads = d->n_heads;
+  sh.n_kv = d->n_kv_heads;
+  sh.group = d->n_heads / d->n_kv_heads;
+  sh.cap = d->max_seq;
+  sh.q16 = d->q_dtype == NWD_F16;
+  sh.o16 = d->o_dtype == NWD_F16;
+  sh.kv16 = d->kv_dtype == NWD_F16;
+  sh.qk_scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
+  return sh;
 }
 
 int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
@@ -102,6 +162,39 @@ int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
   return n < 1 ? 1 : n;
 }
 
+// Records the static scratch holds: a 256-byte status slot, then (m, l)
+// pairs and o[128] rows, each area 256-byte aligned.
+constexpr int64_t kScratchRecords = (int64_t)(kScratchBytes - 512) / (8 + nwd::kHeadDim * 4);
+constexpr size_t kScratchMlOffset = 256;
+constexpr size_t kScratchOOffset = kScratchMlOffset + ((kScratchRecords * 8 + 255) / 256) * 256;
+static_assert(kScratchOOffset + (size_t)kScratchRecords * nwd::kHeadDim * 4 <= kScratchBytes,
+              "records fit the scratch");
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+unsigned char* g_scratch_dev[kMaxDevices];  // per device: the device address of `scratch`
+
+// The device address of the current device's `scratch`, looked up on the
+// first call on that device.
+int scratch_address(const char* who, unsigned char** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(nullptr, NWD_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "%s: device index %d beyond %d", who, dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(nullptr, NWD_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", who,
+                  hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return NWD_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -109,37 +202,8 @@ extern "C" {
 int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (!out_ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_create: out_ctx is NULL");
   *out_ctx = nullptr;
-  if (!d) return fail(nullptr, NWD_ERR_INVALID, "nwd_create: desc is NULL");
-  if (d->n_heads <= 0 || d->n_kv_heads <= 0 || d->head_dim <= 0 || d->max_seq <= 0 ||
-      d->max_batch <= 0)
-    return fail(nullptr, NWD_ERR_INVALID,
-                "nwd_create: sizes must be positive (n_heads=%d n_kv_heads=%d head_dim=%d "
-                "max_seq=%d max_batch=%d)",
-                d->n_heads, d->n_kv_heads, d->head_dim, d->max_seq, d->max_batch);
-  if (d->n_heads % d->n_kv_heads != 0)
-    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: n_heads %d is not a multiple of n_kv_heads %d",
-                d->n_heads, d->n_kv_heads);
+  if (int rc = check_desc(d, "nwd_create")) return rc;
   const int group = d->n_heads / d->n_kv_heads;
-  if (!group_supported(group))
-    return fail(nullptr, NWD_ERR_UNSUPPORTED,
-                "nwd_create: group size n_heads/n_kv_heads = %d is not one of 1, 2, 4, 5, 8", group);
-  if (d->head_dim != nwd::kHeadDim)
-    return fail(nullptr, NWD_ERR_UNSUPPORTED, "nwd_create: head_dim %d is not supported (only 128)",
-                d->head_dim);
-  for (int t : {d->q_dtype, d->o_dtype, d->kv_dtype})
-    if (t != NWD_F16 && t != NWD_F32)
-      return fail(nullptr, NWD_ERR_INVALID, "nwd_create: dtype %d is neither NWD_F16 nor NWD_F32", t);
-  if (!(d->scale >= 0.f) || std::isinf(d->scale))
-    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: scale must be finite and >= 0");
-  if (d->max_seq > nwd::kMaxSeq)
-    return fail(nullptr, NWD_ERR_UNSUPPORTED, "nwd_create: max_seq %d exceeds %d tokens",
-                d->max_seq, nwd::kMaxSeq);
-  // Largest element index of a cache and of the query/output buffers must
-  // fit the kernels' 64-bit index math; keep the per-slab token index in int.
-  if ((int64_t)d->max_batch * d->n_kv_heads * (int64_t)d->max_seq > ((int64_t)1 << 40))
-    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: cache too large");
-  if ((int64_t)d->max_batch * d->n_kv_heads > (1 << 30))
-    return fail(nullptr, NWD_ERR_INVALID, "nwd_create: max_batch * n_kv_heads too large");
 
   nwd_ctx* ctx = new nwd_ctx();
   ctx->desc = *d;
@@ -147,14 +211,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->separate_merge = -1;
   ctx->ev_start = nullptr;
   ctx->ev_stop = nullptr;
-  ctx->shape.n_heads = d->n_heads;
-  ctx->shape.n_kv = d->n_kv_heads;
-  ctx->shape.group = group;
-  ctx->shape.cap = d->max_seq;
-  ctx->shape.q16 = d->q_dtype == NWD_F16;
-  ctx->shape.o16 = d->o_dtype == NWD_F16;
-  ctx->shape.kv16 = d->kv_dtype == NWD_F16;
-  ctx->shape.qk_scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
+  ctx->shape = shape_of(d);
 
   hipError_t e = hipGetDevice(&ctx->device);
   if (e != hipSuccess) {
@@ -252,7 +309,8 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len) {
   if (!ctx || batch < 1 || batch > ctx->desc.max_batch) return 0;
   int len = resolve_len(ctx, max_len);
   if (len > ctx->desc.max_seq) len = ctx->desc.max_seq;
-  int n = ctx->forced_splits > 0 ? ctx->forced_splits : auto_splits(ctx, batch, len);
+  int n = ctx->forced_splits > 0 ? ctx->forced_splits
+                                 : auto_splits(ctx->desc.n_heads, ctx->desc.n_kv_heads, batch, len);
   return clamp_splits(ctx, batch, n);
 }
 
@@ -312,6 +370,57 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new, const void
     return fail(ctx, NWD_ERR_INVALID, "nwd_append_decode: null new K/V rows");
   return decode_common(ctx, "nwd_append_decode", q, k_new, v_new, k_cache, v_cache, pos, out,
                        batch, max_len, stream);
+}
+
+int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k_new,
+                              const void* v_new, void* k_cache, void* v_cache, const int32_t* pos,
+                              void* out, int32_t batch, int32_t max_len, int32_t* status,
+                              void* stream) {
+  const char* who = "nwd_append_decode_noalloc";
+  if (int rc = check_desc(desc, who)) return rc;
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !pos || !out)
+    return fail(nullptr, NWD_ERR_INVALID, "%s: null buffer", who);
+  if (batch < 1 || batch > desc->max_batch)
+    return fail(nullptr, NWD_ERR_CAPACITY, "%s: batch %d outside [1, max_batch=%d]", who, batch,
+                desc->max_batch);
+  const int len = max_len <= 0 ? desc->max_seq : max_len;
+  if (len > desc->max_seq)
+    return fail(nullptr, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
+                desc->max_seq);
+  int n = auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
+  if (n > kMaxSplits) n = kMaxSplits;
+  const int64_t records = n > 1 ? (int64_t)batch * desc->n_heads * n : 0;
+  if (records > kScratchRecords)
+    return fail(nullptr, NWD_ERR_CAPACITY,
+                "%s: %d sequences x %d heads x %d splits need %lld split records; the static "
+                "scratch holds %lld (%zu bytes)",
+                who, batch, desc->n_heads, n, (long long)records, (long long)kScratchRecords,
+                kScratchBytes);
+  unsigned char* base = nullptr;
+  if (int rc = scratch_address(who, &base)) return rc;
+  nwd::Workspace ws;
+  ws.part_ml = reinterpret_cast<float2*>(base + kScratchMlOffset);
+  ws.part_o = reinterpret_cast<float*>(base + kScratchOOffset);
+  ws.records = kScratchRecords;
+  ws.counters = nullptr;  // the separate merge kernel takes no arrival tickets
+  ws.status = status ? status : reinterpret_cast<int*>(base);
+  nwd::DecodeCall c;
+  c.q = q;
+  c.k_cache = k_cache;
+  c.v_cache = v_cache;
+  c.pos = pos;
+  c.out = out;
+  c.k_new = k_new;
+  c.v_new = v_new;
+  c.batch = batch;
+  c.nsplit = n;
+  c.span = len;
+  c.fused_merge = 0;
+  c.ev_start = nullptr;
+  c.ev_stop = nullptr;
+  hipError_t e = nwd::launch_decode(shape_of(desc), c, ws, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(nullptr, NWD_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
+  return NWD_OK;
 }
 
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel) {

@@ -108,6 +108,8 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_kv_append": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
         "nwd_decode_attn": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
         "nwd_append_decode": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, vp]),
+        "nwd_append_decode_noalloc": (ctypes.c_int, [ctypes.POINTER(NwdDesc), vp, vp, vp, vp, vp,
+                                                     vp, vp, i32, i32, vp, vp]),
         "nwd_prefill_attn": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, i32, vp]),
         "nwd_device_status": (ctypes.c_int, [vp, vp]),
         "nwd_decode_splits": (i32, [vp, i32, i32]),
@@ -151,6 +153,18 @@ def _stream(s) -> Optional[int]:
     if handle is not None:
         return int(handle)
     raise TypeError("stream must be an int handle or a torch.cuda.Stream")
+
+
+def append_decode_noalloc(desc: NwdDesc, q, k_new, v_new, k_cache, v_cache, pos, out,
+                          batch: int, max_len: int = 0, status=None, stream=None):
+    """nwd_append_decode_noalloc: nwd_append_decode without a context, its
+    split-K records in the library's static device scratch (no allocation)."""
+    lib = load_library()
+    rc = lib.nwd_append_decode_noalloc(ctypes.byref(desc), _ptr(q), _ptr(k_new), _ptr(v_new),
+                                       _ptr(k_cache), _ptr(v_cache), _ptr(pos), _ptr(out), batch,
+                                       max_len, _ptr(status), _stream(stream))
+    if rc != NWD_OK:
+        raise NwdError(rc, lib.nwd_last_error(None).decode())
 
 
 class AttnContext:
