@@ -99,6 +99,19 @@ __device__ inline float sum_rows(float x) {
   return sum_xor32(sum_xor16(x));
 }
 
+// Max / sum with the lane holding the same dims in another row: step 0
+// pairs lane l with l ^ 32, step 1 with l ^ 16, step 2 with l ^ 8.
+__device__ inline float row_pair_max(float x, int step) {
+  if (step == 0) return max_xor32(x);
+  if (step == 1) return max_xor16(x);
+  return fmaxf(x, dpp_mov<kDppRowRor8>(x));
+}
+__device__ inline float row_pair_sum(float x, int step) {
+  if (step == 0) return sum_xor32(x);
+  if (step == 1) return sum_xor16(x);
+  return x + dpp_mov<kDppRowRor8>(x);
+}
+
 // One 16-byte run (8 values) of a new K/V row, fp16 or fp32, loaded as raw
 // words (fp16: the first 16 bytes) and converted later, so that the load
 // can be issued early and nothing waits for it until the values are used.
@@ -292,13 +305,21 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
   constexpr int kTiles = C::kTiles;
   static_assert(kThreads >= kMergeThreads, "merge_group needs 256 threads");
+  // Row states written to LDS per wavefront (see the end of the kernel). The
+  // rule depends on the shape's group size, not on the heads this
+  // workgroup serves, so both forms of a shape merge in the same order (same
+  // bits).
+  constexpr int kRowSteps = G * kQsub * kWaves * kRows * (kHeadDim + 2) * 4 <= 48 * 1024 ? 0 : 1;
+  constexpr int kRowStates = kRows >> kRowSteps;
+  constexpr int kStates = kWaves * kRowStates;
   constexpr int kMergeFloats = merge_lds_floats<G>();
-  constexpr int kWaveFloats = kWaves * G * (kHeadDim + 2);
-  constexpr int kLdsFloats = kMergeFloats > kWaveFloats ? kMergeFloats : kWaveFloats;
+  constexpr int kStateFloats = kStates * G * (kHeadDim + 2);
+  constexpr int kLdsFloats = kMergeFloats > kStateFloats ? kMergeFloats : kStateFloats;
+  static_assert(kLdsFloats * 4 <= 64 * 1024, "static LDS of one workgroup");
 
   __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
-  float* lds_o = lds;                                 // [kWaves][G][D]
-  float* lds_ml = lds + kWaves * G * kHeadDim;         // [kWaves][G][2]
+  float* lds_o = lds;                                 // [kStates][G][D]
+  float* lds_ml = lds + kStates * G * kHeadDim;        // [kStates][G][2]
 
   // Workgroups are dealt to the 8 XCDs round-robin in launch order, so the
   // XCD of a workgroup follows blockIdx.x. Rotating each sequence's splits
@@ -544,35 +565,45 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     }
   }
 
-  // Merge the row states of this wavefront: the lanes l, l ^ kLanes, ...
-  // hold the same dims of the other rows.
+  // Row states to LDS. The lanes l, l ^ kLanes, ... of a wavefront hold the
+  // same dims of its other rows; kRowSteps of those lane exchanges (xor 32,
+  // then 16, ...) merge rows in registers first, only as far as needed to
+  // keep the LDS area under 64 KB (G = 8); the rest are merged below with
+  // the wavefronts. (Merging all rows with lane swaps first cost ~250
+  // dependent VALU instructions and NOP hazards at the end of every
+  // workgroup.)
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float M = max_rows<kLanes>(m[g]);
-    const float sc = fast_exp2(m[g] - M);
-    l[g] = sum_rows<kLanes>(l[g] * sc);
+  for (int st = 0; st < kRowSteps; ++st) {
 #pragma unroll
-    for (int i = 0; i < kDims; ++i) acc[g][i] = sum_rows<kLanes>(acc[g][i] * sc);
-    m[g] = M;
+    for (int g = 0; g < G; ++g) {
+      const float M = row_pair_max(m[g], st);
+      const float sc = fast_exp2(m[g] - M);
+      l[g] = row_pair_sum(l[g] * sc, st);
+#pragma unroll
+      for (int i = 0; i < kDims; ++i) acc[g][i] = row_pair_sum(acc[g][i] * sc, st);
+      m[g] = M;
+    }
   }
-  if (row == 0) {
+  if (row < kRowStates) {
+    const int sidx = wave * kRowStates + row;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
 #pragma unroll
-      for (int i = 0; i < kRuns; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          lds_o[(wave * G + g) * kHeadDim + (col + i * kLanes) * 8 + e] = acc[g][i * 8 + e];
+      for (int i = 0; i < kRuns; ++i) {
+        f32x4* dst = reinterpret_cast<f32x4*>(&lds_o[(sidx * G + g) * kHeadDim + (col + i * kLanes) * 8]);
+        dst[0] = f32x4{acc[g][i * 8], acc[g][i * 8 + 1], acc[g][i * 8 + 2], acc[g][i * 8 + 3]};
+        dst[1] = f32x4{acc[g][i * 8 + 4], acc[g][i * 8 + 5], acc[g][i * 8 + 6], acc[g][i * 8 + 7]};
+      }
       if (col == 0) {
-        lds_ml[(wave * G + g) * 2] = m[g];
-        lds_ml[(wave * G + g) * 2 + 1] = l[g];
+        lds_ml[(sidx * G + g) * 2] = m[g];
+        lds_ml[(sidx * G + g) * 2 + 1] = l[g];
       }
     }
   }
   __syncthreads();
 
-  // Merge the wavefronts: one record (or the output) per head; thread t
-  // owns the 4-dim run t % 32 of head t / 32.
+  // Merge the row states of all wavefronts: one record (or the output) per
+  // head; thread t owns the 4-dim run t % 32 of head t / 32.
   const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
   // Record stores of the in-kernel merge write through to memory (agent
   // coherence, cache policy sc1), so the merging workgroup can read them on
@@ -583,11 +614,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     const int g = tid >> 5, d4 = tid & 31;
     float M = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
+    for (int w = 0; w < kStates; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
     f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
     float lt = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kStates; ++w) {
       const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
       o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
       lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
