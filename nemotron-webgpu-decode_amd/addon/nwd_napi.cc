@@ -25,6 +25,7 @@
 
 #include <cstdint>
 #include <cstring>
+#include <map>
 #include <string>
 
 #include "nwd_attn.h"
@@ -33,6 +34,28 @@ namespace {
 
 constexpr int kMaxDevices = 64;
 hipStream_t g_streams[kMaxDevices] = {};
+
+// Device buffers made by malloc (base address -> bytes). Every copy and
+// write through the addon must stay inside one of them: a wrongly sized
+// typed array is refused instead of writing past a buffer. (Node calls the
+// addon from its one JavaScript thread.)
+std::map<uintptr_t, size_t> g_allocs;
+
+// True when [p, p + bytes) lies inside one allocation made by malloc.
+bool in_allocation(const void* p, size_t bytes) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  auto it = g_allocs.upper_bound(a);
+  if (it == g_allocs.begin()) return false;
+  --it;
+  const size_t off = a - it->first;
+  return off <= it->second && bytes <= it->second - off;
+}
+
+std::string range_error(const char* op, const void* p, size_t bytes) {
+  return std::string(op) + ": " + std::to_string(bytes) + " bytes at device address " +
+         std::to_string(reinterpret_cast<uintptr_t>(p)) +
+         " do not fit inside one buffer allocated by malloc";
+}
 
 // The addon's stream on the current device, created on first use.
 hipStream_t stream() {
@@ -202,6 +225,7 @@ napi_value Malloc(napi_env env, napi_callback_info info) {
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, (size_t)bytes);
   if (e != hipSuccess) return throw_error(env, std::string("malloc: ") + hipGetErrorString(e));
+  g_allocs[reinterpret_cast<uintptr_t>(p)] = (size_t)bytes;
   return make_ptr(env, p);
 }
 
@@ -210,7 +234,12 @@ napi_value Free(napi_env env, napi_callback_info info) {
   get_args(env, info, 1, argv);
   void* p = nullptr;
   if (!get_ptr(env, argv[0], &p)) return throw_error(env, "free: bad pointer");
-  if (p) (void)hipFree(p);
+  if (p) {
+    auto it = g_allocs.find(reinterpret_cast<uintptr_t>(p));
+    if (it == g_allocs.end()) return throw_error(env, "free: not a buffer allocated by malloc");
+    g_allocs.erase(it);
+    (void)hipFree(p);
+  }
   return make_i32(env, 0);
 }
 
@@ -223,6 +252,7 @@ napi_value Upload(napi_env env, napi_callback_info info) {
   size_t bytes = 0;
   if (!get_ptr(env, argv[0], &dst) || !dst || !get_bytes(env, argv[1], &src, &bytes))
     return throw_error(env, "upload: expected (devicePtr, TypedArray)");
+  if (!in_allocation(dst, bytes)) return throw_error(env, range_error("upload", dst, bytes));
   hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice);
   if (e != hipSuccess) return throw_error(env, std::string("upload: ") + hipGetErrorString(e));
   return make_i32(env, 0);
@@ -238,6 +268,7 @@ napi_value SetI32(napi_env env, napi_callback_info info) {
   int32_t v = 0;
   if (!get_ptr(env, argv[0], &dst) || !dst || napi_get_value_int32(env, argv[1], &v) != napi_ok)
     return throw_error(env, "setI32: expected (devicePtr, int32)");
+  if (!in_allocation(dst, 4)) return throw_error(env, range_error("setI32", dst, 4));
   hipError_t e = hipMemsetD32Async(dst, v, 1, stream());
   if (e != hipSuccess) return throw_error(env, std::string("setI32: ") + hipGetErrorString(e));
   return make_i32(env, 0);
@@ -252,6 +283,7 @@ napi_value Download(napi_env env, napi_callback_info info) {
   size_t bytes = 0;
   if (!get_bytes(env, argv[0], &dst, &bytes) || !get_ptr(env, argv[1], &src) || !src)
     return throw_error(env, "download: expected (TypedArray, devicePtr)");
+  if (!in_allocation(src, bytes)) return throw_error(env, range_error("download", src, bytes));
   hipError_t e = hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
   if (e != hipSuccess) return throw_error(env, std::string("download: ") + hipGetErrorString(e));
   return make_i32(env, 0);
@@ -270,6 +302,7 @@ napi_value Zero(napi_env env, napi_callback_info info) {
   else napi_get_value_int64(env, argv[1], &bytes);
   if (!get_ptr(env, argv[0], &dst) || !dst || bytes < 0 || !lossless)
     return throw_error(env, "zero: expected (devicePtr, bytes)");
+  if (!in_allocation(dst, (size_t)bytes)) return throw_error(env, range_error("zero", dst, (size_t)bytes));
   hipError_t e = hipMemset(dst, 0, (size_t)bytes);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) return throw_error(env, std::string("zero: ") + hipGetErrorString(e));

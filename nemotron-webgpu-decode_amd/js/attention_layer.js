@@ -9,8 +9,16 @@
 //             attn = [q, kCache, vCache, attnO, uAttn]   (:331-333)
 //   _ops      kvK, kvV, attn dispatched in one pass        (:389-391)
 //   submitStep guard seq < maxSeq (:448); uKv.seq = seq, uAttn.seq = seq+1
-//             (:451-452); submit; seq++ (:467)
+//             (:451-452); submit; seq++ (:467) — it never waits for the
+//             device; generate enqueues every token and reads the outputs
+//             once at the end (:641-647, readOutputs :490-511)
 //   reset     zero-fill the caches (:615-633)
+// The token loop here does not wait for the device either: beginStep writes
+// the position with a stream-ordered write and endStep only advances seq.
+// A kernel that sees an out-of-range device position sets a sticky status
+// word; it is checked (one synchronisation) when outputs are read back
+// (readAttnO, GreedyHead.readToken / readLogits), by checkStatus(), or every
+// `statusEvery` tokens when that option is set.
 // Here the three dispatches are one appendDecode call, the caches are fp16
 // (head-major, see include/nwd_attn.h), and the position is one device int32
 // that the host writes before each step, as the reference writes its
@@ -32,10 +40,17 @@ const NANO4B = { hidden: 3136, heads: 40, kvHeads: 8, headDim: 128, maxSeq: 256 
 const Q4_ACCUMULATE = 2;  // nwd_q4_gemv epilogue: y = y + W.a (o_proj + residual add)
 const ATTN_LAYERS = [12, 17, 24, 32];
 
+function expectF32(a, n, what) {
+  if (!(a instanceof Float32Array) || a.length !== n)
+    throw new Error(`${what}: expected a Float32Array of ${n} values, got ` +
+                    `${a && a.constructor ? a.constructor.name : typeof a} of ${a ? a.length : 0}`);
+}
+
 class AttentionSlice {
   constructor({ heads = NANO4B.heads, kvHeads = NANO4B.kvHeads, headDim = NANO4B.headDim,
-                maxSeq = NANO4B.maxSeq, layers = ATTN_LAYERS } = {}) {
+                maxSeq = NANO4B.maxSeq, layers = ATTN_LAYERS, statusEvery = 0 } = {}) {
     this.heads = heads;
+    this.statusEvery = statusEvery;  // 0: check the device status only at readback
     this.kvHeads = kvHeads;
     this.headDim = headDim;
     this.maxSeq = maxSeq;
@@ -136,6 +151,9 @@ class AttentionSlice {
 
   // What the q/k/v GEMVs of a layer write (runtime.js:386-388, outputs :120-122).
   setQKV(q, k, v) {
+    expectF32(q, this.heads * this.headDim, 'setQKV q');
+    expectF32(k, this.kvHeads * this.headDim, 'setQKV k');
+    expectF32(v, this.kvHeads * this.headDim, 'setQKV v');
     addon.upload(this.q, q);
     addon.upload(this.k, k);
     addon.upload(this.v, v);
@@ -156,13 +174,22 @@ class AttentionSlice {
                  this.seq + 1);
   }
 
-  // runtime.js:467
+  // runtime.js:467: seq++ without waiting for the device.
   endStep() {
-    addon.deviceStatus(this.ctx);  // synchronises; throws on a bad device position
     this.seq += 1;
+    if (this.statusEvery > 0 && this.seq % this.statusEvery === 0) this.checkStatus();
+  }
+
+  // Waits for the work enqueued so far and throws if a kernel saw an
+  // out-of-range device position since the last check (the flag is then
+  // cleared). The reference's host guard (runtime.js:448) is beginStep's.
+  checkStatus() {
+    addon.deviceStatus(this.ctx);
   }
 
   readAttnO(out = new Float32Array(this.heads * this.headDim)) {
+    expectF32(out, this.heads * this.headDim, 'readAttnO');
+    this.checkStatus();
     addon.download(out, this.attnO);
     return out;
   }
@@ -198,13 +225,20 @@ class GreedyHead {
     addon.lmHeadArgmax(this.ctx, hNorm, this.w, keepLogits ? this.logits : null, this.tokenOut, 1);
   }
 
+  // Readbacks are where the token loop waits for the device: the status of
+  // every step enqueued so far is checked first (a bad device position
+  // throws here).
   readToken() {
+    addon.deviceStatus(this.ctx);
     const t = new Uint32Array(1);
     addon.download(t, this.tokenOut);
     return t[0];
   }
 
   readLogits(out = new Float32Array(this.w.n)) {
+    if (!this.logits) throw new Error('readLogits: encode(hNorm, true) keeps no logits yet');
+    expectF32(out, this.w.n, 'readLogits');
+    addon.deviceStatus(this.ctx);
     addon.download(out, this.logits);
     return out;
   }

@@ -3,8 +3,10 @@
 // DecodeEngine drives them (engine/runtime.js:386-393 per attention layer,
 // :447-469 per token): per token, beginStep (guard + device position
 // write), then for each of the model's 4 attention layers qkvAppend + decode
-// + q4Gemv(accumulate) from the normalised hidden state, then endStep (device
-// status check, which synchronises). Nano-4B shapes (40 query heads, 8 KV
+// + q4Gemv(accumulate) from the normalised hidden state, then endStep; no
+// token waits for the device (as the reference's submitStep,
+// runtime.js:447-469); the device status is checked, which synchronises, once
+// after the timed tokens. Nano-4B shapes (40 query heads, 8 KV
 // heads, hidden 3136), seeded random 4-bit weights per layer, caches filled
 // with `past` tokens. Prints one JSON line.
 //
@@ -84,8 +86,10 @@ function main() {
       slice.endStep();
     };
     for (let t = 0; t < warmup; t++) run();
+    slice.checkStatus();
     const t0 = process.hrtime.bigint();
     for (let t = 0; t < steps; t++) run();
+    slice.checkStatus();  // the device has finished every timed token
     const us = Number(process.hrtime.bigint() - t0) / 1e3 / steps;
     slice.seq = start;  // both modes attend over the same lengths
     return us;

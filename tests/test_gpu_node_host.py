@@ -122,3 +122,53 @@ def test_node_host_greedy_head(tmp_path):
         y64, bound = gemv_f64(h[t], quant, scales, zp)
         assert np.all(np.abs(logits[t] - y64) <= 1e-6 * bound), t
         assert tokens[t] == oracle.argmax_ref(logits[t]), t
+
+
+def test_node_host_bad_position_reported_at_readback():
+    """The token loop does not wait for the device (engine/runtime.js:447-469):
+    endStep never synchronises, so an out-of-range device position written
+    in token 7 of 20 is reported by the readback after the loop (then
+    cleared), not by the step; a clean run reads back without error."""
+    print("node check_status tokens=20 bad=7", flush=True)
+    res = subprocess.run(["node", str(JS / "check_status.js"), "20", "7"], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 0, res.stdout + res.stderr
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    bad, clean = r["corrupted"], r["clean"]
+    assert bad["stepError"] is None, bad
+    assert bad["readbackError"] and "position" in bad["readbackError"], bad
+    assert bad["secondReadback"] == "ok", bad
+    assert clean == {"stepError": None, "readbackError": None, "secondReadback": "ok"}, clean
+
+
+def test_node_addon_rejects_copies_past_a_buffer():
+    """ADVICE: a wrongly sized typed array must not write past a device
+    buffer; the addon refuses copies that do not fit inside one allocation,
+    and AttentionSlice checks the q/k/v/attnO lengths."""
+    script = r"""
+    const { AttentionSlice, addon } = require('./attention_layer');
+    const out = {};
+    const p = addon.malloc(64);
+    const tryIt = (name, f) => { try { f(); out[name] = 'ok'; } catch (e) { out[name] = String(e.message); } };
+    tryIt('fits', () => addon.upload(p, new Float32Array(16)));
+    tryIt('upload', () => addon.upload(p, new Float32Array(17)));
+    tryIt('download', () => addon.download(new Float32Array(17), p));
+    tryIt('offset', () => addon.upload(p + 8n, new Float32Array(15)));
+    tryIt('setI32', () => addon.setI32(p + 64n, 1));
+    tryIt('zero', () => addon.zero(p, 65));
+    addon.free(p);
+    const s = new AttentionSlice({ heads: 8, kvHeads: 2, headDim: 128, maxSeq: 8, layers: [0] });
+    tryIt('setQKV', () => s.setQKV(new Float32Array(8 * 128), new Float32Array(2 * 128 + 1),
+                                   new Float32Array(2 * 128)));
+    tryIt('readAttnO', () => s.readAttnO(new Float32Array(10)));
+    s.destroy();
+    console.log(JSON.stringify(out));
+    """
+    print("node addon range checks", flush=True)
+    res = subprocess.run(["node", "-e", script], capture_output=True, text=True, timeout=60, cwd=JS)
+    assert res.returncode == 0, res.stdout + res.stderr
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    assert r["fits"] == "ok", r
+    for k in ("upload", "download", "offset", "setI32", "zero"):
+        assert "do not fit" in r[k], (k, r)
+    assert "setQKV k" in r["setQKV"] and "readAttnO" in r["readAttnO"], r
