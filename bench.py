@@ -474,10 +474,10 @@ def hbm_roofline(achieved_gbs: float, kernel: str, algorithmic_bytes: float, tra
             "traffic": traffic, "algorithmic_bytes": int(algorithmic_bytes)}
 
 
-def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, headline: bool = False):
-    """Times `steps` append+attend steps and `steps` decode-only calls of one
-    workload from HIP graphs, and the split kernel alone from eager calls;
-    returns a dict of the measurements."""
+def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: int = 0):
+    """Times `steps` append+attend steps and `dec_steps` (default `steps`)
+    decode-only calls of one workload from HIP graphs, and the split kernel
+    alone from eager calls; returns a dict of the measurements."""
     past, window, layers, dist, desc = WORKLOADS[name]
     log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
@@ -486,7 +486,7 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, headline: boo
     us_step = ms * 1e3 / steps
     mean_b = wl.mean_kv_bytes(steps)
     # the decode call alone (split + merge kernels), same rotation
-    n_dec = max(steps, SECONDARY_STEPS[name])
+    n_dec = dec_steps or steps
     _, ms_dec = time_graph(torch, wl, n_dec, 0, append=False, reps=3)
     dec_us = ms_dec * 1e3 / n_dec
     dec_b = wl.mean_kv_bytes(n_dec)
@@ -700,7 +700,8 @@ def main():
         print(json.dumps(rounded(r)), flush=True)
         return
 
-    head = run_decode(torch, nw, hip, "decode-32k", args.steps, args.warmup, headline=True)
+    head = run_decode(torch, nw, hip, "decode-32k", args.steps, args.warmup,
+                      dec_steps=max(args.steps, SECONDARY_STEPS["decode-32k"]))
     configs = {
         "decode-153": run_decode(torch, nw, hip, "decode-153", SECONDARY_STEPS["decode-153"], 64),
         "decode-4k": run_decode(torch, nw, hip, "decode-4k", SECONDARY_STEPS["decode-4k"], 32),

@@ -74,6 +74,9 @@ struct DecodeCfg {
 
 // Units the key range is split in (128 keys).
 constexpr int kUnitKeys = 128;
+// How far (log2 units) a score may exceed the online softmax's reference
+// point before the reference moves (and the accumulators are rescaled).
+constexpr float kRescaleSlack = 8.f;
 
 // Sum over each aligned group of N lanes (N = 8 or 16); every lane of the
 // group gets it.
@@ -328,7 +331,15 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   // first splits hold keys of every sequence while the last ones hold
   // almost none (64 sequences of 512-16384 keys: 511 against 453 us per
   // step).
-  const int b = blockIdx.z, hkv = blockIdx.y / kQsub;
+  // In the per-query-head form the KV head is the fast grid index
+  // (blockIdx.y = sub * n_kv + hkv), so with 8 KV heads the kQsub
+  // workgroups that read the same K/V rows land on the same XCD and its L2
+  // serves their repeated reads (153 keys: 2.65 MB of HBM reads per call
+  // with them on different XCDs, for 0.63 MB of K/V).
+  const int b = blockIdx.z;
+  const int hkv = kQsub > 1 ? (int)blockIdx.y % a.n_kv : (int)blockIdx.y;
+  const int sub = kQsub > 1 ? (int)blockIdx.y / a.n_kv : 0;
+  const int hgrp = hkv * kQsub + sub;  // this workgroup's group of G query heads
   int split = blockIdx.x + (b & 7);
   while (split >= a.nsplit) split -= a.nsplit;
   const int tid = threadIdx.x;
@@ -406,7 +417,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
 
   // Query registers: this lane's dims of each of the G heads.
-  const int h0 = blockIdx.y * G;
+  const int h0 = hgrp * G;
   const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kHeadDim + col * 8;
   f16x8 q16[kQ16 ? G : 1][kRuns];
   float q32[kQ16 ? 1 : G][kDims];
@@ -519,13 +530,20 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
         s[j][g] = valid ? d * a.qk_scale_log2 : -INFINITY;
       }
     }
+    // The reference point m of the online softmax moves only when a score
+    // exceeds it by more than kRescaleSlack (log2 units), so weights stay in
+    // [0, 2^kRescaleSlack] and the rescale of the accumulators, which ran on
+    // almost every tile when any of the wavefront's rows and heads grew its
+    // maximum, becomes rare after the first tile. The sums use the same m
+    // throughout, so the result is the same softmax.
     float mn[G];
     bool grow = false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      mn[g] = m[g];
+      float mx = s[0][g];
 #pragma unroll
-      for (int j = 0; j < kKpr; ++j) mn[g] = fmaxf(mn[g], s[j][g]);
+      for (int j = 1; j < kKpr; ++j) mx = fmaxf(mx, s[j][g]);
+      mn[g] = mx > m[g] + kRescaleSlack ? mx : m[g];
       grow |= mn[g] > m[g];
     }
     if (grow) {
@@ -657,7 +675,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
   // The new rows go to the caches last: the lanes of row 0 of wavefront 0
   // hold the 16 runs of the new K row in nk, those of row 1 the V row's.
-  if (owns_new && wave == 0 && row < 2 && blockIdx.y % kQsub == 0) {
+  if (owns_new && wave == 0 && row < 2 && sub == 0) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
       f16* dst = (row == 0 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim +
@@ -668,7 +686,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   if (nsplit == 1 || !a.fused_merge) return;
 
   // The workgroup that takes the last arrival ticket of this (b, head
-  // group) merges: one counter per (b, blockIdx.y), i.e. per (b, hkv), or per
+  // group) merges: one counter per (b, hgrp), i.e. per (b, hkv), or per
   // (b, query head) in the per-query-head form, where batch x n_heads fits
   // the counters (the host keeps at least kSubSplitMaxWorkgroups of them).
   //
@@ -683,7 +701,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   // loads in merge_group, which are issued only after the ticket has
   // returned (they depend on it through lds_last).
   __shared__ int lds_last;
-  int* const counter = &a.counters[b * (a.n_kv * kQsub) + blockIdx.y];
+  int* const counter = &a.counters[b * (a.n_kv * kQsub) + hgrp];
   wait_vm();
   __syncthreads();
   if (tid == 0) {
