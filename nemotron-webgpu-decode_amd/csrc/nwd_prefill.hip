@@ -28,9 +28,15 @@
 //     the query rows held in registers as the B operand), so each lane holds
 //     4 consecutive keys of ONE row — its own softmax row;
 //   - causal mask only on tiles that cross a row's limit; online softmax in
-//     log2 units with the scale folded into the exp2 argument (one FMA per
-//     score), the row sum taken over the fp16 weights the PV product uses
-//     (v_dot2 with ones, two weights per instruction); O^T += V^T P^T on the
+//     log2 units: the query rows are pre-scaled by scale * log2(e) and the
+//     QK^T MFMAs accumulate onto -m, so each weight is one v_exp of an MFMA
+//     output (on gfx950 the VALU work adds to the MFMA time rather than
+//     hiding under it, so VALU instructions per score are what the loop
+//     minimises); the reference point m moves lazily (only when a tile's
+//     row maximum exceeds it by more than 8), which keeps the weights below
+//     2^8 and makes the 33-multiply rescale of a row block rare; the row sum
+//     is taken over the fp16 weights the PV product uses (v_dot2 with ones,
+//     two weights per instruction); O^T += V^T P^T on the
 //     same MFMA, where P^T (fp16) is built in registers from the S^T
 //     accumulators with no data movement between lanes, and V^T is read from
 //     the row-major V tile with two ds_read_b64_tr_b16 transpose loads per
@@ -57,6 +63,7 @@ constexpr int kPBM = 128;                   // rows per workgroup
 constexpr int kPBN = 128;                   // keys per tile
 constexpr int kRB = 2;                      // 16-row MFMA blocks per wavefront
 constexpr int kKB = 4;                      // 16-key blocks per wavefront per tile
+constexpr float kPSlack = 8.f;              // lazy-rescale slack, log2 units
 constexpr int kRowBytes = kHeadDim * 2;     // 256: K/V rows are unpadded in LDS
 constexpr int kTileBytes = kPBN * kRowBytes;  // 32 KB
 constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per load (8)
@@ -80,18 +87,24 @@ __device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Eight query elements times s, rounded to fp16.
 template <bool kQ16>
-__device__ inline f16x8 load_q8(const void* q, int64_t elem) {
+__device__ inline f16x8 load_q8_scaled(const void* q, int64_t elem, float s) {
+  f16x8 r;
   if constexpr (kQ16) {
-    return *reinterpret_cast<const f16x8*>(static_cast<const f16*>(q) + elem);
+    const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(q) + elem);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = (f16)((float)h[e] * s);
   } else {
     const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(q) + elem);
-    f32x4 a = p[0], c = p[1];
-    f16x8 r;
-    r[0] = (f16)a[0]; r[1] = (f16)a[1]; r[2] = (f16)a[2]; r[3] = (f16)a[3];
-    r[4] = (f16)c[0]; r[5] = (f16)c[1]; r[6] = (f16)c[2]; r[7] = (f16)c[3];
-    return r;
+    const f32x4 a = p[0], b = p[1];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = (f16)(a[e] * s);
+      r[4 + e] = (f16)(b[e] * s);
+    }
   }
+  return r;
 }
 
 template <bool kO16>
@@ -149,6 +162,9 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   const int t1 = (int)((int64_t)(split + 1) * ntiles_all / a.nsplit);
   const int kend_s = min(kend, t1 * kPBN);  // keys this split may load
 
+  // Query rows in registers, pre-scaled by scale * log2(e): the scores come
+  // out of the MFMAs in log2 units.
+  const float c = a.qk_scale_log2;
   const int r0 = mt * kPBM + rh * 32;
   int qi[kRB], gq[kRB], lim[kRB];
   f16x8 qf[kRB][4];
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       if (ok) {
-        qf[rb][db] = load_q8<kQ16>(a.q, qrow + db * 32 + 8 * lq);
+        qf[rb][db] = load_q8_scaled<kQ16>(a.q, qrow + db * 32 + 8 * lq, c);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[rb][db][e] = (f16)0.f;
@@ -200,6 +216,9 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   };
   auto wait_tile = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
 
+  // Per row (lane lr of each row block): the reference point m (log2
+  // units; kNegBig until the row has seen a key), the sum of weights and
+  // O^T, all relative to m.
   float m[kRB], lsum[kRB];
   f32x4 o[kRB][8];
 #pragma unroll
@@ -209,7 +228,6 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  const float c = a.qk_scale_log2;
 
   if (t1 > t0) {
     load_tile(t0, 0);
@@ -223,12 +241,16 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     const char* vs = lds + (2 + buf) * kTileBytes + kh * 64 * kRowBytes;
     const int k0 = kt * kPBN + kh * 64;
 
-    // st[kb][rb][e] = raw score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr)
-    f32x4 st[kKB][kRB];
+    // st[kb][rb][e] = score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr) - mu[rb]
+    // in log2 units: the MFMAs accumulate onto -mu, the row's reference
+    // point (0 before the row has seen a key).
+    float mu[kRB];
+    f32x4 c0[kRB], st[kKB][kRB];
 #pragma unroll
-    for (int kb = 0; kb < kKB; ++kb)
-#pragma unroll
-      for (int rb = 0; rb < kRB; ++rb) st[kb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < kRB; ++rb) {
+      mu[rb] = m[rb] > kNegBig ? m[rb] : 0.f;
+      c0[rb] = f32x4{-mu[rb], -mu[rb], -mu[rb], -mu[rb]};
+    }
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -236,7 +258,8 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
         const f16x8 k8 = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
                                                          (((4 * db + lq) ^ lr) << 4));
 #pragma unroll
-        for (int rb = 0; rb < kRB; ++rb) st[kb][rb] = mfma16x16x32(k8, qf[rb][db], st[kb][rb]);
+        for (int rb = 0; rb < kRB; ++rb)
+          st[kb][rb] = mfma16x16x32(k8, qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
       }
     }
     if (wave_has_pad || k0 + 63 > wave_min_lim) {
@@ -258,20 +281,27 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][rb][e]);
-      mx = max_xor32(max_xor16(mx));
-      if (mx > m[rb]) {
-        const float alpha = fast_exp2((m[rb] - mx) * c);
+      // Lazy rescale: m moves only when the tile's row maximum exceeds it
+      // by more than kPSlack, so the weights stay below 2^kPSlack (fp16
+      // holds them to its 11 bits) and the rescale of o runs on a handful of
+      // tiles; the scores are then re-based onto the new m.
+      const float ax = max_xor32(max_xor16(mx)) + mu[rb];
+      if (ax > m[rb] + kPSlack) {
+        const float alpha = fast_exp2(m[rb] - ax);
         lsum[rb] *= alpha;
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[rb][j] *= alpha;
-        m[rb] = mx;
+        m[rb] = ax;
+        const float d = mu[rb] - ax;
+#pragma unroll
+        for (int kb = 0; kb < kKB; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st[kb][rb][e] += d;
       }
-      const float mc = m[rb] * c;
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          pb[rb][kb >> 1][(kb & 1) * 4 + e] = (f16)fast_exp2(fmaf(st[kb][rb][e], c, -mc));
+        for (int e = 0; e < 4; ++e) pb[rb][kb >> 1][(kb & 1) * 4 + e] = (f16)fast_exp2(st[kb][rb][e]);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -329,7 +359,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     if (R >= total_rows) continue;
     const float* x = slot(rb);
     const float M = fmaxf(m[rb], x[0]);
-    const float a0 = fast_exp2((m[rb] - M) * c), a1 = fast_exp2((x[0] - M) * c);
+    const float a0 = fast_exp2(m[rb] - M), a1 = fast_exp2(x[0] - M);
     const float lt = lsum[rb] * a0 + x[1] * a1;
     const int64_t grow = ((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb];
     if (a.nsplit == 1) {
@@ -350,7 +380,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
         for (int e = 0; e < 4; ++e) r[e] = fmaf(x[2 + dblk * 4 + e], a1, r[e]);
         *reinterpret_cast<f32x4*>(a.part_o + rec * kHeadDim + dblk * 16 + 4 * lq) = r;
       }
-      if (lq == 0) a.part_ml[rec] = make_float2(M * c, lt);
+      if (lq == 0) a.part_ml[rec] = make_float2(M, lt);
     }
   }
 }
