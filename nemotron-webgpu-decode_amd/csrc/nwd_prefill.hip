@@ -32,9 +32,11 @@
 //     QK^T MFMAs accumulate onto -m, so each weight is one v_exp of an MFMA
 //     output (on gfx950 the VALU work adds to the MFMA time rather than
 //     hiding under it, so VALU instructions per score are what the loop
-//     minimises); the reference point m moves lazily (only when a tile's
-//     row maximum exceeds it by more than 8), which keeps the weights below
-//     2^8 and makes the 33-multiply rescale of a row block rare; the row sum
+//     minimises); the row maximum is taken only for a row's first keys and
+//     when a weight overflows fp16 (seen as an infinite row sum), and the
+//     reference point m then moves lazily (only when the row maximum
+//     exceeds it by more than 8), so the common tile costs one v_exp per
+//     score and the 33-multiply rescale of a row block is rare; the row sum
 //     is taken over the fp16 weights the PV product uses (v_dot2 with ones,
 //     two weights per instruction); O^T += V^T P^T on the
 //     same MFMA, where P^T (fp16) is built in registers from the S^T
@@ -274,17 +276,15 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     // P^T operands, two per row block: pb[rb][h] element e < 4 is key
     // k0 + 32h + 4*lq + e, e >= 4 is key k0 + 32h + 16 + 4*lq + (e-4).
     f16x8 pb[kRB][2];
-#pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) {
+    // Row maximum and lazy rescale of row block rb: m moves only when the
+    // tile's row maximum exceeds it by more than kPSlack, and the scores are
+    // then re-based onto the new m.
+    auto rescale = [&](int rb) {
       float mx = st[0][rb][0];
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][rb][e]);
-      // Lazy rescale: m moves only when the tile's row maximum exceeds it
-      // by more than kPSlack, so the weights stay below 2^kPSlack (fp16
-      // holds them to its 11 bits) and the rescale of o runs on a handful of
-      // tiles; the scores are then re-based onto the new m.
       const float ax = max_xor32(max_xor16(mx)) + mu[rb];
       if (ax > m[rb] + kPSlack) {
         const float alpha = fast_exp2(m[rb] - ax);
@@ -297,16 +297,41 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
         for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) st[kb][rb][e] += d;
+        mu[rb] = ax;
       }
+    };
+    // Weights of row block rb and their per-lane sum, taken over the fp16
+    // values the PV product uses (v_dot2 with ones, two per instruction).
+    auto weights = [&](int rb) {
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
         for (int e = 0; e < 4; ++e) pb[rb][kb >> 1][(kb & 1) * 4 + e] = (f16)fast_exp2(st[kb][rb][e]);
+      float ls = 0.f;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int e = 0; e < 8; e += 2)
-          lsum[rb] = dot2(f16x2{pb[rb][h][e], pb[rb][h][e + 1]}, f16x2{(f16)1.f, (f16)1.f}, lsum[rb]);
+          ls = dot2(f16x2{pb[rb][h][e], pb[rb][h][e + 1]}, f16x2{(f16)1.f, (f16)1.f}, ls);
+      return ls;
+    };
+    // The row maximum is taken only where it is needed: for a row's first
+    // keys (m is set from them, so the largest weight of a row is never
+    // below 1) and when a weight overflowed fp16 (m lags the row maximum by
+    // 16 or more: the tile's fp16 row sum is then +inf). Otherwise the
+    // weights are exponentials of the MFMA outputs as they are: m stays
+    // within 16 of the running maximum and every weight is below 2^16. Both
+    // tests are taken over the whole wavefront, so the four lanes of a row
+    // always take the path together.
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) {
+      if (__builtin_amdgcn_ballot_w64(m[rb] == kNegBig && k0 <= lim[rb])) rescale(rb);
+      float ls = weights(rb);
+      if (__builtin_amdgcn_ballot_w64(__builtin_isinf(ls))) {
+        rescale(rb);
+        ls = weights(rb);
+      }
+      lsum[rb] += ls;
     }
     const int vr0 = 4 * lq + (lr >> 2);
     auto vaddr = [&](int r, int dblk) {

@@ -190,3 +190,44 @@ def test_prefill_at_max_seq():
         want = v[:i + 1].mean(axis=0)
         for h in range(H):
             assert max_abs(o[0, i, h], want) < 2e-3, (i, h)
+
+
+@pytest.mark.parametrize("offset", [0.0, -60.0])
+def test_prefill_rising_and_negative_scores(offset):
+    """Scores that climb ~33 log2 units across the keys make the weights of
+    later tiles overflow fp16 against the reference point a wavefront took
+    from its first keys, so the kernel's overflow path (row maximum, rescale,
+    weights again) runs many times per row; offset -60 puts every score near
+    -60 / ln 2 log2 units, where weights taken without a row maximum would
+    underflow. Checked against a float64 softmax of the same fp16 inputs."""
+    say(f"prefill rising scores offset={offset}")
+    H, Hkv, P, n_new = 8, 2, 1200, 100
+    cap = P + n_new
+    g = rng(4411)
+    u = g.standard_normal(D)
+    u /= np.linalg.norm(u)
+    # q = 4u, k_j = (0.05 j + offset * sqrt(D) / 4) u + noise: the scaled
+    # score is 0.2 j / sqrt(D) + offset (3.3 log2 units more per 128 keys).
+    q = (np.tile(4.0 * u, (1, n_new, H, 1)) + 0.05 * g.standard_normal((1, n_new, H, D))).astype(np.float16)
+    j = np.arange(cap, dtype=np.float64)[:, None]
+    base = (0.05 * j + offset * np.sqrt(D) / 4.0) * u[None, :]
+    k = np.stack([base + 0.05 * g.standard_normal((cap, D)) for _ in range(Hkv)], axis=1).astype(np.float16)
+    v = g.standard_normal((cap, Hkv, D)).astype(np.float16)
+    with nw.AttnContext(H, Hkv, cap, o_dtype="f32") as ctx:
+        kc = dev(np.ascontiguousarray(k.transpose(1, 0, 2))[None])
+        vc = dev(np.ascontiguousarray(v.transpose(1, 0, 2))[None])
+        out = torch.empty((1, n_new, H, D), dtype=torch.float32, device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor([P]), out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        got = out.cpu().numpy()[0]
+    G = H // Hkv
+    kf, vf, qf = k.astype(np.float64), v.astype(np.float64), q[0].astype(np.float64)
+    worst = 0.0
+    for i in (0, 1, 37, 63, 64, 99):
+        L = P + i + 1
+        for h in range(H):
+            s = kf[:L, h // G] @ qf[i, h] / np.sqrt(D)
+            w = np.exp(s - s.max())
+            want = (w[:, None] * vf[:L, h // G]).sum(axis=0) / w.sum()
+            worst = max(worst, float(np.abs(got[i, h] - want).max()))
+    assert worst < TOL, worst
