@@ -455,6 +455,9 @@ EXTRA_WORKLOADS = {
                    "kv_append of 512 rows + fp16-MFMA prefill per step",
     "stream-read": "stream-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
                    "rotated) read with the split kernel's access pattern and nothing else",
+    "mfma-ceiling": "mfma-ceiling: 256 x 512-thread workgroups of 16x16x32 fp16 MFMAs only, "
+                    "v_exp_f32 only (one per two MFMAs, the prefill's ratio), both, v_fma_f32 "
+                    "only (one per MFMA) and MFMAs with FMAs",
     "qkv-append": "qkv-append: B=1, Nano-4B q/k/v 4-bit projections K=3136 -> 5120+1024+1024 "
                   "with k/v rounded into the fp16 caches, 32 weight sets rotated (461 MB)",
     "o-proj": "o-proj: B=1, Nano-4B o_proj 4-bit K=5120 -> 3136 with the residual add, "
@@ -602,6 +605,58 @@ def run_stream_read(torch, nw, launches: int):
     return res
 
 
+def run_mfma_ceiling(torch, iters: int = 2048, launches: int = 5):
+    """The matrix-core ceiling under load and how much of the prefill's
+    exponential work hides under its MFMAs (csrc/bench/nwd_mfma_ceiling.hip):
+    256 x 512-thread workgroups running only 16x16x32 fp16 MFMAs (mode 0),
+    only v_exp_f32 at the prefill's one exponential per two MFMAs (mode 1),
+    both (mode 2), only v_fma_f32 at one per MFMA (mode 3) or MFMAs and
+    FMAs (mode 4); with the shader clock each mode ran at. The hidden
+    fractions are taken in shader cycles (time x clock), since the clock
+    rises when the matrix cores are less busy."""
+    lib = ctypes.CDLL(str(BENCH_LIB))
+    lib.nwd_bench_mfma_ceiling.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p]
+    log("[bench] mfma-ceiling")
+    out = torch.empty(256 * 512, dtype=torch.float32, device="cuda")
+    clk = torch.zeros(2, dtype=torch.int64, device="cuda")
+    stream = torch.cuda.Stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    us, ghz = {}, {}
+    for mode in (0, 1, 2, 3, 4):
+        def launch():
+            rc = lib.nwd_bench_mfma_ceiling(mode, iters, out.data_ptr(), clk.data_ptr(),
+                                            stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"nwd_bench_mfma_ceiling: hip error {rc}")
+        for _ in range(2):
+            launch()
+        e0.record(stream)
+        for _ in range(launches):
+            launch()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us[mode] = e0.elapsed_time(e1) * 1e3 / launches
+        ticks, ref = (int(x) for x in clk.cpu())
+        ghz[mode] = ticks / (ref / 100e6) / 1e9
+    flops = 256 * 8 * iters * 32 * 2.0 * 16 * 16 * 32
+    tflops = flops / (us[0] * 1e-6) / 1e12
+    cyc = {m: us[m] * ghz[m] for m in us}  # thousands of shader cycles
+    hid_exp = (cyc[0] + cyc[1] - cyc[2]) / cyc[1]
+    hid_fma = (cyc[0] + cyc[3] - cyc[4]) / cyc[3]
+    res = {"workload": "mfma-ceiling", "desc": EXTRA_WORKLOADS["mfma-ceiling"],
+           "mfma_tflops": tflops, "mfma_frac_of_peak": tflops / MFMA_F16_PEAK_TFLOPS,
+           "us": {"mfma": us[0], "exp": us[1], "mfma_and_exp": us[2], "fma": us[3],
+                  "mfma_and_fma": us[4]},
+           "clock_ghz": {"mfma": ghz[0], "exp": ghz[1], "mfma_and_exp": ghz[2], "fma": ghz[3],
+                         "mfma_and_fma": ghz[4]},
+           "exp_cycles_hidden_frac": hid_exp, "fma_cycles_hidden_frac": hid_fma}
+    log(f"[bench] mfma-ceiling: {tflops:.0f} TFLOP/s at {ghz[0]:.2f} GHz; hidden under the MFMAs: "
+        f"{hid_exp:.2f} of the exp cycles, {hid_fma:.2f} of the fma cycles; {res['us']}")
+    del out, clk
+    return res
+
+
 def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
     """One 4-bit projection workload: us per call and weight-stream GB/s."""
     log(f"[bench] {name}: {steps} steps")
@@ -703,6 +758,8 @@ def main():
             r = run_prefill(torch, nw, args.steps, args.warmup)
         elif w == "stream-read":
             r = run_stream_read(torch, nw, args.steps)
+        elif w == "mfma-ceiling":
+            r = run_mfma_ceiling(torch)
         else:
             r = run_q4(torch, nw, w, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         print(json.dumps(rounded(r)), flush=True)
@@ -717,6 +774,9 @@ def main():
         "prefill-512": run_prefill(torch, nw, SECONDARY_STEPS["prefill-512"], 4),
     }
     stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
+    ceiling = run_mfma_ceiling(torch)
+    pre = configs["prefill-512"]["roofline"]
+    pre["frac_of_mfma_ceiling"] = pre["achieved"] / ceiling["mfma_tflops"]
     copy_gbs = copy_bandwidth(torch)
     log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
@@ -759,6 +819,7 @@ def main():
         "configs": {k: rounded({kk: vv for kk, vv in v.items() if kk != "mean_kv_bytes"})
                     for k, v in configs.items()},
         "stream_read": rounded(stream),
+        "mfma_ceiling": rounded(ceiling),
         "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(head["wall_s"], 4),
     }
