@@ -19,9 +19,9 @@
 // workgroups with 32-key steps, config 5).
 //   - K and V rows go from memory straight into LDS (buffer_load_dwordx4
 //     with the lds flag, gfx950: one instruction writes 1 KB, lane l's 16
-//     bytes at +16l), double-buffered: the next tile's copies land while the
-//     current tile is computed, and one wait plus one barrier per tile
-//     publish them. Rows are unpadded (256 B); the 16-byte chunks of a row
+//     bytes at +16l), double-buffered: the next tile's copies are issued
+//     between the current tile's QK^T MFMAs and land while it is computed,
+//     and one wait plus one barrier per tile publish them. Rows are unpadded (256 B); the 16-byte chunks of a row
 //     are XOR-swizzled by the row index so the MFMA operand reads hit
 //     distinct banks (each lane fetches the chunk its LDS slot must hold);
 //   - S^T = K Q^T on v_mfma_f32_16x16x32_f16 (K from LDS as the A operand,
@@ -68,7 +68,8 @@ constexpr int kKB = 4;                      // 16-key blocks per wavefront per t
 constexpr float kPSlack = 8.f;              // lazy-rescale slack, log2 units
 constexpr int kRowBytes = kHeadDim * 2;     // 256: K/V rows are unpadded in LDS
 constexpr int kTileBytes = kPBN * kRowBytes;  // 32 KB
-constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per load (8)
+constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per load (4)
+static_assert(4 * kStageInsts == 4 * kKB, "a tile's K and V copies fit one per two QK^T MFMA steps");
 // Chunk swizzles (16 chunks of 16 bytes per row): physical chunk p of LDS
 // row r holds logical chunk p ^ kswz(r) of a K row, p ^ vswz(r) of a V row.
 // A K operand read (16 rows, one logical chunk) then covers 16 distinct
@@ -203,18 +204,22 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   // ever stale.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const int st_row = 16 * wv + (lane >> 4), st_p = lane & 15;
+  // Copy j of this wave's part of tile kt into buffer bb: j < kStageInsts
+  // are K rows, the rest V rows. `oob` (0 or 2^31) pushes the offset past
+  // the range, which makes the copy a no-op read of zeros.
+  auto stage = [&](int kt, int bb, int j, uint32_t oob) {
+    const int i = j % kStageInsts;
+    const bool kpart = j < kStageInsts;
+    const int row = st_row + 4 * i;
+    const uint32_t rb_off = (uint32_t)(kt * kPBN + row) * kRowBytes + oob;
+    char* dst = lds + ((kpart ? 0 : 2) + bb) * kTileBytes + wv * 16 * kRowBytes + i * 1024;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(kpart ? rk : rv, (lds_void*)dst, 16,
+                                             rb_off + ((st_p ^ (kpart ? kswz(row) : vswz(row))) << 4),
+                                             0, 0, 0);
+  };
   auto load_tile = [&](int kt, int bb) {
-    char* kdst = lds + bb * kTileBytes + wv * 16 * kRowBytes;
-    char* vdst = lds + (2 + bb) * kTileBytes + wv * 16 * kRowBytes;
 #pragma unroll
-    for (int i = 0; i < kStageInsts; ++i) {
-      const int row = st_row + 4 * i;
-      const uint32_t rb_off = (uint32_t)(kt * kPBN + row) * kRowBytes;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(kdst + i * 1024), 16,
-                                               rb_off + ((st_p ^ kswz(row)) << 4), 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vdst + i * 1024), 16,
-                                               rb_off + ((st_p ^ vswz(row)) << 4), 0, 0, 0);
-    }
+    for (int j = 0; j < 2 * kStageInsts; ++j) stage(kt, bb, j, 0u);
   };
   auto wait_tile = [&]() { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
 
@@ -235,7 +240,6 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     load_tile(t0, 0);
     wait_tile();
     __syncthreads();
-    load_tile(t0 + 1, 1);
   }
   for (int kt = t0; kt < t1; ++kt) {
     const int buf = (kt - t0) & 1;
@@ -253,10 +257,17 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
       mu[rb] = m[rb] > kNegBig ? m[rb] : 0.f;
       c0[rb] = f32x4{-mu[rb], -mu[rb], -mu[rb], -mu[rb]};
     }
+    // Tile kt+1 is copied into the other buffer during this tile's QK^T,
+    // one copy per two MFMAs: spread out, a workgroup's 64 copies per tile
+    // do not queue at the address unit in one burst (measured: the burst
+    // after the barrier took ~680 cycles of every tile).
+    const int nb = (kt + 1 - t0) & 1;
+    const uint32_t oob = kt + 1 < t1 ? 0u : 0x80000000u;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) {
+        if (((db * kKB + kb) & 1) == 0) stage(kt + 1, nb, (db * kKB + kb) >> 1, oob);
         const f16x8 k8 = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
                                                          (((4 * db + lq) ^ lr) << 4));
 #pragma unroll
@@ -352,7 +363,6 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
 
     wait_tile();      // this wave's part of tile kt+1 is in LDS
     __syncthreads();  // every part is, and every wave is done with tile kt
-    if (kt + 2 < t1) load_tile(kt + 2, buf);  // nothing lands in LDS after the loop
   }
 
   // Merge the two key halves of each row group through LDS: wave (rh, 1)
