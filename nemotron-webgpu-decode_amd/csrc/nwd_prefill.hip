@@ -407,21 +407,31 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
         store_o4<kO16>(a.out, grow * kHeadDim + dblk * 16 + 4 * lq, r * inv);
       }
     } else {
+      // This split's record: (M, lt) and o. With an fp16 output, o is
+      // stored normalised (o / lt, bounded by the largest |V| entry) in
+      // fp16: half the record bytes for one more rounding of the output's
+      // own precision; with an fp32 output it stays unnormalised fp32.
       const int64_t rec = grow * a.nsplit + split;
+      const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
       for (int dblk = 0; dblk < 8; ++dblk) {
         f32x4 r = o[rb][dblk] * a0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = fmaf(x[2 + dblk * 4 + e], a1, r[e]);
-        *reinterpret_cast<f32x4*>(a.part_o + rec * kHeadDim + dblk * 16 + 4 * lq) = r;
+        const int64_t at = rec * kHeadDim + dblk * 16 + 4 * lq;
+        if constexpr (kO16) store_o4<true>(a.part_o, at, r * inv);
+        else *reinterpret_cast<f32x4*>(a.part_o + at) = r;
       }
       if (lq == 0) a.part_ml[rec] = make_float2(M, lt);
     }
   }
 }
 
-// out[row] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M); 32 threads per
-// row, 4 dims each.
+// out[row] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the
+// row's split records, merged in one pass (online maximum) so every load is
+// independent of the others; 32 threads per row, 4 dims each. With kO16 the
+// records hold o_s / l_s in fp16 (see prefill_kernel) and are weighted by
+// l_s 2^(m_s - M).
 template <bool kO16>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float2* __restrict__ part_ml,
@@ -431,17 +441,34 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
   const int64_t row = t >> 5;
   const int d4 = t & 31;
   if (row >= rows) return;
-  float M = kNegBig;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part_ml[row * nsplit + s].x);
+  float M = kNegBig, L = 0.f;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  float lt = 0.f;
+#pragma unroll 4
   for (int s = 0; s < nsplit; ++s) {
-    const float2 ml = part_ml[row * nsplit + s];
-    const float w = fast_exp2(ml.x - M);
-    lt = fmaf(ml.y, w, lt);
-    acc += *reinterpret_cast<const f32x4*>(part_o + (row * nsplit + s) * kHeadDim + d4 * 4) * w;
+    const int64_t rec = row * nsplit + s;
+    const float2 ml = part_ml[rec];
+    f32x4 ov;
+    if constexpr (kO16) {
+      const f16x4 h = *reinterpret_cast<const f16x4*>(reinterpret_cast<const f16*>(part_o) +
+                                                     rec * kHeadDim + d4 * 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ov[e] = (float)h[e];
+    } else {
+      ov = *reinterpret_cast<const f32x4*>(part_o + rec * kHeadDim + d4 * 4);
+    }
+    const float Mn = fmaxf(M, ml.x);
+    const float sc = fast_exp2(M - Mn);
+    float w = fast_exp2(ml.x - Mn);
+    if constexpr (kO16) {
+      w *= ml.y;
+      L = fmaf(L, sc, w);
+    } else {
+      L = fmaf(L, sc, ml.y * w);
+    }
+    acc = acc * sc + ov * w;
+    M = Mn;
   }
-  store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / lt));
+  store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / L));
 }
 
 constexpr size_t kPrefillLds = (size_t)4 * kTileBytes;
