@@ -257,24 +257,32 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
       mu[rb] = m[rb] > kNegBig ? m[rb] : 0.f;
       c0[rb] = f32x4{-mu[rb], -mu[rb], -mu[rb], -mu[rb]};
     }
-    // Tile kt+1 is copied into the other buffer during this tile's QK^T,
-    // one copy per two MFMAs: spread out, a workgroup's 64 copies per tile
-    // do not queue at the address unit in one burst (measured: the burst
-    // after the barrier took ~680 cycles of every tile).
+    // All 16 K fragments of this wavefront's 64 keys are read first (64
+    // VGPRs), then the 32 MFMAs run on them: no MFMA waits on a read issued
+    // just before it. Tile kt+1 is copied into the other buffer between the
+    // reads, one copy per two: issued in one burst after the barrier, a
+    // workgroup's 64 copies per tile queued at the address unit for ~680
+    // cycles of every tile.
     const int nb = (kt + 1 - t0) & 1;
     const uint32_t oob = kt + 1 < t1 ? 0u : 0x80000000u;
+    f16x8 kf[4][kKB];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb) {
         if (((db * kKB + kb) & 1) == 0) stage(kt + 1, nb, (db * kKB + kb) >> 1, oob);
-        const f16x8 k8 = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
-                                                         (((4 * db + lq) ^ lr) << 4));
-#pragma unroll
-        for (int rb = 0; rb < kRB; ++rb)
-          st[kb][rb] = mfma16x16x32(k8, qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
+        kf[db][kb] = *reinterpret_cast<const f16x8*>(ks + (kb * 16 + lr) * kRowBytes +
+                                                     (((4 * db + lq) ^ lr) << 4));
       }
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep every read ahead of the MFMAs
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb)
+          st[kb][rb] = mfma16x16x32(kf[db][kb], qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
     if (wave_has_pad || k0 + 63 > wave_min_lim) {
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb)
