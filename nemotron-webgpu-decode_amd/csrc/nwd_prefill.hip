@@ -283,6 +283,24 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
           st[kb][rb] = mfma16x16x32(kf[db][kb], qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
+    // The Vᵀ operands of this tile's PV product do not depend on the
+    // softmax: all 16 (32 transpose reads) are requested now, and arrive
+    // while the softmax runs.
+    const int vr0 = 4 * lq + (lr >> 2);
+    auto vaddr = [&](int r, int dblk) {
+      return reinterpret_cast<const f16*>(vs + r * kRowBytes +
+                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz(r)) << 4) + 8 * (lr & 1));
+    };
+    f16x8 vf[2][8];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int dblk = 0; dblk < 8; ++dblk) {
+        const f16x4 lo = lds_read_tr16(vaddr(h * 32 + vr0, dblk));
+        const f16x4 hi = lds_read_tr16(vaddr(h * 32 + 16 + vr0, dblk));
+        vf[h][dblk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    __builtin_amdgcn_sched_barrier(0);
     if (wave_has_pad || k0 + 63 > wave_min_lim) {
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb)
@@ -352,22 +370,12 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
       }
       lsum[rb] += ls;
     }
-    const int vr0 = 4 * lq + (lr >> 2);
-    auto vaddr = [&](int r, int dblk) {
-      return reinterpret_cast<const f16*>(vs + r * kRowBytes +
-                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz(r)) << 4) + 8 * (lr & 1));
-    };
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int dblk = 0; dblk < 8; ++dblk) {
-        const f16x4 lo = lds_read_tr16(vaddr(h * 32 + vr0, dblk));
-        const f16x4 hi = lds_read_tr16(vaddr(h * 32 + 16 + vr0, dblk));
-        const f16x8 v8 = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      for (int dblk = 0; dblk < 8; ++dblk)
 #pragma unroll
-        for (int rb = 0; rb < kRB; ++rb) o[rb][dblk] = mfma16x16x32(v8, pb[rb][h], o[rb][dblk]);
-      }
-    }
+        for (int rb = 0; rb < kRB; ++rb) o[rb][dblk] = mfma16x16x32(vf[h][dblk], pb[rb][h], o[rb][dblk]);
 
     wait_tile();      // this wave's part of tile kt+1 is in LDS
     __syncthreads();  // every part is, and every wave is done with tile kt
