@@ -444,6 +444,9 @@ WORKLOADS = {
     "decode-4k": (4096, 64, 32, "head-scale",
                   "decode-4k-64steps: B=1, 32q/8kv/d128, past 4096, K/V N(0,1) x per-head "
                   "U[0.5,2], append+attend per step, 32 layer caches rotated (545 MB)"),
+    "decode-1k": (1024, 64, 128, "normal",
+                  "decode-1k: B=1, 32q/8kv/d128, past 1024, K/V N(0,1), append+attend per step, "
+                  "128 layer caches rotated (570 MB)"),
     "decode-153": (152, 1, 64, "normal",
                    "decode-153: B=1, 32q/8kv/d128, past 152, one token appended at 152 and 153 "
                    "keys attended per step, K/V N(0,1), 64 layer caches rotated (40 MB)"),
@@ -467,7 +470,7 @@ EXTRA_WORKLOADS = {
 }
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
-SECONDARY_STEPS = {"decode-32k": 256, "decode-4k": 512, "decode-153": 1024, "ragged-64": 64,
+SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-4k": 512, "decode-153": 1024, "ragged-64": 64,
                    "prefill-512": 32, "stream-read": 64}
 
 
@@ -477,10 +480,14 @@ def hbm_roofline(achieved_gbs: float, kernel: str, algorithmic_bytes: float, tra
             "traffic": traffic, "algorithmic_bytes": int(algorithmic_bytes)}
 
 
-def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: int = 0):
+def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: int = 0,
+               other_splits=()):
     """Times `steps` append+attend steps and `dec_steps` (default `steps`)
     decode-only calls of one workload from HIP graphs, and the split kernel
-    alone from eager calls; returns a dict of the measurements."""
+    alone from eager calls; returns a dict of the measurements. For each n in
+    `other_splits` the decode-only calls are timed again with the split count
+    forced to n (nwd_set_decode_splits), which at short contexts also selects
+    the per-KV-head form instead of one workgroup per query head."""
     past, window, layers, dist, desc = WORKLOADS[name]
     log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
@@ -497,6 +504,13 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     n_eager = min(steps, 512)
     eager_us = time_eager(torch, wl, n_eager) * 1e3 / n_eager
     splits = wl.ctx.decode_splits(1, wl.cap)
+    forced = {}
+    for n in other_splits:
+        wl.ctx.set_decode_splits(n)
+        _, ms_n = time_graph(torch, wl, n_dec, 0, append=False, reps=3)
+        forced[str(n)] = ms_n * 1e3 / n_dec
+    if other_splits:
+        wl.ctx.set_decode_splits(0)
     res = {
         "workload": name, "desc": desc, "past": past, "window": window, "layers": layers,
         "steps": steps, "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
@@ -504,6 +518,8 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
         "split_kernel_us": split_us, "eager_us_per_step": eager_us, "mean_kv_bytes": mean_b,
         "wall_s": wall, "splits": splits,
     }
+    if forced:
+        res["decode_us_forced_splits"] = forced
     # The dominant kernel's duration: HIP events at the split kernel's start
     # and end (eager calls), or the whole graph-timed call when that is
     # shorter (the events include the dispatch latency of an eager launch,
@@ -769,6 +785,8 @@ def main():
                       dec_steps=max(args.steps, SECONDARY_STEPS["decode-32k"]))
     configs = {
         "decode-153": run_decode(torch, nw, hip, "decode-153", SECONDARY_STEPS["decode-153"], 64),
+        "decode-1k": run_decode(torch, nw, hip, "decode-1k", SECONDARY_STEPS["decode-1k"], 32,
+                                other_splits=(16, 32)),
         "decode-4k": run_decode(torch, nw, hip, "decode-4k", SECONDARY_STEPS["decode-4k"], 32),
         "ragged-64": run_ragged(torch, nw, SECONDARY_STEPS["ragged-64"], 8),
         "prefill-512": run_prefill(torch, nw, SECONDARY_STEPS["prefill-512"], 4),
