@@ -577,7 +577,7 @@ def run_prefill(torch, nw, steps: int, warmup: int):
            "roofline": {"bound": "mfma", "kernel": "nwd_prefill_attn (prefill + split merge)",
                         "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                        "traffic": None, "algorithmic_flops": wl.flops()}}
+                        "traffic": measured_traffic("prefill-512"), "algorithmic_flops": wl.flops()}}
     log(f"[bench] prefill-512: step {us_step:.1f} us (kv_append + prefill), prefill {us_main:.1f} us "
         f"({tflops:.1f} TFLOP/s)")
     wl.ctx.close()
