@@ -20,38 +20,42 @@
 //   - K and V rows go from memory straight into LDS (buffer_load_dwordx4
 //     with the lds flag, gfx950: one instruction writes 1 KB, lane l's 16
 //     bytes at +16l), double-buffered: the next tile's copies are issued
-//     between the current tile's QK^T MFMAs and land while it is computed,
-//     and one wait plus one barrier per tile publish them. Rows are unpadded (256 B); the 16-byte chunks of a row
-//     are XOR-swizzled by the row index so the MFMA operand reads hit
-//     distinct banks (each lane fetches the chunk its LDS slot must hold);
+//     between the current tile's K fragment reads and land while it is
+//     computed; one wait plus one barrier per tile publish them. Rows are
+//     unpadded (256 B); the 16-byte chunks of a row are XOR-swizzled by the
+//     row index so the MFMA operand reads hit distinct banks (each lane
+//     fetches the chunk its LDS slot must hold);
 //   - S^T = K Q^T on v_mfma_f32_16x16x32_f16 (K from LDS as the A operand,
-//     the query rows held in registers as the B operand), so each lane holds
-//     4 consecutive keys of ONE row — its own softmax row;
+//     all 16 fragments of a tile read before its MFMAs, the query rows held
+//     in registers as the B operand), so each lane holds 4 consecutive keys
+//     of ONE row — its own softmax row;
 //   - causal mask only on tiles that cross a row's limit; online softmax in
 //     log2 units: the query rows are pre-scaled by scale * log2(e) and the
 //     QK^T MFMAs accumulate onto -m, so each weight is one v_exp of an MFMA
-//     output (on gfx950 the VALU work adds to the MFMA time rather than
-//     hiding under it, so VALU instructions per score are what the loop
-//     minimises); the row maximum is taken only for a row's first keys and
-//     when a weight overflows fp16 (seen as an infinite row sum), and the
-//     reference point m then moves lazily (only when the row maximum
-//     exceeds it by more than 8), so the common tile costs one v_exp per
-//     score and the 33-multiply rescale of a row block is rare; the row sum
-//     is taken over the fp16 weights the PV product uses (v_dot2 with ones,
-//     two weights per instruction); O^T += V^T P^T on the
-//     same MFMA, where P^T (fp16) is built in registers from the S^T
-//     accumulators with no data movement between lanes, and V^T is read from
-//     the row-major V tile with two ds_read_b64_tr_b16 transpose loads per
-//     operand (gfx950): within a 16-lane group, output lane j element e comes
-//     from position j%4 of the 8 bytes lane 4e + j/4 addresses, so lanes
-//     4e..4e+3 addressing 16 consecutive dims of key row e give lane j
-//     V[key_e][d0 + j];
+//     output (the softmax's VALU work hides only partly behind the MFMAs,
+//     so VALU instructions per score are what the loop minimises); the row
+//     maximum is taken only for a row's first keys and when a weight
+//     overflows fp16 (seen as an infinite row sum), and the reference point
+//     m then moves lazily (only when the row maximum exceeds it by more
+//     than 8), so the common tile costs one v_exp per score and the
+//     33-multiply rescale of a row block is rare; the row sum is taken over
+//     the fp16 weights the PV product uses (v_dot2 with ones, two weights
+//     per instruction);
+//   - O^T += V^T P^T on the same MFMA, where P^T (fp16) is built in
+//     registers from the S^T accumulators with no data movement between
+//     lanes, and V^T is read from the row-major V tile with two
+//     ds_read_b64_tr_b16 transpose loads per operand (gfx950), all of a
+//     tile's requested before its softmax: within a 16-lane group, output
+//     lane j element e comes from position j%4 of the 8 bytes lane
+//     4e + j/4 addresses, so lanes 4e..4e+3 addressing 16 consecutive dims
+//     of key row e give lane j V[key_e][d0 + j];
 //   - the two key halves of a row group are merged through LDS at the end;
 //     accumulation is fp32 throughout.
 // With fewer than 256 row tiles, each row tile's key range is split over
-// nsplit workgroups (the decode kernel's split-K): they write (max, sum,
-// o[128]) records to the context's workspace, and prefill_merge_kernel
-// combines them; with one split the workgroup writes O directly.
+// nsplit workgroups (the decode kernel's split-K): they write (max, sum, o)
+// records to the context's workspace (o / sum in fp16 when the output is
+// fp16, o in fp32 otherwise), and prefill_merge_kernel combines them; with
+// one split the workgroup writes O directly.
 #include <atomic>
 
 #include "nwd_common.h"
