@@ -180,7 +180,8 @@ int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
 
 /* Synchronises the stream, returns NWD_OK if no kernel since the last call
  * flagged an out-of-range device position (else NWD_ERR_DEVICE), and clears
- * the flag. The reference throws at the host guard instead
+ * the flag. A library built with -DNWD_CHECK also flags, and drops, any
+ * kernel store whose address falls outside its buffer. The reference throws at the host guard instead
  * (engine/runtime.js:448). */
 int nwd_device_status(nwd_ctx* ctx, void* stream);
 

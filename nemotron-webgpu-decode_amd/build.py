@@ -1,10 +1,20 @@
 """Builds libnwd_attn.so (the gfx950 HIP kernels + C ABI) in-tree.
 
-Usage: python nemotron-webgpu-decode_amd/build.py [--jobs N]
+Usage: python nemotron-webgpu-decode_amd/build.py [--jobs N] [--variants]
 
 Each .hip file under csrc/ is compiled to an object with hipcc for gfx950
 only, then linked into lib/libnwd_attn.so. Packed-fp32 instruction selection
 is disabled for the device code (-packed-fp32-ops).
+
+Two debug variants of the same sources (--variants, or build_variants()):
+  lib/check/libnwd_attn.so  -DNWD_CHECK: every kernel store checks its
+                            address against its buffer, drops it when it is
+                            outside and flags it in the device status word;
+  lib/asan/libnwd_attn.so   host code built with AddressSanitizer (device
+                            code unchanged: GPU ASan is not used), plus
+                            lib/asan/nwd_abi_asan, a host driver program
+                            linked with the ASan runtime that exercises the
+                            C ABI (tests/asan/nwd_abi_asan.cc).
 """
 from __future__ import annotations
 
@@ -20,6 +30,10 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "lib" / "libnwd_attn.so"
+CHECK_LIB = PKG / "lib" / "check" / "libnwd_attn.so"
+ASAN_LIB = PKG / "lib" / "asan" / "libnwd_attn.so"
+ASAN_DRIVER = PKG / "lib" / "asan" / "nwd_abi_asan"
+ASAN_DRIVER_SRC = PKG.parent / "tests" / "asan" / "nwd_abi_asan.cc"
 BENCH_LIB = PKG / "lib" / "libnwd_bench.so"  # measurement kernels for bench.py
 ADDON = PKG / "lib" / "nwd_napi.node"
 INCLUDE = PKG.parent / "include"
@@ -44,10 +58,15 @@ DEVICE_FLAGS = [
 # costs an extra v_max (measured 12% of the kernel's time).
 FILE_FLAGS = {"nwd_prefill.hip": ["-fno-honor-nans"]}
 
+# Host-only AddressSanitizer: -Xarch_host sits right before each -fsanitize=,
+# so the device code is built exactly as in the product library.
+ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
 
-def _compile(src: Path) -> Path:
-    out = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(out)]
+
+def _compile(src: Path, objdir: Path = OBJ, extra: tuple = ()) -> Path:
+    out = objdir / (src.stem + ".o")
+    cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o",
+           str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     msg = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
@@ -58,29 +77,66 @@ def _compile(src: Path) -> Path:
     return out
 
 
-def build(jobs: int | None = None) -> Path:
-    """Compiles every csrc/*.hip and links lib/libnwd_attn.so; returns its path."""
+def _build_lib(lib: Path, objdir: Path, extra: tuple = (), link_extra: tuple = (),
+               jobs: int | None = None) -> Path:
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found: the HIP library cannot be built")
-    OBJ.mkdir(exist_ok=True)
-    LIB.parent.mkdir(exist_ok=True)
+    objdir.mkdir(parents=True, exist_ok=True)
+    lib.parent.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     jobs = jobs or min(len(sources), os.cpu_count() or 1, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+        objs = list(ex.map(lambda s: _compile(s, objdir, extra), sources))
+    tmp = lib.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, "-o", str(tmp),
+           *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib.name} failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, lib)
+    return lib
+
+
+def build(jobs: int | None = None) -> Path:
+    """Compiles every csrc/*.hip and links lib/libnwd_attn.so; returns its path."""
+    _build_lib(LIB, OBJ, jobs=jobs)
     build_bench()
     return LIB
+
+
+def build_check(jobs: int | None = None) -> Path:
+    """lib/check/libnwd_attn.so: the kernels with -DNWD_CHECK store checks."""
+    return _build_lib(CHECK_LIB, OBJ / "check", ("-DNWD_CHECK",), jobs=jobs)
+
+
+def build_asan(jobs: int | None = None) -> Path:
+    """lib/asan/libnwd_attn.so (host code under AddressSanitizer) and the
+    host driver lib/asan/nwd_abi_asan linked against it. The shared library
+    leaves the ASan runtime to the program that loads it: the driver links it
+    in, so nothing is preloaded."""
+    _build_lib(ASAN_LIB, OBJ / "asan", tuple(ASAN_HOST_FLAGS), jobs=jobs)
+    tmp = ASAN_DRIVER.with_suffix(".tmp")
+    # a host-only program (no .hip source): hipcc drives clang, whose ASan
+    # runtime matches the library's instrumentation
+    cmd = [HIPCC, "-O1", "-g", "-std=c++17", *ASAN_HOST_FLAGS, f"-I{INCLUDE}",
+           str(ASAN_DRIVER_SRC), "-o", str(tmp), f"-L{ASAN_LIB.parent}", "-lnwd_attn",
+           "-Wl,-rpath,$ORIGIN", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,/opt/rocm/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"ASan driver build failed:\n{res.stdout}{res.stderr}")
+    os.replace(tmp, ASAN_DRIVER)
+    return ASAN_LIB
+
+
+def build_variants(jobs: int | None = None) -> list:
+    """Both debug variants; each compiles every source again."""
+    return [build_check(jobs), build_asan(jobs)]
 
 
 def build_bench() -> Path:
     """Links lib/libnwd_bench.so from csrc/bench/*.hip: kernels that only
     bench.py uses (the stream-read ceiling), kept out of the product ABI."""
+    OBJ.mkdir(exist_ok=True)
     objs = [_compile(src) for src in sorted((CSRC / "bench").glob("*.hip"))]
     tmp = BENCH_LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
@@ -113,5 +169,10 @@ def build_addon() -> Path | None:
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
-    print(build(ap.parse_args().jobs))
+    ap.add_argument("--variants", action="store_true",
+                    help="also build lib/check and lib/asan (debug variants)")
+    args = ap.parse_args()
+    print(build(args.jobs))
     print(build_addon())
+    if args.variants:
+        print(build_variants(args.jobs))

@@ -473,6 +473,11 @@ int nwd_device_status(nwd_ctx* ctx, void* stream) {
   e = hipMemsetAsync(ctx->ws.status, 0, sizeof(int), s);
   if (e == hipSuccess) e = hipStreamSynchronize(s);
   if (e != hipSuccess) return hip_fail(ctx, "nwd_device_status: clear", e);
+  if (host & nwd::kStatusOutOfBounds)
+    return fail(ctx, NWD_ERR_DEVICE,
+                "a kernel of this bounds-checked build computed an address outside its "
+                "buffer; the access was skipped (status bits 0x%x)",
+                host);
   return fail(ctx, NWD_ERR_DEVICE,
               "a kernel saw a position outside [0, max_seq=%d): the cache was not written "
               "there and attention was clamped to the capacity",

@@ -56,6 +56,7 @@ __global__ __launch_bounds__(kAppendThreads) void kv_append_kernel(
   const int64_t dst = cache_index(b, (int)p, h, run * 8, n_kv, cap);
   f16x8 kr = load_run<kSrc16>(k_new, src);
   f16x8 vr = load_run<kSrc16>(v_new, src);
+  if (!in_bounds(dst, 8, (int64_t)gridDim.y * n_kv * cap * kHeadDim, status)) return;
   *reinterpret_cast<f16x8*>(k_cache + dst) = kr;
   *reinterpret_cast<f16x8*>(v_cache + dst) = vr;
 }

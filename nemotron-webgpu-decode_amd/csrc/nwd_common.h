@@ -34,6 +34,25 @@ constexpr int kStreamPolicy = 2;
 
 // Status bits written by kernels into the context's device status word.
 constexpr int kStatusBadPos = 1;
+constexpr int kStatusOutOfBounds = 2;  // set only by bounds-checked builds
+
+// Bounds-checked builds (compiled with -DNWD_CHECK) check every kernel
+// store into an output, a cache or the split-K workspace, and the merges'
+// reads of the workspace: the element range [at, at + n) must lie in
+// [0, size), the size the call's shape (or the workspace's capacity)
+// implies. An access outside it is skipped and sets kStatusOutOfBounds;
+// other builds compile the check away.
+#ifdef NWD_CHECK
+constexpr bool kCheckBounds = true;
+#else
+constexpr bool kCheckBounds = false;
+#endif
+__device__ inline bool in_bounds(int64_t at, int64_t n, int64_t size, int* status) {
+  if constexpr (!kCheckBounds) return true;
+  if (at >= 0 && at + n <= size) return true;
+  atomicOr(status, kStatusOutOfBounds);
+  return false;
+}
 
 // Element index of (b, t, h, d) in a cache: each (sequence, kv head) owns a
 // contiguous [cap][D] fp16 slab, so the keys a workgroup streams are one run.

@@ -175,7 +175,8 @@ template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) 
 template <int G, bool kO16, int kPolicy>
 __device__ inline void merge_group(const float* __restrict__ part_o,
                                    const float2* __restrict__ part_ml, void* __restrict__ out,
-                                   int64_t hrow0, int nsplit, float* lds) {
+                                   int64_t hrow0, int nsplit, float* lds, int64_t out_rows,
+                                   int64_t records, int* status) {
   static_assert(G * kMergeChunk <= kMergeThreads, "one (m, l) pair per thread per pass");
   constexpr int kPer = kMergeChunk / 8;  // splits per thread per head per pass
   const int t = threadIdx.x;
@@ -187,6 +188,8 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
   float* lds_mp = lds + G * 512 + 2 * kMergeThreads;            // [G]
   float* lds_lp = lds_mp + G;                                   // [G]
   const int64_t rec0 = hrow0 * nsplit;  // record (g, s) is rec0 + g * nsplit + s
+  // uniform over the workgroup, so returning here skips every barrier below
+  if (!in_bounds(rec0, (int64_t)G * nsplit, records, status)) return;
   const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(part_ml + rec0), 0,
                                                       G * nsplit * 8, kBufferWord3);
   const auto r_o = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_o + rec0 * kHeadDim), 0,
@@ -269,6 +272,7 @@ __device__ inline void merge_group(const float* __restrict__ part_o,
     for (int gg = 1; gg < G; ++gg) lt = gg == g ? Lr[gg] : lt;
     const float inv = 1.f / lt;
     const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
+    if (!in_bounds(at, 4, out_rows * kHeadDim, status)) return;
     if constexpr (kO16) {
       f16x4 v;
 #pragma unroll
@@ -288,11 +292,12 @@ struct DecodeArgs {
   void* out;
   float* part_o;
   float2* part_ml;
+  int64_t records;    // capacity of part_o / part_ml in records
   const void* k_new;  // optional new rows [batch][n_kv][D] (fused append)
   const void* v_new;
   int new16;          // new rows are fp16 (else fp32)
   int* counters;      // [batch][n_kv] arrival tickets, zero between calls
-  int n_heads, n_kv, cap, nsplit;
+  int batch, n_heads, n_kv, cap, nsplit;
   int span;           // host bound on L: keys [0, span) are partitioned
   int fused_merge;    // merge in the split kernel's last workgroup
   float qk_scale_log2;
@@ -641,10 +646,13 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
       o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
       lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
     }
+    const int64_t out_rows = (int64_t)a.batch * a.n_heads;
     if (nsplit == 1) {
       const float inv = 1.f / lt;
       const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
-      if constexpr (kO16) {
+      if (!in_bounds(at, 4, out_rows * kHeadDim, a.status)) {
+        // (bounds-checked builds only) the store is dropped
+      } else if constexpr (kO16) {
         f16x4 v;
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
@@ -655,12 +663,17 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     } else {
       // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
       const int64_t rec0 = hrow0 * nsplit + split;
+      // the descriptors below stop stores past this head group's records;
+      // the head's nsplit records must lie inside the workspace
+      const bool rec_ok = in_bounds(rec0 + g * nsplit, nsplit, a.records, a.status);
       const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
                                                          G * nsplit * kHeadDim * 4, kBufferWord3);
       const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
                                                           kBufferWord3);
       const uint32_t off = (g * nsplit * kHeadDim + d4 * 4) * 4;
-      if (a.fused_merge) {
+      if (!rec_ok) {
+        // (bounds-checked builds only) the stores are dropped
+      } else if (a.fused_merge) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, kRecPolicy);
         if (d4 == 0)
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
@@ -678,9 +691,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   if (owns_new && wave == 0 && row < 2 && sub == 0) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      f16* dst = (row == 0 ? a.k_cache : a.v_cache) + slab + (int64_t)pnew * kHeadDim +
-                 (col + i * kLanes) * 8;
-      *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
+      const int64_t at = slab + (int64_t)pnew * kHeadDim + (col + i * kLanes) * 8;
+      if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kHeadDim, a.status)) {
+        f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
+        *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
+      }
     }
   }
   if (nsplit == 1 || !a.fused_merge) return;
@@ -710,7 +725,8 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
   if (!lds_last) return;
-  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds);
+  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds,
+                                   (int64_t)a.batch * a.n_heads, a.records, a.status);
   if (tid == 0)
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -723,10 +739,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 template <bool kO16>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
     const float* __restrict__ part_o, const float2* __restrict__ part_ml,
-    void* __restrict__ out, int n_heads, int nsplit) {
+    void* __restrict__ out, int n_heads, int nsplit, int64_t records, int* __restrict__ status) {
   __shared__ __attribute__((aligned(16))) float lds[merge_lds_floats<1>()];
   const int h = blockIdx.x, b = blockIdx.y;
-  merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds);
+  merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds,
+                          (int64_t)gridDim.y * n_heads, records, status);
 }
 
 // The split workgroup's shape, from sweeps on MI355X (decode-only, per call,
@@ -760,7 +777,7 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, v
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
   decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kMergeThreads, 0, stream>>>(
-      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit);
+      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
   return hipGetLastError();
 }
 
@@ -785,9 +802,11 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.out = c.out;
   a.part_o = ws.part_o;
   a.part_ml = ws.part_ml;
+  a.records = ws.records;
   a.k_new = c.k_new;
   a.v_new = c.v_new;
   a.new16 = s.kv16;
+  a.batch = c.batch;
   a.n_heads = s.n_heads;
   a.n_kv = s.n_kv;
   a.cap = s.cap;

@@ -134,7 +134,8 @@ struct PrefillArgs {
   void* out;
   float* part_o;    // [rows][nsplit][D] (nsplit > 1)
   float2* part_ml;  // [rows][nsplit] (max in log2 units, sum)
-  int n_heads, n_kv, cap, n_new, mtiles, nsplit;
+  int64_t records;  // capacity of part_o / part_ml in records
+  int batch, n_heads, n_kv, cap, n_new, mtiles, nsplit;
   float qk_scale_log2;
   int* status;
 };
@@ -417,6 +418,8 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     const float a0 = fast_exp2(m[rb] - M), a1 = fast_exp2(x[0] - M);
     const float lt = lsum[rb] * a0 + x[1] * a1;
     const int64_t grow = ((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb];
+    const int64_t out_rows = (int64_t)a.batch * a.n_new * a.n_heads;
+    if (!in_bounds(grow, 1, out_rows, a.status)) continue;
     if (a.nsplit == 1) {
       const float inv = 1.f / lt;
 #pragma unroll
@@ -432,6 +435,7 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
       // fp16: half the record bytes for one more rounding of the output's
       // own precision; with an fp32 output it stays unnormalised fp32.
       const int64_t rec = grow * a.nsplit + split;
+      if (!in_bounds(rec, 1, a.records, a.status)) continue;
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
 #pragma unroll
       for (int dblk = 0; dblk < 8; ++dblk) {
@@ -456,11 +460,13 @@ template <bool kO16>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
                                                             const float2* __restrict__ part_ml,
                                                             void* __restrict__ out, int64_t rows,
-                                                            int nsplit) {
+                                                            int nsplit, int64_t records,
+                                                            int* status) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = t >> 5;
   const int d4 = t & 31;
   if (row >= rows) return;
+  if (!in_bounds(row * nsplit, nsplit, records, status)) return;
   float M = kNegBig, L = 0.f;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 4
@@ -488,6 +494,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
     acc = acc * sc + ov * w;
     M = Mn;
   }
+  if (!in_bounds(row * kHeadDim + d4 * 4, 4, rows * kHeadDim, status)) return;
   store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / L));
 }
 
@@ -544,11 +551,14 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
   a.nsplit = nsplit;
   a.part_o = ws.part_o;
   a.part_ml = ws.part_ml;
+  a.records = ws.records;
+  a.batch = batch;
   kern<<<(unsigned)(row_tiles * nsplit), kPThreads, kPrefillLds, stream>>>(a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   const unsigned blocks = (unsigned)((rows * 32 + 255) / 256);
-  prefill_merge_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows, nsplit);
+  prefill_merge_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows, nsplit,
+                                                                 ws.records, ws.status);
   return hipGetLastError();
 }
 

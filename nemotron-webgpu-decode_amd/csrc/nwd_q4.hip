@@ -449,7 +449,9 @@ __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
 #pragma unroll
   for (int c = 0; c < kQ4Cols; ++c) h[c] = (f16)r[c];
   f16* cache = which == 1 ? k_cache : v_cache;
-  *reinterpret_cast<f16x4*>(cache + cache_index(b, p, col0 / kHeadDim, col0 % kHeadDim, n_kv, cap)) = h;
+  const int64_t at = cache_index(b, p, col0 / kHeadDim, col0 % kHeadDim, n_kv, cap);
+  if (!in_bounds(at, kQ4Cols, (int64_t)gridDim.y * n_kv * cap * kHeadDim, status)) return;
+  *reinterpret_cast<f16x4*>(cache + at) = h;
 }
 
 namespace {

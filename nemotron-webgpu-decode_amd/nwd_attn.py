@@ -18,6 +18,9 @@ from typing import Optional
 
 PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = PKG_DIR / "lib" / "libnwd_attn.so"
+# debug build of the same sources with -DNWD_CHECK (build.py --variants):
+# every kernel store checks its address and flags NWD_ERR_DEVICE if outside
+CHECK_LIB_PATH = PKG_DIR / "lib" / "check" / "libnwd_attn.so"
 HEADER_PATH = PKG_DIR.parent / "include" / "nwd_attn.h"
 
 NWD_OK = 0
@@ -133,6 +136,18 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     return lib
 
 
+_others: dict = {}
+
+
+def _load_other(path: os.PathLike) -> ctypes.CDLL:
+    """A second build of the library, loaded once per path beside the first
+    (ctypes loads it with local symbol binding, so the builds stay apart)."""
+    key = str(Path(path).resolve())
+    if key not in _others:
+        _others[key] = load_library(path)
+    return _others[key]
+
+
 def _ptr(x) -> Optional[int]:
     if x is None:
         return None
@@ -178,8 +193,10 @@ class AttnContext:
 
     def __init__(self, n_heads: int, n_kv_heads: int, max_seq: int, *, head_dim: int = 128,
                  max_batch: int = 1, q_dtype: str = "f16", o_dtype: str = "f16",
-                 kv_dtype: str = "f16", scale: float = 0.0):
-        self.lib = load_library()
+                 kv_dtype: str = "f16", scale: float = 0.0,
+                 lib_path: Optional[os.PathLike] = None):
+        # lib_path: another build of the library (e.g. CHECK_LIB_PATH)
+        self.lib = load_library() if lib_path is None else _load_other(lib_path)
         self.desc = NwdDesc(n_heads, n_kv_heads, head_dim, max_seq, max_batch,
                             _DTYPES[q_dtype], _DTYPES[o_dtype], _DTYPES[kv_dtype], scale)
         h = ctypes.c_void_p()
