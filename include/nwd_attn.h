@@ -203,6 +203,17 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * keys). Same results, bit for bit. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
+/* Chooses the split kernel of later decode calls (the workgroup form of
+ * sparse_attn.wgsl main, kernels/sparse_attn.wgsl:31-114): 0 the dot-product
+ * kernel (VALU, whose work per key grows with the group size G), 1 the
+ * matrix-core kernel (MFMA, the same work for every G), -1 restores the
+ * default, which takes the matrix-core kernel for calls that run one
+ * workgroup per KV head with G = 8, or with G = 5 and at least 512 keys per
+ * split (the measured crossovers on MI355X), the dot-product kernel
+ * otherwise. Same records and merges; results agree
+ * within fp32 rounding (both accumulate in fp32), not bit for bit. */
+int nwd_set_decode_kernel(nwd_ctx* ctx, int32_t kernel);
+
 /* Measurement hook (no counterpart in the reference, whose split/merge
  * kernels are timed only as a whole step, bench/engine.js:70-137): while set,
  * the split kernel of every decode call on ctx is launched so that the HIP

@@ -34,6 +34,7 @@ struct nwd_ctx {
   int device;
   int forced_splits;
   int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 default (separate)
+  int decode_kernel;   // -1 the launch's choice, 0 dot-product, 1 matrix-core
   void* ev_start;      // hipEvent_t pair recorded around decode split kernels, or NULL
   void* ev_stop;
   int* status_host;    // pinned copy target of the device status word
@@ -209,6 +210,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->desc = *d;
   ctx->forced_splits = 0;
   ctx->separate_merge = -1;
+  ctx->decode_kernel = -1;
   ctx->ev_start = nullptr;
   ctx->ev_stop = nullptr;
   ctx->shape = shape_of(d);
@@ -349,6 +351,7 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   // 32K keys (its one launch costs less than the in-kernel merge's serialised
   // store, ticket and record round trips).
   c.fused_merge = ctx->separate_merge == 0 ? 1 : 0;
+  c.kernel = ctx->decode_kernel;
   c.ev_start = ctx->ev_start;
   c.ev_stop = ctx->ev_stop;
   hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
@@ -416,6 +419,7 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   c.nsplit = n;
   c.span = len;
   c.fused_merge = 0;
+  c.kernel = -1;
   c.ev_start = nullptr;
   c.ev_stop = nullptr;
   hipError_t e = nwd::launch_decode(shape_of(desc), c, ws, (hipStream_t)stream);
@@ -426,6 +430,14 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel) {
   if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_merge: ctx is NULL");
   ctx->separate_merge = separate_kernel < 0 ? -1 : (separate_kernel ? 1 : 0);
+  return NWD_OK;
+}
+
+int nwd_set_decode_kernel(nwd_ctx* ctx, int32_t kernel) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_kernel: ctx is NULL");
+  if (kernel < -1 || kernel > 1)
+    return fail(ctx, NWD_ERR_INVALID, "nwd_set_decode_kernel: kernel %d is not -1, 0 or 1", kernel);
+  ctx->decode_kernel = kernel;
   return NWD_OK;
 }
 

@@ -127,6 +127,52 @@ __device__ inline float sum64(float x) { return sum_xor32(sum32(x)); }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// LDS byte address of a pointer into LDS.
+__device__ inline uint32_t lds_address(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group, output lane j
+// element e comes from position j % 4 of the 8 bytes that lane 4e + j / 4
+// addresses.
+__device__ inline f16x4 lds_read_tr16(const f16* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
+
+// The same read as inline assembly. While LDS copies
+// (buffer_load ... lds) are in flight, the compiler puts a wait for every
+// global load in flight (vmcnt(0)) before each builtin transpose read, as it
+// cannot tell which LDS bytes a copy writes; in a loop that keeps the next
+// block's copies in flight that wait drains them every block. The compiler
+// does not track this form: the caller makes its results wait for it with
+// lds_reads_done before using them.
+__device__ inline f16x4 lds_read_tr16_asm(const void* p) {
+  f16x4 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(lds_address(p)));
+  return r;
+}
+
+// s_waitcnt lgkmcnt(0), ordered before every later use of v (taken as
+// in-out operands): every LDS access issued before it is complete.
+__device__ inline void lds_reads_done(f16x8 (&v)[8]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
+                 "+v"(v[6]), "+v"(v[7])
+               :
+               : "memory");
+}
+
+// D = A B + C on v_mfma_f32_16x16x32_f16: lane (r = lane % 16, q = lane / 16)
+// holds A[r][8q .. 8q+7], B[8q .. 8q+7][r] and D[4q .. 4q+3][r].
+__device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
 __device__ inline float dot2(f16x2 a, f16x2 b, float c) {
   return __builtin_amdgcn_fdot2(a, b, c, false);
 }

@@ -50,6 +50,8 @@
 // engine/runtime.js:389-391) is one launch.
 #include <hip/hip_ext.h>
 
+#include <atomic>
+
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
@@ -304,6 +306,111 @@ struct DecodeArgs {
   int* status;
 };
 
+// Record stores of the in-kernel merge write through to memory (agent
+// coherence, cache policy sc1), so the merging workgroup can read them on
+// any XCD without an L2 write-back.
+constexpr int kRecPolicy = 16;
+
+// The end of a split workgroup, shared by both loop forms: merges the
+// kStates partial states its wavefronts left in LDS (lds_o [kStates][G][D]
+// and lds_ml [kStates][G][2], (m, l) in log2 units) into one record per
+// query head, or, with one split, the normalised output. Called by every
+// thread after a barrier; thread t < 32 G owns the 4-dim run t % 32 of
+// head t / 32. hrow0 = b * n_heads + first head.
+template <int G, bool kO16, int kStates>
+__device__ inline void store_split_states(const DecodeArgs& a, const float* lds_o,
+                                          const float* lds_ml, int64_t hrow0, int split) {
+  const int tid = threadIdx.x;
+  const int nsplit = a.nsplit;
+  if (tid < G * 32) {
+    const int g = tid >> 5, d4 = tid & 31;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kStates; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
+    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    float lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kStates; ++w) {
+      const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
+      o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
+      lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
+    }
+    const int64_t out_rows = (int64_t)a.batch * a.n_heads;
+    if (nsplit == 1) {
+      const float inv = 1.f / lt;
+      const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
+      if (!in_bounds(at, 4, out_rows * kHeadDim, a.status)) {
+        // (bounds-checked builds only) the store is dropped
+      } else if constexpr (kO16) {
+        f16x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
+        *reinterpret_cast<f16x4*>(static_cast<f16*>(a.out) + at) = v;
+      } else {
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + at) = o * inv;
+      }
+    } else {
+      // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
+      const int64_t rec0 = hrow0 * nsplit + split;
+      // the descriptors below stop stores past this head group's records;
+      // the head's nsplit records must lie inside the workspace
+      const bool rec_ok = in_bounds(rec0 + g * nsplit, nsplit, a.records, a.status);
+      const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
+                                                         G * nsplit * kHeadDim * 4, kBufferWord3);
+      const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
+                                                          kBufferWord3);
+      const uint32_t off = (g * nsplit * kHeadDim + d4 * 4) * 4;
+      if (!rec_ok) {
+        // (bounds-checked builds only) the stores are dropped
+      } else if (a.fused_merge) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, kRecPolicy);
+        if (d4 == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
+                                                g * nsplit * 8, 0, kRecPolicy);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, 0);
+        if (d4 == 0)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
+                                                g * nsplit * 8, 0, 0);
+      }
+    }
+  }
+}
+
+// In-kernel merge (nwd_set_decode_merge): the workgroup that takes the last
+// arrival ticket of its (b, head group) merges the group's records. One
+// counter per (b, head group): per (b, hkv), or per (b, query head) in the
+// per-query-head form, where batch x n_heads fits the counters (the host
+// keeps at least kSubSplitMaxWorkgroups of them).
+//
+// Ordering (the AMDGPU memory model for gfx942-family targets, which gfx950
+// follows): an agent-scope release is "write back dirty L2 lines, wait for
+// the stores", an agent-scope acquire is "agent-scope load, then invalidate
+// L2". The records are the only data handed over, and they are stored and
+// loaded with the agent-scope cache policy sc1 itself, so they leave no
+// dirty L2 line behind and no stale L2 line can serve them: the release
+// reduces to waiting for this thread's record stores (vmcnt(0)) before the
+// barrier that precedes the ticket, and the acquire to the sc1 loads in
+// merge_group, which are issued only after the ticket has returned (they
+// depend on it through lds_last). `lds` holds merge_lds_floats<G>() floats.
+template <int G, bool kO16>
+__device__ inline void merge_on_last_arrival(const DecodeArgs& a, float* lds, int* counter,
+                                             int64_t hrow0) {
+  __shared__ int lds_last;
+  wait_vm();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    lds_last = ticket == a.nsplit - 1;
+  }
+  __syncthreads();
+  if (!lds_last) return;
+  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, a.nsplit, lds,
+                                   (int64_t)a.batch * a.n_heads, a.records, a.status);
+  if (threadIdx.x == 0)
+    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // kQsub workgroups per KV head, each serving G of its query heads (kQsub = 1:
 // one workgroup serves the whole group).
 template <int G, bool kQ16, bool kO16, int kQsub, class C>
@@ -313,6 +420,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
   constexpr int kTiles = C::kTiles;
   static_assert(kThreads >= kMergeThreads, "merge_group needs 256 threads");
+  static_assert(G * 32 <= kThreads, "one 4-dim run of each head per thread");
   // Row states written to LDS per wavefront (see the end of the kernel). The
   // rule depends on the shape's group size, not on the heads this
   // workgroup serves, so both forms of a shape merge in the same order (same
@@ -625,67 +733,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
 
-  // Merge the row states of all wavefronts: one record (or the output) per
-  // head; thread t owns the 4-dim run t % 32 of head t / 32.
-  const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
-  // Record stores of the in-kernel merge write through to memory (agent
-  // coherence, cache policy sc1), so the merging workgroup can read them on
-  // any XCD without an L2 write-back here.
-  constexpr int kRecPolicy = 16;
-  static_assert(G * 32 <= kThreads, "one 4-dim run per thread");
-  if (tid < G * 32) {
-    const int g = tid >> 5, d4 = tid & 31;
-    float M = kNegBig;
-#pragma unroll
-    for (int w = 0; w < kStates; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
-    float lt = 0.f;
-#pragma unroll
-    for (int w = 0; w < kStates; ++w) {
-      const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
-      o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
-      lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
-    }
-    const int64_t out_rows = (int64_t)a.batch * a.n_heads;
-    if (nsplit == 1) {
-      const float inv = 1.f / lt;
-      const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
-      if (!in_bounds(at, 4, out_rows * kHeadDim, a.status)) {
-        // (bounds-checked builds only) the store is dropped
-      } else if constexpr (kO16) {
-        f16x4 v;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
-        *reinterpret_cast<f16x4*>(static_cast<f16*>(a.out) + at) = v;
-      } else {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + at) = o * inv;
-      }
-    } else {
-      // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
-      const int64_t rec0 = hrow0 * nsplit + split;
-      // the descriptors below stop stores past this head group's records;
-      // the head's nsplit records must lie inside the workspace
-      const bool rec_ok = in_bounds(rec0 + g * nsplit, nsplit, a.records, a.status);
-      const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
-                                                         G * nsplit * kHeadDim * 4, kBufferWord3);
-      const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
-                                                          kBufferWord3);
-      const uint32_t off = (g * nsplit * kHeadDim + d4 * 4) * 4;
-      if (!rec_ok) {
-        // (bounds-checked builds only) the stores are dropped
-      } else if (a.fused_merge) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, kRecPolicy);
-        if (d4 == 0)
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
-                                                g * nsplit * 8, 0, kRecPolicy);
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, 0);
-        if (d4 == 0)
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
-                                                g * nsplit * 8, 0, 0);
-      }
-    }
-  }
+  store_split_states<G, kO16, kStates>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0, split);
   // The new rows go to the caches last: the lanes of row 0 of wavefront 0
   // hold the 16 runs of the new K row in nk, those of row 1 the V row's.
   if (owns_new && wave == 0 && row < 2 && sub == 0) {
@@ -699,36 +747,386 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     }
   }
   if (nsplit == 1 || !a.fused_merge) return;
+  merge_on_last_arrival<G, kO16>(a, lds, a.counters + b * (a.n_kv * kQsub) + hgrp,
+                                 (int64_t)b * a.n_heads + h0);
+}
 
-  // The workgroup that takes the last arrival ticket of this (b, head
-  // group) merges: one counter per (b, hgrp), i.e. per (b, hkv), or per
-  // (b, query head) in the per-query-head form, where batch x n_heads fits
-  // the counters (the host keeps at least kSubSplitMaxWorkgroups of them).
-  //
-  // Ordering (the AMDGPU memory model for gfx942-family targets, which
-  // gfx950 follows): an agent-scope release is "write back dirty L2 lines,
-  // wait for the stores", an agent-scope acquire is "agent-scope load, then
-  // invalidate L2". The records are the only data handed over, and they are
-  // stored and loaded with the agent-scope cache policy sc1 itself, so they
-  // leave no dirty L2 line behind and no stale L2 line can serve them: the
-  // release reduces to waiting for this thread's record stores (vmcnt(0))
-  // before the barrier that precedes the ticket, and the acquire to the sc1
-  // loads in merge_group, which are issued only after the ticket has
-  // returned (they depend on it through lds_last).
-  __shared__ int lds_last;
-  int* const counter = &a.counters[b * (a.n_kv * kQsub) + hgrp];
-  wait_vm();
+// ---------------------------------------------------------------------------
+// Matrix-core form of the split workgroup (decode_mfma_kernel). Same
+// key-range partition, records and merges as decode_split_kernel; the loop
+// runs on v_mfma_f32_16x16x32_f16 instead of VALU dot products, so its work
+// per key does not grow with the group size G. decode_split_kernel's VALU
+// work does: per 32K-key decode call (B = 1, 8 KV heads) it takes
+// 25.6 / 28.7 / 38.6 us at G = 4 / 5 / 8, this kernel 26.0-26.4 us at each
+// (K/V N(0,1) with 1% +-8 outliers; 27.5 against 27.1 us at G = 5 without
+// the outliers, whose larger score swings make the VALU kernel's per-row
+// references move more often). The launch picks it for G = 8, and for
+// G = 5 when a split holds 512 keys or more (at 256, 12.4 against 12.9 us;
+// at 512, 17.8 against 17.3); nwd_set_decode_kernel can force either.
+// Four wavefronts,
+// each owning one 32-key block of every 128-key workgroup iteration (keys
+// t0 + 128 it + 32 w ..), each independent of the others inside the loop:
+//   - K: lane (r = lane % 16, q = lane / 16) loads dims 32 db + 8q .. +8 of
+//     key r of each 16-key half straight into registers (per instruction,
+//     one 64-byte run of each of 16 rows): the A operand of S^T = K Q^T;
+//   - Q^T, the B operand, holds query head h0 + r in column r (zero for
+//     r >= G), so one MFMA serves every head of the group, and a
+//     workgroup's work per key does not grow with G;
+//   - V: the wavefront copies its block's V rows into its own LDS ring
+//     (buffer_load_dwordx4 with the lds flag, no registers held) and reads
+//     the V^T operands with ds_read_b64_tr_b16, as prefill does;
+//   - softmax: each lane holds 4 consecutive keys of one head; weights are
+//     exp2(s * scale * log2 e - m) in fp32, given to the PV MFMAs as fp16
+//     high and low parts (so the result keeps fp32-like precision and does
+//     not depend on the split count); the reference m moves only for a
+//     head's first keys and when a weight may exceed fp16 (then lazily, by
+//     more than kRescaleSlack).
+// The loads of block it + 1 are issued before block it is computed (two
+// blocks in flight: 27.3 against 26.9 us at G = 4 with three). K loads use
+// the default cache policy, V copies the non-temporal one (non-temporal K
+// loads: 26.9 against 26.0 us at G = 4; with three blocks in flight, 454
+// against 425 us for 64 ragged sequences). An fp32 query is split into fp16 high and low parts (two
+// MFMAs per operand), so the scores keep ~22 bits of the query. (Staging K
+// through LDS as whole rows too, with ds_read_b128 for the A operand,
+// measured the same: 26.6 against 26.4 us.)
+constexpr int kMWaves = 4;
+constexpr int kMThreads = kMWaves * 64;
+constexpr int kMWaveKeys = 32;                           // keys per wavefront per iteration
+constexpr int kMBlockKeys = kMWaves * kMWaveKeys;       // keys per workgroup iteration
+constexpr int kMSlotBytes = kMWaveKeys * kHeadDim * 2;  // one V block: 8 KB
+constexpr int kMDepth = 2;                               // blocks in flight per wavefront
+constexpr size_t kMLdsBytes = (size_t)kMWaves * kMDepth * kMSlotBytes;
+constexpr int kMBlockLoads = 2 * 4 + kMSlotBytes / 1024;  // K fragments + V copies
+static_assert(kMBlockKeys == kUnitKeys, "a split's range is whole workgroup iterations");
+static_assert(kMBlockLoads * (kMDepth - 1) <= 63, "vmcnt counts at most 63 loads");
+static_assert(kMLdsBytes <= 160 * 1024, "LDS of one gfx950 CU");
+
+// Chunk swizzle of the V rows in LDS (16 chunks of 16 bytes per row):
+// physical chunk p of row r holds logical chunk p ^ vswz_m(r), so the
+// transpose reads (4 rows x 2 chunks per 16 lanes) hit 8 distinct chunks.
+__device__ inline int vswz_m(int r) { return (r & 7) << 1; }
+
+// s_waitcnt vmcnt(n) that the compiler keeps in place: memory accesses do
+// not move across it.
+template <int n>
+__device__ inline void wait_vm_keep() {
+  static_assert(n == 0 || n == 16, "instantiated counts");
+  if constexpr (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (n == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+}
+__device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
+
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeArgs a) {
+  static_assert(G <= 16, "the heads of a group are the MFMA's 16 columns");
+  static_assert(kMBlockLoads == 16, "wait counts below assume 16 loads per block");
+  static_assert(G * 32 <= kMThreads, "one 4-dim run of each head per thread");
+  static_assert((size_t)kMWaves * G * (kHeadDim + 2) * 4 <= kMLdsBytes &&
+                    (size_t)merge_lds_floats<G>() * 4 <= kMLdsBytes,
+                "the end of the kernel reuses the ring");
+  extern __shared__ __attribute__((aligned(16))) f16 dsmem[];
+  char* lds = reinterpret_cast<char*>(dsmem);
+
+  const int b = blockIdx.z, hkv = blockIdx.y;
+  int split = blockIdx.x + (b & 7);  // XCD rotation, as decode_split_kernel
+  while (split >= a.nsplit) split -= a.nsplit;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15, lq = lane >> 4;
+  const int nsplit = a.nsplit;
+
+  const int units = (a.span + kUnitKeys - 1) / kUnitKeys;
+  const int u0 = (int)((int64_t)split * units / nsplit);
+  const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
+  const int t0 = u0 * kUnitKeys;
+  const int t1h = min(a.span, u1 * kUnitKeys);
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  auto slab_rsrc = [&](f16* cache, int end_key) {
+    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kHeadDim * 2),
+                                             kBufferWord3);
+  };
+  char* const ring = lds + wave * (kMDepth * kMSlotBytes);
+
+  struct KFrag {
+    f16x8 k[2][4];  // [16-key half][32-dim block]
+  };
+  auto load_k = [&](KFrag& f, const __amdgpu_buffer_rsrc_t rk, int it) {
+    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const uint32_t off = (uint32_t)(key0 + kb * 16 + lr) * (kHeadDim * 2) + db * 64 + lq * 16;
+        f.k[kb][db] = __builtin_bit_cast(
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+      }
+  };
+  // The block's V rows into ring slot `slot`: 8 copies of 4 rows (1 KB);
+  // lane l fills physical chunk l % 16 of row 4i + l / 16, so it loads the
+  // logical chunk the swizzle puts there.
+  auto load_v = [&](const __amdgpu_buffer_rsrc_t rv, int it, int slot) {
+    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+    char* dst = ring + slot * kMSlotBytes;
+#pragma unroll
+    for (int i = 0; i < kMSlotBytes / 1024; ++i) {
+      const int row = 4 * i + lq;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rv, (lds_void*)(dst + i * 1024), 16,
+          (uint32_t)(key0 + row) * (kHeadDim * 2) + ((lr ^ vswz_m(row)) << 4), 0, 0,
+          kStreamPolicy);
+    }
+  };
+
+  // Fused append: the new rows are requested first (the K chunks this
+  // lane's fragments hold, and V logical chunk lr), before the position
+  // says which split owns them.
+  const bool has_new = a.k_new != nullptr;
+  SrcRun nk_raw[4], nv_raw;
+  if (has_new) {
+    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) nk_raw[db] = load_src_run_raw(a.k_new, src + db * 32 + 8 * lq, a.new16);
+    nv_raw = load_src_run_raw(a.v_new, src + 8 * lr, a.new16);
+  }
+
+  // The first kMDepth - 1 blocks are requested before the position is
+  // known, over the keys this split can own; rows at or past L are zeroed
+  // in LDS before use (see below). Each block's copies are kept together,
+  // so the wait counts below see whole blocks.
+  KFrag kf[kMDepth];
+  {
+    const int own_end = split == nsplit - 1 ? a.cap : t1h;
+    const auto ek = slab_rsrc(a.k_cache, own_end), ev = slab_rsrc(a.v_cache, own_end);
+#pragma unroll
+    for (int t = 0; t < kMDepth - 1; ++t) {
+      load_k(kf[t], ek, t);
+      load_v(ev, t, t);
+      compiler_fence();
+    }
+  }
+
+  // Q^T: column lr is head h0 + lr; the rows past the group are zero.
+  const int h0 = hkv * G;
+  f16x8 qh[4], ql[kQ16 ? 1 : 4];
+  {
+    const bool qv = lr < G;
+    const int64_t qrow = ((int64_t)b * a.n_heads + h0 + (qv ? lr : 0)) * kHeadDim + 8 * lq;
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      if constexpr (kQ16) {
+        const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qrow + db * 32);
+        qh[db] = qv ? h : f16x8{};
+      } else {
+        const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(a.q) + qrow + db * 32);
+        const f32x4 x0 = p[0], x1 = p[1];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float x = qv ? (e < 4 ? x0[e] : x1[e - 4]) : 0.f;
+          qh[db][e] = (f16)x;
+          ql[db][e] = (f16)(x - (float)qh[db][e]);
+        }
+      }
+    }
+  }
+
+  const int pos_raw = a.pos[b];
+  const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
+  if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
+  const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
+  const int t1 = split == nsplit - 1 ? L : min(t1h, L);
+  const int n_it = t1 > t0 ? (t1 - t0 + kMBlockKeys - 1) / kMBlockKeys : 0;
+  const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
+
+  // Fused append: the wavefront whose block holds the new position
+  // substitutes the new rows (K in its fragments, V in its LDS slot) and
+  // writes them to the caches at the end.
+  const int pnew = L - 1;
+  const bool owns_new = has_new && pos_ok && t0 <= pnew && pnew < t1;
+  const int it_new = owns_new ? (pnew - t0) / kMBlockKeys : -1;
+  const int w_new = owns_new ? (pnew - t0) % kMBlockKeys / kMWaveKeys : -1;
+  const int r_new = (pnew - t0) % kMWaveKeys;
+  f16x8 nk[4], nv;
+  if (owns_new) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db) nk[db] = convert_src_run(nk_raw[db], a.new16);
+    nv = convert_src_run(nv_raw, a.new16);
+  }
+
+  const float c = a.qk_scale_log2;
+  float m = kNegBig, lsum = 0.f;  // head lr: reference point (log2 units), sum of weights
+  f32x4 o[8];                     // O^T: dims 16 dblk + 4 lq .. +4 of head lr
+#pragma unroll
+  for (int d = 0; d < 8; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](KFrag& f, int it, int slot) {
+    wait_vm_keep<kMBlockLoads * (kMDepth - 1)>();  // block it's K fragments and V rows are in
+    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+    if (key0 >= t1) return;  // nothing of this block is attended
+    char* vs = ring + slot * kMSlotBytes;
+    const bool partial = key0 + kMWaveKeys > t1;
+    if (it == it_new && wave == w_new) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bool sub = kb == (r_new >> 4) && lr == (r_new & 15);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) f.k[kb][db] = sub ? nk[db] : f.k[kb][db];
+      }
+      if (lq == 0) *reinterpret_cast<f16x8*>(vs + r_new * (kHeadDim * 2) + ((lr ^ vswz_m(r_new)) << 4)) = nv;
+    }
+    if (partial) {
+      // Rows at or past t1: zeros past the descriptor's end, or stale cache
+      // rows in the blocks requested before the position was known; a stale
+      // Inf or NaN times a zero weight would be NaN, so they are zeroed.
+#pragma unroll
+      for (int i = 0; i < kMSlotBytes / 1024; ++i) {
+        const int row = 4 * i + lq;
+        if (key0 + row >= t1) *reinterpret_cast<u32x4*>(vs + row * (kHeadDim * 2) + (lr << 4)) = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    // S^T: s[kb][e] = q . k for key key0 + 16 kb + 4 lq + e, head lr.
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        s[kb] = mfma16x16x32(f.k[kb][db], qh[db], s[kb]);
+        if constexpr (!kQ16) s[kb] = mfma16x16x32(f.k[kb][db], ql[db], s[kb]);
+      }
+    }
+    // V^T operands (dims 16 dblk + lr; element e < 4: key 4 lq + e, e >= 4:
+    // key 16 + 4 lq + e - 4), requested before the softmax.
+    const int vr0 = 4 * lq + (lr >> 2);
+    auto vaddr = [&](int r, int dblk) {
+      return reinterpret_cast<const f16*>(vs + r * (kHeadDim * 2) +
+                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz_m(r)) << 4) + 8 * (lr & 1));
+    };
+    f16x8 vf[8];
+#pragma unroll
+    for (int dblk = 0; dblk < 8; ++dblk) {
+      const f16x4 lo = lds_read_tr16_asm(vaddr(vr0, dblk));
+      const f16x4 hi = lds_read_tr16_asm(vaddr(16 + vr0, dblk));
+      vf[dblk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+    const float mu = m > kNegBig ? m : 0.f;
+    float st[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        st[kb][e] = fmaf(s[kb][e], c, -mu);
+        if (partial && key0 + kb * 16 + 4 * lq + e >= t1) st[kb][e] = -INFINITY;
+      }
+    float mu_now = mu;
+    auto rescale = [&]() {
+      float mx = st[0][0];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][e]);
+      const float ax = max_xor32(max_xor16(mx)) + mu_now;  // the head's maximum
+      if (ax > m + kRescaleSlack) {
+        const float al = fast_exp2(m - ax);
+        lsum *= al;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) o[d] *= al;
+        m = ax;
+        const float dd = mu_now - ax;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st[kb][e] += dd;
+        mu_now = ax;
+      }
+    };
+    // P^T operands, keys as in vf: each fp32 weight w as fp16 hi + lo
+    // (w - hi rounded), two PV MFMAs, so the product keeps ~22 bits of w and
+    // the result does not depend on where a split's reference point lies.
+    f16x8 ph, pl;
+    auto weights = [&]() {
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float w = fast_exp2(st[kb][e]);
+          const f16 h = (f16)w;
+          ph[kb * 4 + e] = h;
+          pl[kb * 4 + e] = (f16)(w - (float)h);
+          ls += w;
+        }
+      return ls;
+    };
+    // The maximum is taken for a head's first keys (so its largest weight
+    // is never below 1) and when a weight may exceed fp16 (a lane's sum of
+    // 8 weights reaches 65504: the maximum then exceeds m by more than 12,
+    // so m moves); both tests are wavefront-wide.
+    if (__builtin_amdgcn_ballot_w64(m == kNegBig)) rescale();
+    float ls = weights();
+    if (__builtin_amdgcn_ballot_w64(ls >= 65504.f)) {
+      rescale();
+      ls = weights();
+    }
+    lsum += ls;
+    lds_reads_done(vf);
+#pragma unroll
+    for (int dblk = 0; dblk < 8; ++dblk) {
+      o[dblk] = mfma16x16x32(vf[dblk], ph, o[dblk]);
+      o[dblk] = mfma16x16x32(vf[dblk], pl, o[dblk]);
+    }
+  };
+
+  for (int it0 = 0; it0 < n_it; it0 += kMDepth) {
+#pragma unroll
+    for (int t = 0; t < kMDepth; ++t) {
+      // The slot copied into next was read by the previous block: its
+      // transpose reads are complete before the copy is issued.
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      // The prefetch past the split's last block reads zeros without a
+      // memory access (descriptor range) and keeps the wait counts exact.
+      load_k(kf[(t + kMDepth - 1) % kMDepth], rk, it0 + t + kMDepth - 1);
+      load_v(rv, it0 + t + kMDepth - 1, (t + kMDepth - 1) % kMDepth);
+      if (it0 + t < n_it) compute(kf[t], it0 + t, t);
+    }
+  }
+  wait_vm_keep<0>();  // no copy into the ring is in flight when it is reused below
+
+  // Wavefront states to LDS ([kMWaves][G][D] and [kMWaves][G][2]), then the
+  // shared end of a split workgroup.
+  lsum = sum_xor32(sum_xor16(lsum));  // the head's sum over its 4 lane groups
   __syncthreads();
-  if (tid == 0) {
-    const int ticket = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    lds_last = ticket == nsplit - 1;
+  float* lds_o = reinterpret_cast<float*>(lds);
+  float* lds_ml = lds_o + kMWaves * G * kHeadDim;
+  if (lr < G) {
+#pragma unroll
+    for (int dblk = 0; dblk < 8; ++dblk)
+      *reinterpret_cast<f32x4*>(&lds_o[(wave * G + lr) * kHeadDim + dblk * 16 + 4 * lq]) = o[dblk];
+    if (lq == 0) {
+      lds_ml[(wave * G + lr) * 2] = m;
+      lds_ml[(wave * G + lr) * 2 + 1] = lsum;
+    }
   }
   __syncthreads();
-  if (!lds_last) return;
-  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, nsplit, lds,
-                                   (int64_t)a.batch * a.n_heads, a.records, a.status);
-  if (tid == 0)
-    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
+  store_split_states<G, kO16, kMWaves>(a, lds_o, lds_ml, hrow0, split);
+  // The new rows to the caches: K chunks 4 db + lq from the lanes of key
+  // row 0, V chunk lr from lane group 0.
+  if (owns_new && wave == w_new) {
+    const int64_t at = slab + (int64_t)pnew * kHeadDim;
+    const int64_t cache_elems = (int64_t)a.batch * a.n_kv * a.cap * kHeadDim;
+    if (lr == 0) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int64_t e = at + db * 32 + 8 * lq;
+        if (in_bounds(e, 8, cache_elems, a.status)) *reinterpret_cast<f16x8*>(a.k_cache + e) = nk[db];
+      }
+    }
+    if (lq == 0 && in_bounds(at + 8 * lr, 8, cache_elems, a.status))
+      *reinterpret_cast<f16x8*>(a.v_cache + at + 8 * lr) = nv;
+  }
+  if (nsplit == 1 || !a.fused_merge) return;
+  merge_on_last_arrival<G, kO16>(a, reinterpret_cast<float*>(lds), a.counters + b * a.n_kv + hkv,
+                                 hrow0);
 }
 
 // Separate merge: one 256-thread workgroup per (query head, sequence), the
@@ -792,6 +1190,51 @@ static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, const DecodeCal
                : launch_g<G, false, false, kQsub>(a, B, st, c.ev_start, c.ev_stop);
 }
 
+
+template <int G, bool kQ16, bool kO16>
+static hipError_t launch_mfma_t(const DecodeArgs& a, int batch, hipStream_t stream, void* ev_start,
+                                void* ev_stop) {
+  auto kern = decode_mfma_kernel<G, kQ16, kO16>;
+  // The ring exceeds the 64 KB default of dynamic LDS: raise the kernel's
+  // limit once per device (the attribute is per device).
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const uint64_t bit = 1ull << (dev & 63);
+  if (!(attr_set.load() & bit)) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMLdsBytes);
+    if (e != hipSuccess) return e;
+    attr_set.fetch_or(bit);
+  }
+  const dim3 grid((unsigned)a.nsplit, (unsigned)a.n_kv, (unsigned)batch);
+  if (ev_start || ev_stop) {
+    DecodeArgs arg = a;
+    void* args[] = {&arg};
+    e = hipExtLaunchKernel(reinterpret_cast<const void*>(kern), grid, dim3(kMThreads), args,
+                           kMLdsBytes, stream, (hipEvent_t)ev_start, (hipEvent_t)ev_stop, 0);
+  } else {
+    kern<<<grid, kMThreads, kMLdsBytes, stream>>>(a);
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
+  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kMergeThreads, 0, stream>>>(
+      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
+  return hipGetLastError();
+}
+
+template <int G>
+static hipError_t launch_mfma(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
+                              hipStream_t st) {
+  const int B = c.batch;
+  if (s.q16)
+    return s.o16 ? launch_mfma_t<G, true, true>(a, B, st, c.ev_start, c.ev_stop)
+                 : launch_mfma_t<G, true, false>(a, B, st, c.ev_start, c.ev_stop);
+  return s.o16 ? launch_mfma_t<G, false, true>(a, B, st, c.ev_start, c.ev_stop)
+               : launch_mfma_t<G, false, false>(a, B, st, c.ev_start, c.ev_stop);
+}
+
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                          hipStream_t stream) {
   DecodeArgs a;
@@ -823,6 +1266,17 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   // here (per append + attend step, B = 1, G = 4: 4.5 against 6.3 us at 153
   // keys with one split; 6.1 against 8.1 at 832 keys and 6.8 against 8.3 at
   // 1088 with 8 splits). Same bits.
+  auto mfma = [&]() -> hipError_t {
+    switch (s.group) {
+      case 1: return launch_mfma<1>(s, a, c, stream);
+      case 2: return launch_mfma<2>(s, a, c, stream);
+      case 4: return launch_mfma<4>(s, a, c, stream);
+      case 5: return launch_mfma<5>(s, a, c, stream);
+      case 8: return launch_mfma<8>(s, a, c, stream);
+      default: return hipErrorInvalidValue;
+    }
+  };
+  if (c.kernel == 1) return mfma();  // the caller's choice (nwd_set_decode_kernel)
   if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
     switch (s.group) {
       case 2: return launch_qo<1, 2>(s, a, c, stream);
@@ -832,6 +1286,10 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
       default: break;  // group 1 is already one workgroup per query head
     }
   }
+  // One workgroup per KV head: the matrix-core kernel where its
+  // G-independent work per key wins (see decode_mfma_kernel).
+  const int split_keys = (c.span + a.nsplit - 1) / a.nsplit;
+  if (c.kernel < 0 && (s.group == 8 || (s.group == 5 && split_keys >= 512))) return mfma();
   switch (s.group) {
     case 1: return launch_qo<1>(s, a, c, stream);
     case 2: return launch_qo<2>(s, a, c, stream);

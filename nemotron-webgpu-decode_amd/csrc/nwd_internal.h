@@ -41,6 +41,7 @@ struct DecodeCall {
   int nsplit;
   int span;  // host bound on the keys attended (max_len), partitions the splits
   int fused_merge;  // merge in the split kernel (else a separate merge kernel)
+  int kernel;       // -1 the launch's choice, 0 dot-product (VALU), 1 matrix-core
   void* ev_start;   // optional hipEvent_t pair recorded around the split kernel
   void* ev_stop;
 };

@@ -80,20 +80,6 @@ static_assert(4 * kStageInsts == 4 * kKB, "a tile's K and V copies fit one per t
 // chunks, and a transpose read (4 rows x 2 chunks per 16 lanes) 8.
 __device__ inline int kswz(int r) { return r & 15; }
 __device__ inline int vswz(int r) { return (r & 7) << 1; }
-typedef __attribute__((address_space(3))) void lds_void;
-
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
-
-__device__ inline f16x4 lds_read_tr16(const f16* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
-  return __builtin_bit_cast(f16x4, v);
-}
-
-__device__ inline f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
 // Eight query elements times s, rounded to fp16.
 template <bool kQ16>
 __device__ inline f16x8 load_q8_scaled(const void* q, int64_t elem, float s) {

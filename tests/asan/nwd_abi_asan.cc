@@ -96,6 +96,7 @@ static void cpu_checks() {
   expect(nwd_set_decode_splits(nullptr, 3), NWD_ERR_INVALID, "nwd_set_decode_splits(NULL)",
          nullptr);
   expect(nwd_set_decode_merge(nullptr, 1), NWD_ERR_INVALID, "nwd_set_decode_merge(NULL)", nullptr);
+  expect(nwd_set_decode_kernel(nullptr, 1), NWD_ERR_INVALID, "nwd_set_decode_kernel(NULL)", nullptr);
   expect(nwd_set_kernel_events(nullptr, nullptr, nullptr), NWD_ERR_INVALID,
          "nwd_set_kernel_events(NULL)", nullptr);
   expect(nwd_q4_gemv(nullptr, nullptr, nullptr, nullptr, 1, 0, nullptr), NWD_ERR_INVALID,
@@ -191,6 +192,12 @@ static void gpu_cycle(int group) {
            "nwd_decode_attn(3 splits)", ctx);
     expect(nwd_set_decode_splits(ctx, 0), NWD_OK, "nwd_set_decode_splits(0)", ctx);
     expect(nwd_set_decode_merge(ctx, -1), NWD_OK, "nwd_set_decode_merge(-1)", ctx);
+    expect(nwd_set_decode_kernel(ctx, 2), NWD_ERR_INVALID, "nwd_set_decode_kernel(2)", ctx);
+    for (int k : {1, 0, -1}) {
+      expect(nwd_set_decode_kernel(ctx, k), NWD_OK, "nwd_set_decode_kernel", ctx);
+      expect(nwd_append_decode(ctx, q, kn, vn, kc, vc, pos, out, batch, 0, nullptr), NWD_OK,
+             "nwd_append_decode(kernel choice)", ctx);
+    }
     int32_t st = 0;
     auto* status = static_cast<int32_t*>(m.get(sizeof st));
     expect(nwd_append_decode_noalloc(&desc, q, kn, vn, kc, vc, pos, out, batch, 0, status, nullptr),

@@ -375,6 +375,9 @@ def test_one_workgroup_per_query_head_same_bits(G):
     newv = normal_f16(g, (B, Hkv, D))
     q = normal_f16(g, (B, H, D))
     with nw.AttnContext(H, Hkv, L, max_batch=B) as ctx:
+        # both workgroup forms of the dot-product kernel (at G = 8 the batch
+        # would otherwise take the matrix-core kernel)
+        ctx.set_decode_kernel(0)
         base_k = to_cache([r[0] for r in rows], Hkv, L)
         base_v = to_cache([r[1] for r in rows], Hkv, L)
         assert ctx.decode_splits(B, L) == 1 and ctx.decode_splits(1, L) == 1
