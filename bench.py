@@ -90,8 +90,9 @@ class DecodeWorkload:
     entries replaced by +-8 (`dist="outliers"`)."""
 
     def __init__(self, torch, nw, past: int, window: int, layers: int, seed: int,
-                 dist: str = "normal"):
+                 dist: str = "normal", heads: int = H):
         self.torch, self.past, self.window, self.layers = torch, past, window, layers
+        self.heads = heads
         self.cap = past + window
         g = torch.Generator(device="cuda")
         g.manual_seed(seed)
@@ -118,10 +119,10 @@ class DecodeWorkload:
         self.vc = [kv((1, HKV, self.cap, D), hs_v, 1) for _ in range(layers)]
         self.knew = kv((window, 1, HKV, D), hs_k, 2)
         self.vnew = kv((window, 1, HKV, D), hs_v, 2)
-        self.q = rnd(window, 1, H, D)
-        self.out = torch.empty(1, H, D, dtype=f16, device="cuda")
+        self.q = rnd(window, 1, heads, D)
+        self.out = torch.empty(1, heads, D, dtype=f16, device="cuda")
         self.pos = torch.arange(past, past + window, dtype=torch.int32, device="cuda")
-        self.ctx = nw.AttnContext(H, HKV, self.cap)
+        self.ctx = nw.AttnContext(heads, HKV, self.cap)
 
     def pos_ptr(self, i: int) -> int:
         return self.pos.data_ptr() + 4 * i
@@ -450,7 +451,13 @@ WORKLOADS = {
     "decode-153": (152, 1, 64, "normal",
                    "decode-153: B=1, 32q/8kv/d128, past 152, one token appended at 152 and 153 "
                    "keys attended per step, K/V N(0,1), 64 layer caches rotated (40 MB)"),
+    "decode-32k-nano": (32768, 64, 4, "outliers",
+                        "decode-32k-nano: decode-32k on the Nemotron-H Nano-4B attention shape, "
+                        "B=1, 40q/8kv/d128 (group 5), past 32768, K/V N(0,1) with 1% +-8 "
+                        "outliers, append+attend per step, 4 layer caches rotated (537 MB)", 40),
 }
+# Split kernels of a decode call (nwd_set_decode_kernel).
+DECODE_KERNELS = {0: "dot-product (decode_split_kernel)", 1: "matrix-core (decode_mfma_kernel)"}
 EXTRA_WORKLOADS = {
     "ragged-64": "ragged-64: 64 sequences, past U{512..16384} (seed 4), one query each, "
                  "append+attend per step",
@@ -470,7 +477,8 @@ EXTRA_WORKLOADS = {
 }
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
-SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-4k": 512, "decode-153": 1024, "ragged-64": 64,
+SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,
+                   "decode-153": 1024, "ragged-64": 64,
                    "prefill-512": 32, "stream-read": 64}
 
 
@@ -481,16 +489,19 @@ def hbm_roofline(achieved_gbs: float, kernel: str, algorithmic_bytes: float, tra
 
 
 def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: int = 0,
-               other_splits=()):
+               other_splits=(), other_kernels=()):
     """Times `steps` append+attend steps and `dec_steps` (default `steps`)
     decode-only calls of one workload from HIP graphs, and the split kernel
     alone from eager calls; returns a dict of the measurements. For each n in
     `other_splits` the decode-only calls are timed again with the split count
     forced to n (nwd_set_decode_splits), which at short contexts also selects
-    the per-KV-head form instead of one workgroup per query head."""
-    past, window, layers, dist, desc = WORKLOADS[name]
-    log(f"[bench] {name}: past={past} window={window} layers={layers}, {steps} steps")
-    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
+    the per-KV-head form instead of one workgroup per query head. For each k
+    in `other_kernels` they are timed with the split kernel forced to k
+    (nwd_set_decode_kernel: 0 dot-product, 1 matrix-core)."""
+    past, window, layers, dist, desc = WORKLOADS[name][:5]
+    heads = WORKLOADS[name][5] if len(WORKLOADS[name]) > 5 else H
+    log(f"[bench] {name}: past={past} window={window} layers={layers} heads={heads}, {steps} steps")
+    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist, heads=heads)
     # median of 3 timed replays, each of exactly `steps` steps
     wall, ms = time_graph(torch, wl, steps, warmup, reps=3)
     us_step = ms * 1e3 / steps
@@ -511,6 +522,13 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
         forced[str(n)] = ms_n * 1e3 / n_dec
     if other_splits:
         wl.ctx.set_decode_splits(0)
+    by_kernel = {}
+    for k in other_kernels:
+        wl.ctx.set_decode_kernel(k)
+        _, ms_k = time_graph(torch, wl, n_dec, 0, append=False, reps=3)
+        by_kernel[DECODE_KERNELS[k]] = ms_k * 1e3 / n_dec
+    if other_kernels:
+        wl.ctx.set_decode_kernel(None)
     res = {
         "workload": name, "desc": desc, "past": past, "window": window, "layers": layers,
         "steps": steps, "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
@@ -520,14 +538,22 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     }
     if forced:
         res["decode_us_forced_splits"] = forced
+    if by_kernel:
+        res["decode_us_by_kernel"] = by_kernel
+    res["n_heads"] = heads
+    # the launch's choice of split kernel for this shape (see nwd_decode.hip)
+    per_kv_head = heads * splits > 256
+    res["split_kernel"] = DECODE_KERNELS[1 if per_kv_head and (heads // HKV == 8 or (
+        heads // HKV == 5 and -(-wl.cap // splits) >= 512)) else 0]
     # The dominant kernel's duration: HIP events at the split kernel's start
     # and end (eager calls), or the whole graph-timed call when that is
     # shorter (the events include the dispatch latency of an eager launch,
     # which dominates a few-microsecond kernel).
     kern_us = min(split_us, dec_us)
-    kernel = ("decode_split_kernel (HIP events at its start and end, or the whole call if shorter); "
+    kname = res["split_kernel"].split("(")[1].rstrip(")")
+    kernel = (f"{kname} (HIP events at its start and end, or the whole call if shorter); "
               "the call adds decode_merge_kernel" if splits > 1
-              else "decode_split_kernel (one split, no merge: the graph-timed call or its events)")
+              else f"{kname} (one split, no merge: the graph-timed call or its events)")
     res["kernel_us"] = kern_us
     res["roofline"] = hbm_roofline(dec_b / (kern_us * 1e-6) / 1e9, kernel, dec_b,
                                    measured_traffic(name))
@@ -782,8 +808,10 @@ def main():
         return
 
     head = run_decode(torch, nw, hip, "decode-32k", args.steps, args.warmup,
-                      dec_steps=max(args.steps, SECONDARY_STEPS["decode-32k"]))
+                      dec_steps=max(args.steps, SECONDARY_STEPS["decode-32k"]), other_kernels=(1,))
     configs = {
+        "decode-32k-nano": run_decode(torch, nw, hip, "decode-32k-nano",
+                                      SECONDARY_STEPS["decode-32k-nano"], 16, other_kernels=(0, 1)),
         "decode-153": run_decode(torch, nw, hip, "decode-153", SECONDARY_STEPS["decode-153"], 64),
         "decode-1k": run_decode(torch, nw, hip, "decode-1k", SECONDARY_STEPS["decode-1k"], 32,
                                 other_splits=(16, 32)),
@@ -832,7 +860,9 @@ def main():
         "roofline": rounded(head["roofline"]),
         "decode_call": {"us": round(head["decode_us"], 3), "gbs": round(head["decode_gbs"], 1),
                         "frac": round(head["decode_gbs"] / HBM_PEAK_GBS, 4),
-                        "split_kernel_us": round(head["split_kernel_us"], 3)},
+                        "split_kernel_us": round(head["split_kernel_us"], 3),
+                        "split_kernel": head["split_kernel"],
+                        "us_by_kernel": rounded(head.get("decode_us_by_kernel", {}))},
         "cpu_baseline": cpu,
         "configs": {k: rounded({kk: vv for kk, vv in v.items() if kk != "mean_kv_bytes"})
                     for k, v in configs.items()},
