@@ -543,8 +543,7 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     res["n_heads"] = heads
     # the launch's choice of split kernel for this shape (see nwd_decode.hip)
     per_kv_head = heads * splits > 256
-    res["split_kernel"] = DECODE_KERNELS[1 if per_kv_head and (heads // HKV == 8 or (
-        heads // HKV == 5 and -(-wl.cap // splits) >= 512)) else 0]
+    res["split_kernel"] = DECODE_KERNELS[1 if per_kv_head and heads // HKV >= 5 else 0]
     # The dominant kernel's duration: HIP events at the split kernel's start
     # and end (eager calls), or the whole graph-timed call when that is
     # shorter (the events include the dispatch latency of an eager launch,

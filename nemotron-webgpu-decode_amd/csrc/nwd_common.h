@@ -159,7 +159,7 @@ __device__ inline f16x4 lds_read_tr16_asm(const void* p) {
 
 // s_waitcnt lgkmcnt(0), ordered before every later use of v (taken as
 // in-out operands): every LDS access issued before it is complete.
-__device__ inline void lds_reads_done(f16x8 (&v)[8]) {
+__device__ inline void lds_reads_done(f16x4 (&v)[8]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]),
                  "+v"(v[6]), "+v"(v[7])

@@ -754,50 +754,54 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 // ---------------------------------------------------------------------------
 // Matrix-core form of the split workgroup (decode_mfma_kernel). Same
 // key-range partition, records and merges as decode_split_kernel; the loop
-// runs on v_mfma_f32_16x16x32_f16 instead of VALU dot products, so its work
-// per key does not grow with the group size G. decode_split_kernel's VALU
-// work does: per 32K-key decode call (B = 1, 8 KV heads) it takes
-// 25.6 / 28.7 / 38.6 us at G = 4 / 5 / 8, this kernel 26.0-26.4 us at each
-// (K/V N(0,1) with 1% +-8 outliers; 27.5 against 27.1 us at G = 5 without
-// the outliers, whose larger score swings make the VALU kernel's per-row
-// references move more often). The launch picks it for G = 8, and for
-// G = 5 when a split holds 512 keys or more (at 256, 12.4 against 12.9 us;
-// at 512, 17.8 against 17.3); nwd_set_decode_kernel can force either.
-// Four wavefronts,
-// each owning one 32-key block of every 128-key workgroup iteration (keys
-// t0 + 128 it + 32 w ..), each independent of the others inside the loop:
+// runs on fp16 MFMAs instead of VALU dot products, so its work per key does
+// not grow with the group size G, while decode_split_kernel's does.
+// Decode-only calls, B = 1, 8 KV heads, K/V N(0,1), same box (us,
+// dot-product / matrix-core):
+//   G = 4: 2K 8.3 / 8.5, 4K 9.2 / 9.5, 16K 16.3 / 17.0, 32K 26.2 / 26.5
+//   G = 5: 2K 8.9 / 8.6, 4K 9.9 / 9.6, 16K 17.9 / 17.1, 32K 27.3 / 26.4
+//   G = 8: 1K 11.0 / 8.6, 4K 12.2 / 9.9, 16K 23.5 / 17.3, 32K 38.9 / 26.7
+// (with 1% of K/V at +-8, whose larger score swings move the dot-product
+// kernel's per-row references more often, 32K: 27.0 / 26.3, 28.6 / 26.6,
+// 39.0 / 26.8). The launch takes it for one-workgroup-per-KV-head calls
+// with G >= 5 (G = 4, the shape the dot-product kernel was built for,
+// keeps that kernel); nwd_set_decode_kernel forces either.
+// Four wavefronts, each owning one 16-key block of every 64-key workgroup
+// iteration (keys t0 + 64 it + 16 w ..), independent of each other inside
+// the loop:
 //   - K: lane (r = lane % 16, q = lane / 16) loads dims 32 db + 8q .. +8 of
-//     key r of each 16-key half straight into registers (per instruction,
-//     one 64-byte run of each of 16 rows): the A operand of S^T = K Q^T;
+//     key r straight into registers (per instruction, one 64-byte run of
+//     each of 16 rows): the A operands of S^T = K Q^T on
+//     v_mfma_f32_16x16x32_f16;
 //   - Q^T, the B operand, holds query head h0 + r in column r (zero for
-//     r >= G), so one MFMA serves every head of the group, and a
-//     workgroup's work per key does not grow with G;
+//     r >= G), so one MFMA serves every head of the group;
 //   - V: the wavefront copies its block's V rows into its own LDS ring
 //     (buffer_load_dwordx4 with the lds flag, no registers held) and reads
 //     the V^T operands with ds_read_b64_tr_b16, as prefill does;
-//   - softmax: each lane holds 4 consecutive keys of one head; weights are
-//     exp2(s * scale * log2 e - m) in fp32, given to the PV MFMAs as fp16
-//     high and low parts (so the result keeps fp32-like precision and does
-//     not depend on the split count); the reference m moves only for a
-//     head's first keys and when a weight may exceed fp16 (then lazily, by
-//     more than kRescaleSlack).
-// The loads of block it + 1 are issued before block it is computed (two
-// blocks in flight: 27.3 against 26.9 us at G = 4 with three). K loads use
-// the default cache policy, V copies the non-temporal one (non-temporal K
-// loads: 26.9 against 26.0 us at G = 4; with three blocks in flight, 454
-// against 425 us for 64 ragged sequences). An fp32 query is split into fp16 high and low parts (two
-// MFMAs per operand), so the scores keep ~22 bits of the query. (Staging K
-// through LDS as whole rows too, with ds_read_b128 for the A operand,
-// measured the same: 26.6 against 26.4 us.)
+//   - softmax: each lane holds 4 consecutive keys of one head, the B
+//     operand layout of v_mfma_f32_16x16x16_f16, which computes O^T += V^T
+//     P^T; weights are exp2(s * scale * log2 e - m) in fp32, given to it as
+//     fp16 high and low parts (so the result keeps fp32-like precision and
+//     does not depend on the split count); the reference m moves only for
+//     a head's first keys and when a weight may exceed fp16 (then lazily,
+//     by more than kRescaleSlack).
+// The loads of block it + 1 are issued before block it is computed. Shape
+// of the loop, measured at G = 4, 32K keys (us per call): 16-key blocks
+// with two in flight 25.3, three 25.7, four 26.1; 32-key blocks with two in
+// flight 26.0, three 26.9 (and staging K through LDS as whole rows too,
+// 26.6). K loads use the default cache policy, V copies the non-temporal
+// one (non-temporal K: 25.7 against 25.3; default-policy V: 28.9). An fp32
+// query is split into fp16 high and low parts (two MFMAs per operand), so
+// the scores keep ~22 bits of the query.
 constexpr int kMWaves = 4;
 constexpr int kMThreads = kMWaves * 64;
-constexpr int kMWaveKeys = 32;                           // keys per wavefront per iteration
+constexpr int kMWaveKeys = 16;                           // keys per wavefront per iteration
 constexpr int kMBlockKeys = kMWaves * kMWaveKeys;       // keys per workgroup iteration
-constexpr int kMSlotBytes = kMWaveKeys * kHeadDim * 2;  // one V block: 8 KB
+constexpr int kMSlotBytes = kMWaveKeys * kHeadDim * 2;  // one V block: 4 KB
 constexpr int kMDepth = 2;                               // blocks in flight per wavefront
 constexpr size_t kMLdsBytes = (size_t)kMWaves * kMDepth * kMSlotBytes;
-constexpr int kMBlockLoads = 2 * 4 + kMSlotBytes / 1024;  // K fragments + V copies
-static_assert(kMBlockKeys == kUnitKeys, "a split's range is whole workgroup iterations");
+constexpr int kMBlockLoads = 4 + kMSlotBytes / 1024;  // K fragments + V copies
+static_assert(kUnitKeys % kMBlockKeys == 0, "a split's range is whole workgroup iterations");
 static_assert(kMBlockLoads * (kMDepth - 1) <= 63, "vmcnt counts at most 63 loads");
 static_assert(kMLdsBytes <= 160 * 1024, "LDS of one gfx950 CU");
 
@@ -810,16 +814,16 @@ __device__ inline int vswz_m(int r) { return (r & 7) << 1; }
 // not move across it.
 template <int n>
 __device__ inline void wait_vm_keep() {
-  static_assert(n == 0 || n == 16, "instantiated counts");
+  static_assert(n == 0 || n == 8, "instantiated counts");
   if constexpr (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (n == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  if constexpr (n == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
 }
 __device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
 
 template <int G, bool kQ16, bool kO16>
 __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeArgs a) {
   static_assert(G <= 16, "the heads of a group are the MFMA's 16 columns");
-  static_assert(kMBlockLoads == 16, "wait counts below assume 16 loads per block");
+  static_assert(kMBlockLoads == 8, "wait counts below assume 8 loads per block");
   static_assert(G * 32 <= kMThreads, "one 4-dim run of each head per thread");
   static_assert((size_t)kMWaves * G * (kHeadDim + 2) * 4 <= kMLdsBytes &&
                     (size_t)merge_lds_floats<G>() * 4 <= kMLdsBytes,
@@ -848,18 +852,15 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   char* const ring = lds + wave * (kMDepth * kMSlotBytes);
 
   struct KFrag {
-    f16x8 k[2][4];  // [16-key half][32-dim block]
+    f16x8 k[4];  // [32-dim block]
   };
   auto load_k = [&](KFrag& f, const __amdgpu_buffer_rsrc_t rk, int it) {
     const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const uint32_t off = (uint32_t)(key0 + kb * 16 + lr) * (kHeadDim * 2) + db * 64 + lq * 16;
-        f.k[kb][db] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-      }
+    for (int db = 0; db < 4; ++db) {
+      const uint32_t off = (uint32_t)(key0 + lr) * (kHeadDim * 2) + db * 64 + lq * 16;
+      f.k[db] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    }
   };
   // The block's V rows into ring slot `slot`: 8 copies of 4 rows (1 KB);
   // lane l fills physical chunk l % 16 of row 4i + l / 16, so it loads the
@@ -965,12 +966,9 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     char* vs = ring + slot * kMSlotBytes;
     const bool partial = key0 + kMWaveKeys > t1;
     if (it == it_new && wave == w_new) {
+      const bool sub = lr == r_new;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        const bool sub = kb == (r_new >> 4) && lr == (r_new & 15);
-#pragma unroll
-        for (int db = 0; db < 4; ++db) f.k[kb][db] = sub ? nk[db] : f.k[kb][db];
-      }
+      for (int db = 0; db < 4; ++db) f.k[db] = sub ? nk[db] : f.k[db];
       if (lq == 0) *reinterpret_cast<f16x8*>(vs + r_new * (kHeadDim * 2) + ((lr ^ vswz_m(r_new)) << 4)) = nv;
     }
     if (partial) {
@@ -983,47 +981,33 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
         if (key0 + row >= t1) *reinterpret_cast<u32x4*>(vs + row * (kHeadDim * 2) + (lr << 4)) = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    // S^T: s[kb][e] = q . k for key key0 + 16 kb + 4 lq + e, head lr.
-    f32x4 s[2];
+    // S^T: s[e] = q . k for key key0 + 4 lq + e, head lr.
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        s[kb] = mfma16x16x32(f.k[kb][db], qh[db], s[kb]);
-        if constexpr (!kQ16) s[kb] = mfma16x16x32(f.k[kb][db], ql[db], s[kb]);
-      }
+    for (int db = 0; db < 4; ++db) {
+      s = mfma16x16x32(f.k[db], qh[db], s);
+      if constexpr (!kQ16) s = mfma16x16x32(f.k[db], ql[db], s);
     }
-    // V^T operands (dims 16 dblk + lr; element e < 4: key 4 lq + e, e >= 4:
-    // key 16 + 4 lq + e - 4), requested before the softmax.
+    // V^T operands (dims 16 dblk + lr, keys 4 lq + e), requested before the
+    // softmax: the A operands of v_mfma_f32_16x16x16_f16, whose B operand
+    // layout (keys 4 lq .. 4 lq + 3 of column lr) is that of S^T, so the
+    // weights need no data movement between lanes.
     const int vr0 = 4 * lq + (lr >> 2);
-    auto vaddr = [&](int r, int dblk) {
-      return reinterpret_cast<const f16*>(vs + r * (kHeadDim * 2) +
-                                          (((2 * dblk + ((lr >> 1) & 1)) ^ vswz_m(r)) << 4) + 8 * (lr & 1));
-    };
-    f16x8 vf[8];
+    f16x4 vf[8];
 #pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk) {
-      const f16x4 lo = lds_read_tr16_asm(vaddr(vr0, dblk));
-      const f16x4 hi = lds_read_tr16_asm(vaddr(16 + vr0, dblk));
-      vf[dblk] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    }
+    for (int dblk = 0; dblk < 8; ++dblk)
+      vf[dblk] = lds_read_tr16_asm(vs + vr0 * (kHeadDim * 2) +
+                                   (((2 * dblk + ((lr >> 1) & 1)) ^ vswz_m(vr0)) << 4) + 8 * (lr & 1));
     const float mu = m > kNegBig ? m : 0.f;
-    float st[2][4];
+    float st[4];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        st[kb][e] = fmaf(s[kb][e], c, -mu);
-        if (partial && key0 + kb * 16 + 4 * lq + e >= t1) st[kb][e] = -INFINITY;
-      }
+    for (int e = 0; e < 4; ++e) {
+      st[e] = fmaf(s[e], c, -mu);
+      if (partial && key0 + 4 * lq + e >= t1) st[e] = -INFINITY;
+    }
     float mu_now = mu;
     auto rescale = [&]() {
-      float mx = st[0][0];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) mx = fmaxf(mx, st[kb][e]);
+      const float mx = fmaxf(fmaxf(st[0], st[1]), fmaxf(st[2], st[3]));
       const float ax = max_xor32(max_xor16(mx)) + mu_now;  // the head's maximum
       if (ax > m + kRescaleSlack) {
         const float al = fast_exp2(m - ax);
@@ -1033,33 +1017,29 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
         m = ax;
         const float dd = mu_now - ax;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) st[kb][e] += dd;
+        for (int e = 0; e < 4; ++e) st[e] += dd;
         mu_now = ax;
       }
     };
-    // P^T operands, keys as in vf: each fp32 weight w as fp16 hi + lo
-    // (w - hi rounded), two PV MFMAs, so the product keeps ~22 bits of w and
-    // the result does not depend on where a split's reference point lies.
-    f16x8 ph, pl;
+    // P^T operands: each fp32 weight w as fp16 hi + lo (w - hi rounded), two
+    // PV MFMAs, so the product keeps ~22 bits of w and the result does not
+    // depend on where a split's reference point lies.
+    f16x4 ph, pl;
     auto weights = [&]() {
       float ls = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float w = fast_exp2(st[kb][e]);
-          const f16 h = (f16)w;
-          ph[kb * 4 + e] = h;
-          pl[kb * 4 + e] = (f16)(w - (float)h);
-          ls += w;
-        }
+      for (int e = 0; e < 4; ++e) {
+        const float w = fast_exp2(st[e]);
+        const f16 h = (f16)w;
+        ph[e] = h;
+        pl[e] = (f16)(w - (float)h);
+        ls += w;
+      }
       return ls;
     };
     // The maximum is taken for a head's first keys (so its largest weight
     // is never below 1) and when a weight may exceed fp16 (a lane's sum of
-    // 8 weights reaches 65504: the maximum then exceeds m by more than 12,
+    // 4 weights reaches 65504: the maximum then exceeds m by more than 13,
     // so m moves); both tests are wavefront-wide.
     if (__builtin_amdgcn_ballot_w64(m == kNegBig)) rescale();
     float ls = weights();
@@ -1071,8 +1051,8 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     lds_reads_done(vf);
 #pragma unroll
     for (int dblk = 0; dblk < 8; ++dblk) {
-      o[dblk] = mfma16x16x32(vf[dblk], ph, o[dblk]);
-      o[dblk] = mfma16x16x32(vf[dblk], pl, o[dblk]);
+      o[dblk] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dblk], ph, o[dblk], 0, 0, 0);
+      o[dblk] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dblk], pl, o[dblk], 0, 0, 0);
     }
   };
 
@@ -1288,8 +1268,7 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   }
   // One workgroup per KV head: the matrix-core kernel where its
   // G-independent work per key wins (see decode_mfma_kernel).
-  const int split_keys = (c.span + a.nsplit - 1) / a.nsplit;
-  if (c.kernel < 0 && (s.group == 8 || (s.group == 5 && split_keys >= 512))) return mfma();
+  if (c.kernel < 0 && s.group >= 5) return mfma();
   switch (s.group) {
     case 1: return launch_qo<1>(s, a, c, stream);
     case 2: return launch_qo<2>(s, a, c, stream);

@@ -201,13 +201,14 @@ def test_matrix_core_rising_and_negative_scores(offset):
 
 def test_default_kernel_choice():
     """Without nwd_set_decode_kernel a call that runs one workgroup per KV
-    head takes the matrix-core kernel for G = 8, and for G = 5 with 512 or
-    more keys per split, the dot-product kernel otherwise: the default
-    result equals the chosen kernel's bits."""
+    head takes the matrix-core kernel for G >= 5 and the dot-product kernel
+    otherwise; a call that runs one workgroup per query head takes the
+    dot-product kernel. The default result equals the chosen kernel's bits."""
     cases = [  # (H, Hkv, L, splits, expected kernel)
         (64, 8, 3000, 0, MFMA),
-        (40, 8, 20000, 32, MFMA),  # 625 keys per split
-        (40, 8, 3000, 32, VALU),   # 94
+        (40, 8, 20000, 32, MFMA),
+        (40, 8, 3000, 32, MFMA),
+        (40, 8, 1000, 0, VALU),    # 6 splits x 40 heads <= 256: one workgroup per query head
         (32, 8, 20000, 32, VALU),
         (16, 8, 3000, 0, VALU),
     ]
