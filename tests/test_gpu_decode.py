@@ -172,16 +172,19 @@ def test_config2_past4096_64_steps(path):
     assert worst < TOL, worst
 
 
-def test_config3_past32768_outliers_split_k():
-    """L = 32769 with 1% +-8 outliers; split-K + merge, and split-count invariance."""
+@pytest.mark.parametrize("kernel", [None, 1])
+def test_config3_past32768_outliers_split_k(kernel):
+    """L = 32769 with 1% +-8 outliers; split-K + merge, and split-count
+    invariance; on the default split kernel and on the matrix-core one."""
     H, Hkv, P = 32, 8, 32768
-    say("config3 past=32768")
+    say(f"config3 past=32768 kernel={kernel}")
     g = rng(3)
     k, v = kv_rows(g, P + 1, Hkv, outlier_frac=0.01)
     q = normal_f16(g, (1, H, D))
     cap = P + 1
     want = oracle.sparse_attn_f32(f32(q[0]), f32(k), f32(v), threads=0)
     with nw.AttnContext(H, Hkv, cap) as ctx:
+        ctx.set_decode_kernel(kernel)
         kc = dev(to_cache([k[:P]], Hkv, cap))
         vc = dev(to_cache([v[:P]], Hkv, cap))
         pos = pos_tensor([P])
@@ -208,17 +211,19 @@ def test_config3_past32768_outliers_split_k():
         assert max_abs(outs[n], outs[0]) < 1e-3
 
 
-def test_config4_ragged_batch64():
+@pytest.mark.parametrize("kernel", [None, 1])
+def test_config4_ragged_batch64(kernel):
     """64 sequences, past lengths U{512..16384}, one query each: one new token
     per sequence appended at pos = past and attended, both as nwd_kv_append +
     nwd_decode_attn and as the fused nwd_append_decode the benchmark times.
     The fused path writes the same cache bits and gives the same output bits;
-    every sequence matches the oracle."""
+    every sequence matches the oracle. On the default split kernel and on
+    the matrix-core one."""
     H, Hkv, B = 32, 8, 64
     g = rng(4)
     past = g.integers(512, 16385, size=B)
     cap = int(past.max()) + 1
-    say(f"config4 ragged B={B} cap={cap} sum_L={int(past.sum() + B)}")
+    say(f"config4 ragged B={B} cap={cap} sum_L={int(past.sum() + B)} kernel={kernel}")
     kc = randn_f16((B, Hkv, cap, D), 40)
     vc = randn_f16((B, Hkv, cap, D), 41)
     q = randn_f16((B, H, D), 42)
@@ -226,6 +231,7 @@ def test_config4_ragged_batch64():
     vn = randn_f16((B, Hkv, D), 44)
     pos = pos_tensor(past.tolist())
     with nw.AttnContext(H, Hkv, cap, max_batch=B) as ctx:
+        ctx.set_decode_kernel(kernel)
         kc2, vc2 = kc.clone(), vc.clone()
         ctx.kv_append(kn[:, None], vn[:, None], kc, vc, pos, B, 1)
         out = _decode(ctx, q, kc, vc, pos, B, max_len=cap)
