@@ -543,7 +543,7 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     res["n_heads"] = heads
     # the launch's choice of split kernel for this shape (see nwd_decode.hip)
     per_kv_head = heads * splits > 256
-    res["split_kernel"] = DECODE_KERNELS[1 if per_kv_head and heads // HKV >= 5 else 0]
+    res["split_kernel"] = DECODE_KERNELS[1 if per_kv_head and heads // HKV >= 5 else 0]  # B = 1
     # The dominant kernel's duration: HIP events at the split kernel's start
     # and end (eager calls), or the whole graph-timed call when that is
     # shorter (the events include the dispatch latency of an eager launch,
@@ -574,14 +574,23 @@ def run_ragged(torch, nw, steps: int, warmup: int):
     wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
     _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
     us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
+    by_kernel = {}
+    for k in (0, 1):  # the decode call on each split kernel (nwd_set_decode_kernel)
+        wl.ctx.set_decode_kernel(k)
+        _, ms_k = time_graph(torch, wl, steps, 0, append=False, reps=3)
+        by_kernel[DECODE_KERNELS[k]] = ms_k * 1e3 / steps
+    wl.ctx.set_decode_kernel(None)
     b = wl.mean_kv_bytes(steps)
     res = {"workload": "ragged-64", "desc": EXTRA_WORKLOADS["ragged-64"], "us_per_step": us_step,
            "decode_us": us_main, "wall_s": wall, "mean_kv_bytes": b,
            "splits": wl.ctx.decode_splits(wl.batch, wl.cap),
+           # the launch's choice for this batch of 64 (see nwd_decode.hip)
+           "split_kernel": DECODE_KERNELS[1 if H // HKV >= 4 else 0],
+           "decode_us_by_kernel": by_kernel,
            "gbs": b / (us_step * 1e-6) / 1e9, "decode_gbs": b / (us_main * 1e-6) / 1e9}
     res["roofline"] = hbm_roofline(res["decode_gbs"],
-                                   "nwd_decode_attn (split + merge kernels, one call)", b,
-                                   measured_traffic("ragged-64"))
+                                   "nwd_decode_attn (split + merge kernels, one call; split kernel "
+                                   f"{res['split_kernel']})", b, measured_traffic("ragged-64"))
     log(f"[bench] ragged-64: step {us_step:.1f} us, decode {us_main:.1f} us "
         f"({res['decode_gbs']:.1f} GB/s)")
     wl.ctx.close()

@@ -763,9 +763,13 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 //   G = 8: 1K 11.0 / 8.6, 4K 12.2 / 9.9, 16K 23.5 / 17.3, 32K 38.9 / 26.7
 // (with 1% of K/V at +-8, whose larger score swings move the dot-product
 // kernel's per-row references more often, 32K: 27.0 / 26.3, 28.6 / 26.6,
-// 39.0 / 26.8). The launch takes it for one-workgroup-per-KV-head calls
-// with G >= 5 (G = 4, the shape the dot-product kernel was built for,
-// keeps that kernel); nwd_set_decode_kernel forces either.
+// 39.0 / 26.8). Batches at G = 4, N(0,1): B 2 x 8K 15.5-16.4 / 15.5-15.8,
+// 8 x 16K 98.6 / 89.6, 12 x 8K 65.0 / 61.0, 16 x 256 8.9 / 8.4, 16 x 8K
+// 90.3 / 83.4, 64 x 2K 86.8 / 81.3, 64 ragged 512..16K 422 / 409 (ties at
+// 4 x 8K, 8 x 4K, 16 x 2K). The launch takes it for one-workgroup-per-KV-
+// head calls with G >= 5, or G = 4 and batch >= 2 (at B = 1 and G = 4 the
+// dot-product kernel, which that shape was built for, stays faster);
+// nwd_set_decode_kernel forces either.
 // Four wavefronts, each owning one 16-key block of every 64-key workgroup
 // iteration (keys t0 + 64 it + 16 w ..), independent of each other inside
 // the loop:
@@ -1266,9 +1270,9 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
       default: break;  // group 1 is already one workgroup per query head
     }
   }
-  // One workgroup per KV head: the matrix-core kernel where its
-  // G-independent work per key wins (see decode_mfma_kernel).
-  if (c.kernel < 0 && s.group >= 5) return mfma();
+  // One workgroup per KV head: the matrix-core kernel where it measured
+  // faster (see decode_mfma_kernel).
+  if (c.kernel < 0 && (s.group >= 5 || (s.group == 4 && c.batch >= 2))) return mfma();
   switch (s.group) {
     case 1: return launch_qo<1>(s, a, c, stream);
     case 2: return launch_qo<2>(s, a, c, stream);

@@ -201,34 +201,40 @@ def test_matrix_core_rising_and_negative_scores(offset):
 
 def test_default_kernel_choice():
     """Without nwd_set_decode_kernel a call that runs one workgroup per KV
-    head takes the matrix-core kernel for G >= 5 and the dot-product kernel
-    otherwise; a call that runs one workgroup per query head takes the
-    dot-product kernel. The default result equals the chosen kernel's bits."""
-    cases = [  # (H, Hkv, L, splits, expected kernel)
-        (64, 8, 3000, 0, MFMA),
-        (40, 8, 20000, 32, MFMA),
-        (40, 8, 3000, 32, MFMA),
-        (40, 8, 1000, 0, VALU),    # 6 splits x 40 heads <= 256: one workgroup per query head
-        (32, 8, 20000, 32, VALU),
-        (16, 8, 3000, 0, VALU),
+    head takes the matrix-core kernel for G >= 5, or G = 4 and batch >= 2,
+    and the dot-product kernel otherwise; a call that runs one workgroup per
+    query head takes the dot-product kernel. The default result equals the
+    chosen kernel's bits."""
+    cases = [  # (H, Hkv, B, L, splits, expected kernel)
+        (64, 8, 1, 3000, 0, MFMA),
+        (40, 8, 1, 20000, 32, MFMA),
+        (40, 8, 1, 3000, 32, MFMA),
+        (40, 8, 1, 1000, 0, VALU),   # 6 splits x 40 heads <= 256: one workgroup per query head
+        (32, 8, 1, 20000, 32, VALU),
+        (32, 8, 2, 3000, 0, MFMA),
+        (32, 8, 9, 300, 0, MFMA),
+        (16, 8, 1, 3000, 0, VALU),
+        (16, 8, 4, 3000, 0, VALU),
     ]
-    for H, Hkv, L, n, kernel in cases:
-        say(f"default kernel H={H} Hkv={Hkv} L={L} splits={n}")
-        g = rng(990 + H + L)
-        k, v = kv_rows(g, L, Hkv)
-        q = normal_f16(g, (1, H, D))
-        with nw.AttnContext(H, Hkv, L, o_dtype="f32") as ctx:
+    for H, Hkv, B, L, n, kernel in cases:
+        say(f"default kernel H={H} Hkv={Hkv} B={B} L={L} splits={n}")
+        g = rng(990 + H + L + B)
+        rows = [kv_rows(g, L - 7 * b, Hkv) for b in range(B)]
+        q = normal_f16(g, (B, H, D))
+        with nw.AttnContext(H, Hkv, L, max_batch=B, o_dtype="f32") as ctx:
             ctx.set_decode_splits(n)
-            kc, vc = dev(to_cache([k], Hkv, L)), dev(to_cache([v], Hkv, L))
-            pos = pos_tensor([L - 1])
-            default = _decode(ctx, -1, dev(q), kc, vc, pos, 1)
-            chosen = _decode(ctx, kernel, dev(q), kc, vc, pos, 1)
-            other = _decode(ctx, 1 - kernel, dev(q), kc, vc, pos, 1)
-            assert np.array_equal(default, chosen), (H, L)
-            assert max_abs(default, other) < AGREE, (H, L)
+            kc = dev(to_cache([r[0] for r in rows], Hkv, L))
+            vc = dev(to_cache([r[1] for r in rows], Hkv, L))
+            pos = pos_tensor([L - 1 - 7 * b for b in range(B)])
+            default = _decode(ctx, -1, dev(q), kc, vc, pos, B)
+            chosen = _decode(ctx, kernel, dev(q), kc, vc, pos, B)
+            other = _decode(ctx, 1 - kernel, dev(q), kc, vc, pos, B)
+            assert np.array_equal(default, chosen), (H, B, L)
+            assert max_abs(default, other) < AGREE, (H, B, L)
             assert ctx.device_status() == nw.NWD_OK
-        want = oracle.sparse_attn_f32(f32(q[0]), f32(k), f32(v))
-        assert max_abs(default[0], want) < TOL, (H, L)
+        for b in range(B):
+            want = oracle.sparse_attn_f32(f32(q[b]), f32(rows[b][0]), f32(rows[b][1]))
+            assert max_abs(default[b], want) < TOL, (H, B, L, b)
 
 
 def test_set_decode_kernel_rejects_unknown_values():
