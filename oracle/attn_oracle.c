@@ -1,7 +1,7 @@
 /*
  * attn_oracle.c — CPU restatement of the reference decode-attention path.
  *
- * TEST INFRASTRUCTURE ONLY. This file is the checker for the HIP library:
+ * TEST INFRASTRUCTURE ONLY. The HIP library's results are checked against it:
  * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg load
  * it, and never as the thing measured or shipped. The product path
  * (libnwd_attn.so) does not link, load or call it.

@@ -1,6 +1,6 @@
 """ctypes binding of oracle/liboracle.so — TEST INFRASTRUCTURE ONLY.
 
-The oracle is the checker of the HIP library. Only tests/,
+The oracle is what the HIP library's results are checked against. Only tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.
 Each wrapped function cites the reference file:line its C code restates (see
 attn_oracle.c). Inputs are numpy arrays in the reference's layouts:

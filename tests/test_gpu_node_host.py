@@ -142,7 +142,7 @@ def test_node_host_bad_position_reported_at_readback():
 
 
 def test_node_addon_rejects_copies_past_a_buffer():
-    """ADVICE: a wrongly sized typed array must not write past a device
+    """A wrongly sized typed array must not write past a device
     buffer; the addon refuses copies that do not fit inside one allocation,
     and AttentionSlice checks the q/k/v/attnO lengths."""
     script = r"""

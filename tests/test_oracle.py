@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/attn_oracle.c) before it is used as a checker.
+"""Pins the CPU oracle (oracle/attn_oracle.c) before the GPU results are checked against it.
 
 Every oracle function is checked against something it does not restate:
 numpy's float16 conversion, closed forms, an independent numpy float64
