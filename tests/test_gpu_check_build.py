@@ -69,6 +69,7 @@ def _same(run, prod, chk, outputs):
     (8, 8, (1000,), "f16", 0, None),
     (64, 8, (17, 2500), "f32", 0, None),
     (40, 8, (153,), "f16", 0, None),
+    (40, 8, (3000, 3900), "f32", 0, None),  # the matrix-core split kernel
 ])
 def test_decode_checked_build_matches(H, Hkv, lens, o_dtype, splits, separate):
     say("check build decode", H, Hkv, lens, o_dtype, splits, separate)
