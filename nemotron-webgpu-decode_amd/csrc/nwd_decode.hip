@@ -866,7 +866,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
       f.k[db] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
     }
   };
-  // The block's V rows into ring slot `slot`: 8 copies of 4 rows (1 KB);
+  // The block's 16 V rows into ring slot `slot`: 4 copies of 4 rows (1 KB);
   // lane l fills physical chunk l % 16 of row 4i + l / 16, so it loads the
   // logical chunk the swizzle puts there.
   auto load_v = [&](const __amdgpu_buffer_rsrc_t rv, int it, int slot) {
