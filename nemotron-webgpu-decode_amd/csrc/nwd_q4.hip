@@ -105,9 +105,14 @@ __device__ inline void q4_columns(const Q4Mat& m, int n_blocks, int first, int e
     for (int j = 0; j < kSlots; ++j) {
       const int blk = min(first + lane + 64 * j, end - 1);
       idx[c][j] = (int64_t)col * n_blocks + blk;
-      qv[c][j] = *reinterpret_cast<const uint4*>(m.quant + idx[c][j] * 16);
-      sc[c][j] = m.scales[idx[c][j]];
-      zb[c][j] = m.zp[idx[c][j] >> 1];
+      // non-temporal: each weight byte is read once per call (1-2% faster
+      // here; the wide form below keeps the default policy, under which the
+      // lm_head measured 52.5 us against 56.4 with its quant stream, 73.1
+      // with all three streams, non-temporal)
+      qv[c][j] = __builtin_bit_cast(
+          uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(m.quant + idx[c][j] * 16)));
+      sc[c][j] = __builtin_nontemporal_load(m.scales + idx[c][j]);
+      zb[c][j] = __builtin_nontemporal_load(m.zp + (idx[c][j] >> 1));
     }
   }
   __builtin_amdgcn_sched_barrier(0);  // every load above is issued before any compute
