@@ -25,6 +25,12 @@
 // uniforms. q/k/v/attnO stay f32, the reference's activation type, so the
 // q/k/v GEMVs and the o_proj GEMV bind unchanged.
 //
+// A prompt can also go through the attention layers as chunks (beginPrefill,
+// prefillLayer, endPrefill): the reference runs each prompt token through the
+// whole decode step (generate, runtime.js:640-643); here a chunk's rows are
+// appended with one kvAppend and attended with one causal prefill call per
+// layer, with the same result for every token.
+//
 // With the layer's 4-bit weights registered (setLayerWeights), the whole
 // attention layer from the normalised hidden state runs on the library too:
 // the reference's L-q, L-k, L-v, L-kvK, L-kvV, L-attn, L-o, L-add
@@ -70,6 +76,7 @@ class AttentionSlice {
       this.vCache.set(i, addon.malloc(this.cacheBytes));
     }
     this.pos = addon.malloc(4);
+    this.chunk = null;         // prefill buffers {n, q, k, v, o}, grown on demand
     this.weights = new Map();  // layer -> {q, k, v, o} nwd_q4_weight descriptors
     this.owned = [];           // device buffers uploadQ4 allocated
     this.graphs = [];          // token graphs captureToken made
@@ -174,6 +181,54 @@ class AttentionSlice {
                  this.seq + 1);
   }
 
+  // Chunked prefill of n prompt tokens (the reference's generate loop,
+  // runtime.js:640-643, runs them one decode step each): guard and position
+  // as beginStep, for the whole chunk.
+  beginPrefill(n) {
+    if (!(Number.isInteger(n) && n >= 1)) throw new Error(`beginPrefill: bad token count ${n}`);
+    if (this.seq + n > this.maxSeq)
+      throw new Error(`seq ${this.seq} + ${n} prompt tokens exceeds maxSeq ${this.maxSeq}`);
+    if (!this.chunk || this.chunk.n < n) {
+      if (this.chunk) for (const b of ['q', 'k', 'v', 'o']) addon.free(this.chunk[b]);
+      const qBytes = n * this.heads * this.headDim * 4;
+      const kvBytes = n * this.kvHeads * this.headDim * 4;
+      this.chunk = { n, q: addon.malloc(qBytes), k: addon.malloc(kvBytes), v: addon.malloc(kvBytes),
+                     o: addon.malloc(qBytes) };
+    }
+    this.chunkLen = n;
+    addon.setI32(this.pos, this.seq);
+  }
+
+  // The chunk's q [n][heads][headDim], k and v [n][kvHeads][headDim] (f32)
+  // for attention layer i: the rows go to the caches at seq .. seq+n-1
+  // (kvAppend), then query j attends keys 0 .. seq+j (prefill).
+  prefillLayer(i, q, k, v) {
+    if (!this.kCache.has(i)) throw new Error(`layer ${i} is not an attention layer`);
+    const n = this.chunkLen;
+    expectF32(q, n * this.heads * this.headDim, 'prefillLayer q');
+    expectF32(k, n * this.kvHeads * this.headDim, 'prefillLayer k');
+    expectF32(v, n * this.kvHeads * this.headDim, 'prefillLayer v');
+    addon.upload(this.chunk.q, q);
+    addon.upload(this.chunk.k, k);
+    addon.upload(this.chunk.v, v);
+    addon.kvAppend(this.ctx, this.chunk.k, this.chunk.v, this.kCache.get(i), this.vCache.get(i),
+                   this.pos, 1, n);
+    addon.prefill(this.ctx, this.chunk.q, this.kCache.get(i), this.vCache.get(i), this.pos,
+                  this.chunk.o, 1, n, this.seq + n);
+  }
+
+  // The last prefillLayer's output, [n][heads][headDim] f32.
+  readPrefillO(out = new Float32Array(this.chunkLen * this.heads * this.headDim)) {
+    expectF32(out, this.chunkLen * this.heads * this.headDim, 'readPrefillO');
+    this.checkStatus();
+    addon.download(out, this.chunk.o);
+    return out;
+  }
+
+  endPrefill() {
+    this.seq += this.chunkLen;
+  }
+
   // runtime.js:467: seq++ without waiting for the device.
   endStep() {
     this.seq += 1;
@@ -196,6 +251,7 @@ class AttentionSlice {
 
   destroy() {
     for (const g of this.graphs) addon.graphDestroy(g);
+    if (this.chunk) for (const b of ['q', 'k', 'v', 'o']) addon.free(this.chunk[b]);
     for (const p of [this.q, this.k, this.v, this.attnO, this.pos, ...this.owned]) addon.free(p);
     for (const i of this.layers) {
       addon.free(this.kCache.get(i));

@@ -5,7 +5,10 @@
 // LCG; inputs and attention outputs are written to <outDir> for the Python
 // parity test, which checks them against the oracle.
 //
-// usage: node check_attention.js <outDir> [heads kvHeads tokens maxSeq]
+// usage: node check_attention.js <outDir> [heads kvHeads tokens maxSeq [chunks]]
+// chunks (e.g. "37,64"): the first tokens go through chunked prefill in
+// chunks of these sizes, the rest one decode step each; the inputs are the
+// same either way.
 const fs = require('fs');
 const path = require('path');
 const { AttentionSlice } = require('./attention_layer');
@@ -39,34 +42,64 @@ function main() {
   const headDim = 128;
   fs.mkdirSync(outDir, { recursive: true });
   const slice = new AttentionSlice({ heads, kvHeads, headDim, maxSeq });
+  const chunks = (process.argv[7] || '').split(',').filter((x) => x).map(Number);
   const rand = lcg(20260512);
+  const nL = slice.layers.length;
+  // inputs of token t, layer li at t * nL + li, drawn in that order
   const qAll = [];
   const kAll = [];
   const vAll = [];
-  const oAll = [];
   for (let t = 0; t < tokens; t++) {
+    for (let li = 0; li < nL; li++) {
+      qAll.push(normals(rand, heads * headDim));
+      kAll.push(normals(rand, kvHeads * headDim));
+      vAll.push(normals(rand, kvHeads * headDim));
+    }
+  }
+  const oAll = new Array(tokens * nL);
+  const gather = (arrs, t0, n, li, w) => {
+    const out = new Float32Array(n * w);
+    for (let j = 0; j < n; j++) out.set(arrs[(t0 + j) * nL + li], j * w);
+    return out;
+  };
+  let t = 0;
+  for (const n of chunks) {
+    slice.beginPrefill(n);
+    slice.layers.forEach((layer, li) => {
+      slice.prefillLayer(layer, gather(qAll, t, n, li, heads * headDim),
+                         gather(kAll, t, n, li, kvHeads * headDim),
+                         gather(vAll, t, n, li, kvHeads * headDim));
+      const o = slice.readPrefillO();
+      for (let j = 0; j < n; j++)
+        oAll[(t + j) * nL + li] = o.slice(j * heads * headDim, (j + 1) * heads * headDim);
+    });
+    slice.endPrefill();
+    t += n;
+  }
+  for (; t < tokens; t++) {
     slice.beginStep();
-    for (const layer of slice.layers) {
-      const q = normals(rand, heads * headDim);
-      const k = normals(rand, kvHeads * headDim);
-      const v = normals(rand, kvHeads * headDim);
-      slice.setQKV(q, k, v);
+    slice.layers.forEach((layer, li) => {
+      const at = t * nL + li;
+      slice.setQKV(qAll[at], kAll[at], vAll[at]);
       if ((t + layer) % 2 === 0) slice.encodeLayer(layer);
       else slice.encodeLayerTwoCalls(layer);
-      qAll.push(q);
-      kAll.push(k);
-      vAll.push(v);
-      oAll.push(slice.readAttnO());
-    }
+      oAll[at] = slice.readAttnO();
+    });
     slice.endStep();
   }
   // the maxSeq guard (runtime.js:448) must throw, not write past the cache
   let guard = 'no-throw';
+  let prefillGuard = 'no-throw';
   if (tokens === maxSeq) {
     try {
       slice.beginStep();
     } catch (e) {
       guard = String(e.message);
+    }
+    try {
+      slice.beginPrefill(1);
+    } catch (e) {
+      prefillGuard = String(e.message);
     }
   }
   const cat = (arrs) => Buffer.concat(arrs.map((a) => Buffer.from(a.buffer, a.byteOffset, a.byteLength)));
@@ -75,7 +108,7 @@ function main() {
   fs.writeFileSync(path.join(outDir, 'v.f32'), cat(vAll));
   fs.writeFileSync(path.join(outDir, 'o.f32'), cat(oAll));
   fs.writeFileSync(path.join(outDir, 'manifest.json'), JSON.stringify({
-    heads, kvHeads, headDim, tokens, maxSeq, layers: slice.layers, guard,
+    heads, kvHeads, headDim, tokens, maxSeq, layers: slice.layers, guard, prefillGuard, chunks,
   }));
   slice.destroy();
   console.log(`check_attention: ${tokens} tokens x ${slice.layers.length} layers written to ${outDir}`);

@@ -20,11 +20,11 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")]
 
 
-def _run(tmp_path, heads, kv_heads, tokens, max_seq):
-    out = tmp_path / f"run_{heads}_{tokens}"
-    print(f"node check_attention {heads}/{kv_heads} tokens={tokens}", flush=True)
+def _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks=""):
+    out = tmp_path / f"run_{heads}_{tokens}_{chunks.replace(',', '-')}"
+    print(f"node check_attention {heads}/{kv_heads} tokens={tokens} chunks={chunks}", flush=True)
     res = subprocess.run(["node", str(JS / "check_attention.js"), str(out), str(heads),
-                          str(kv_heads), str(tokens), str(max_seq)],
+                          str(kv_heads), str(tokens), str(max_seq), chunks],
                          capture_output=True, text=True, timeout=180)
     assert res.returncode == 0, res.stdout + res.stderr
     man = json.loads((out / "manifest.json").read_text())
@@ -37,9 +37,19 @@ def _run(tmp_path, heads, kv_heads, tokens, max_seq):
     return man, q, k, v, o
 
 
-@pytest.mark.parametrize("heads,kv_heads,tokens,max_seq", [(40, 8, 153, 256), (32, 8, 256, 256)])
-def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq):
-    man, q, k, v, o = _run(tmp_path, heads, kv_heads, tokens, max_seq)
+@pytest.mark.parametrize("heads,kv_heads,tokens,max_seq,chunks", [
+    (40, 8, 153, 256, ""),
+    (32, 8, 256, 256, ""),
+    # a 101-token prompt as two prefill chunks, then decode steps
+    (40, 8, 153, 256, "37,64"),
+    # the whole capacity through prefill chunks, then both guards
+    (32, 8, 256, 256, "1,127,128"),
+])
+def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, chunks):
+    """Every token through the decode step, or the first ones through chunked
+    prefill (query t of a chunk attends keys 0..t, the reference's result for
+    a prompt run token by token)."""
+    man, q, k, v, o = _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks)
     # the cache holds the f32 rows rounded to fp16 (kv_append's rule)
     kh = oracle.f16_to_f32(oracle.f32_to_f16(k))
     vh = oracle.f16_to_f32(oracle.f32_to_f16(v))
@@ -52,6 +62,7 @@ def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq):
     assert worst < 2e-3, worst
     if tokens == max_seq:  # engine/runtime.js:448: the next step must throw
         assert "exceeds maxSeq" in man["guard"]
+        assert "exceeds maxSeq" in man["prefillGuard"]
 
 
 @pytest.mark.parametrize("mode", ["eager", "graph"])
