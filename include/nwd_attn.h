@@ -172,7 +172,9 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * pos0[b] .. pos0[b] + n_new - 1 (nwd_kv_append with n_tokens = n_new).
  * Query i of sequence b attends keys 0 .. pos0[b] + i. q and out are
  * [batch][n_new][n_heads][head_dim]. QK^T and PV run on fp16 MFMA with fp32
- * accumulation. max_len bounds pos0[b] + n_new (0 means max_seq). */
+ * accumulation: an fp32 q is scaled by scale * log2(e) and rounded to fp16
+ * as it is loaded, so it carries fp16 precision (nwd_decode_attn keeps an
+ * fp32 q in fp32). max_len bounds pos0[b] + n_new (0 means max_seq). */
 int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
                      const void* v_cache, const int32_t* pos0, void* out,
                      int32_t batch, int32_t n_new, int32_t max_len,

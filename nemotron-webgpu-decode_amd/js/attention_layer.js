@@ -43,6 +43,7 @@ const addon = require(ADDON);
 
 // Nemotron-3-Nano-4B attention shapes (engine/config.js:10-12,24,31).
 const NANO4B = { hidden: 3136, heads: 40, kvHeads: 8, headDim: 128, maxSeq: 256 };
+const Q4_PLAIN = 0;       // nwd_q4_gemv epilogue: y = W.a
 const Q4_ACCUMULATE = 2;  // nwd_q4_gemv epilogue: y = y + W.a (o_proj + residual add)
 const ATTN_LAYERS = [12, 17, 24, 32];
 
@@ -217,7 +218,26 @@ class AttentionSlice {
                   this.chunk.o, 1, n, this.seq + n);
   }
 
-  // The last prefillLayer's output, [n][heads][headDim] f32.
+  // runtime.js:386-393 for the chunk's n tokens through attention layer i,
+  // from their normalised hidden states hNorm (f32 [n][hidden], device):
+  // the q, k and v projections as n-row GEMVs, the k/v rows appended and the
+  // chunk attended, and o_proj added into the residual rows h (f32
+  // [n][hidden], device).
+  prefillLayerFromHidden(i, hNorm, h) {
+    const w = this.weights.get(i);
+    if (!w) throw new Error(`layer ${i} has no weights (setLayerWeights)`);
+    const n = this.chunkLen;
+    addon.q4Gemv(this.ctx, hNorm, w.q, this.chunk.q, n, Q4_PLAIN);
+    addon.q4Gemv(this.ctx, hNorm, w.k, this.chunk.k, n, Q4_PLAIN);
+    addon.q4Gemv(this.ctx, hNorm, w.v, this.chunk.v, n, Q4_PLAIN);
+    addon.kvAppend(this.ctx, this.chunk.k, this.chunk.v, this.kCache.get(i), this.vCache.get(i),
+                   this.pos, 1, n);
+    addon.prefill(this.ctx, this.chunk.q, this.kCache.get(i), this.vCache.get(i), this.pos,
+                  this.chunk.o, 1, n, this.seq + n);
+    addon.q4Gemv(this.ctx, this.chunk.o, w.o, h, n, Q4_ACCUMULATE);
+  }
+
+  // The last prefill's attention output, [n][heads][headDim] f32.
   readPrefillO(out = new Float32Array(this.chunkLen * this.heads * this.headDim)) {
     expectF32(out, this.chunkLen * this.heads * this.headDim, 'readPrefillO');
     this.checkStatus();

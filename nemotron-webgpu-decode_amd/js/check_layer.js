@@ -7,7 +7,9 @@
 // to <outDir> for the Python parity test, which checks them against the
 // oracle.
 //
-// usage: node check_layer.js <outDir> [hidden tokens]
+// usage: node check_layer.js <outDir> [hidden tokens [eager|graph|prefill]]
+// prefill: the tokens go through the layer as two prompt chunks
+// (AttentionSlice.prefillLayerFromHidden), with the same inputs.
 const fs = require('fs');
 const path = require('path');
 const { AttentionSlice, addon } = require('./attention_layer');
@@ -48,7 +50,8 @@ function main() {
   const outDir = process.argv[2];
   const hidden = Number(process.argv[3] || 512);
   const tokens = Number(process.argv[4] || 12);
-  const useGraph = process.argv[5] === 'graph';  // replay one captured token graph
+  const mode = process.argv[5] || 'eager';
+  const useGraph = mode === 'graph';  // replay one captured token graph
   const heads = 40;
   const kvHeads = 8;
   const headDim = 128;
@@ -66,11 +69,40 @@ function main() {
   for (const [name, w] of Object.entries(hostW)) devW[name] = slice.uploadQ4(w);
   slice.setLayerWeights(layer, devW);
 
+  const outs = { hnorm: [], hin: [], attn: [], hout: [] };
+  if (mode === 'prefill') {
+    const first = Math.floor(tokens / 2);
+    for (const n of [first, tokens - first]) {
+      const hNorm = new Float32Array(n * hidden);
+      const hIn = new Float32Array(n * hidden);
+      for (let j = 0; j < n; j++) {  // the per-token order of the token loop below
+        hNorm.set(normals(rand, hidden), j * hidden);
+        hIn.set(normals(rand, hidden), j * hidden);
+      }
+      const hNormDev = addon.malloc(n * hidden * 4);
+      const hDev = addon.malloc(n * hidden * 4);
+      addon.upload(hNormDev, hNorm);
+      addon.upload(hDev, hIn);
+      slice.beginPrefill(n);
+      slice.prefillLayerFromHidden(layer, hNormDev, hDev);
+      const attn = slice.readPrefillO();
+      slice.endPrefill();
+      const hOut = new Float32Array(n * hidden);
+      addon.download(hOut, hDev);
+      for (let j = 0; j < n; j++) {
+        outs.hnorm.push(hNorm.slice(j * hidden, (j + 1) * hidden));
+        outs.hin.push(hIn.slice(j * hidden, (j + 1) * hidden));
+        outs.attn.push(attn.slice(j * heads * headDim, (j + 1) * heads * headDim));
+        outs.hout.push(hOut.slice(j * hidden, (j + 1) * hidden));
+      }
+      addon.free(hNormDev);
+      addon.free(hDev);
+    }
+  }
   const hNormDev = addon.malloc(hidden * 4);
   const hDev = addon.malloc(hidden * 4);
   const graph = useGraph ? slice.captureToken(hNormDev, hDev) : null;
-  const outs = { hnorm: [], hin: [], attn: [], hout: [] };
-  for (let t = 0; t < tokens; t++) {
+  for (let t = mode === 'prefill' ? tokens : 0; t < tokens; t++) {
     const hNorm = normals(rand, hidden);
     const hIn = normals(rand, hidden);
     addon.upload(hNormDev, hNorm);
@@ -97,7 +129,7 @@ function main() {
     fs.writeFileSync(path.join(outDir, `w${name}.zp`), bytes(w.zp));
   }
   fs.writeFileSync(path.join(outDir, 'manifest.json'), JSON.stringify({
-    heads, kvHeads, headDim, hidden, tokens, graph: useGraph,
+    heads, kvHeads, headDim, hidden, tokens, graph: useGraph, mode,
   }));
   addon.free(hNormDev);
   addon.free(hDev);

@@ -65,7 +65,7 @@ def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, ch
         assert "exceeds maxSeq" in man["prefillGuard"]
 
 
-@pytest.mark.parametrize("mode", ["eager", "graph"])
+@pytest.mark.parametrize("mode", ["eager", "graph", "prefill"])
 def test_node_host_full_layer_from_hidden_state(tmp_path, mode):
     """js/check_layer.js: one attention layer per token from the normalised
     hidden state (q/k/v projections + kv_append, attention, o_proj + residual
@@ -75,7 +75,9 @@ def test_node_host_full_layer_from_hidden_state(tmp_path, mode):
     h_in + o_proj(attention output) in float64 (1e-6 of sum |w a|, plus one
     f32 rounding of the add). `graph`: the token's calls are captured once
     into a HIP graph and replayed every token (AttentionSlice.captureToken,
-    attention sized for the capacity)."""
+    attention sized for the capacity). `prefill`: the 12 tokens as two prompt
+    chunks (AttentionSlice.prefillLayerFromHidden: n-row GEMVs, kv_append,
+    the causal prefill, o_proj over the n rows), with the same checks."""
     out = tmp_path / "layer"
     print(f"node check_layer hidden=512 tokens=12 {mode}", flush=True)
     res = subprocess.run(["node", str(JS / "check_layer.js"), str(out), "512", "12", mode],
@@ -96,8 +98,16 @@ def test_node_host_full_layer_from_hidden_state(tmp_path, mode):
     attn = np.fromfile(out / "attn.f32", np.float32).reshape(T, H, D)
     hout = np.fromfile(out / "hout.f32", np.float32).reshape(T, hid)
     k_rows, v_rows, worst = [], [], 0.0
+    # The prefill kernel's QK^T runs on fp16 MFMA inputs: each query row is
+    # scaled by c = scale * log2(e) and rounded to fp16 when it is loaded
+    # (the decode kernel keeps an fp32 query). The oracle is given the same
+    # rounded rows, fp16(q c) / c, which leaves its softmax and products as
+    # they are.
+    c = np.float32(1.0 / np.sqrt(np.float32(D))) * np.float32(np.log2(np.e))
     for t in range(T):
         q = oracle.q4_gemv_f32(hnorm[t], *wq).reshape(H, D)
+        if mode == "prefill":
+            q = (oracle.f16_to_f32(oracle.f32_to_f16((q * c).astype(np.float32))) / c).astype(np.float32)
         for rows, wm in ((k_rows, wk), (v_rows, wv)):
             rows.append(oracle.f16_to_f32(oracle.f32_to_f16(oracle.q4_gemv_f32(hnorm[t], *wm)))
                         .reshape(Hkv, D))
