@@ -210,9 +210,11 @@ int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
  * kernel (VALU, whose work per key grows with the group size G), 1 the
  * matrix-core kernel (MFMA, the same work for every G), -1 restores the
  * default, which takes the matrix-core kernel for calls that run one
- * workgroup per KV head with G >= 5, or with G = 4 and batch >= 2 (where
- * it measured faster on MI355X), the dot-product kernel otherwise. Same records and merges; results agree
- * within fp32 rounding (both accumulate in fp32), not bit for bit. */
+ * workgroup per KV head with G >= 5, or with G = 4 and either batch >= 2 or
+ * splits of at least 512 keys whose workgroups all run at once (where it
+ * measured faster on MI355X), the dot-product kernel otherwise. Same records
+ * and merges; results agree within fp32 rounding (both accumulate in fp32),
+ * not bit for bit. */
 int nwd_set_decode_kernel(nwd_ctx* ctx, int32_t kernel);
 
 /* Measurement hook (no counterpart in the reference, whose split/merge

@@ -52,7 +52,7 @@ thread_local std::string g_create_err;
 // 36.1 / 32.2).
 constexpr int kTargetWorkgroups = 256;
 constexpr int kMinKeysPerSplit = 128;    // one workgroup iteration
-constexpr int kMaxKeysPerSplit = 2048;   // bounds the slowest workgroup
+constexpr int kMaxKeysPerSplit = 2048;   // bounds the slowest workgroup of a large batch
 constexpr int kMaxSplits = 256;
 
 int fail(nwd_ctx* ctx, int code, const char* fmt, ...) __attribute__((format(printf, 3, 4)));
@@ -89,6 +89,18 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
 // beyond, enough splits to fill the chip, even where that leaves splits with
 // no 128-key unit (an empty split costs less than the unused CUs: 8.0-8.9
 // against 8.5-9.7 us per step from 384 to 2048 keys). Measured on MI355X.
+//
+// Past that, the split count keeps every workgroup of the launch in one
+// wave of the chip (one per CU) while the sequences alone leave it at most
+// half full (batch x KV heads <= 128): a partial second wave costs the whole
+// per-split time again. B = 1, 32q/8kv, append + attend per step: 64K keys,
+// 44.1 us with 32 splits (one wave) against 62.6 with 33 (the earlier
+// 2048-key cap per split); 96K, 65.3 against 73.0 with 49; 128K, 83.5
+// against 95.4 with 48 and 85.2 with 64 (two full waves). B = 2 at 32K, 43.7
+// with 16 against 60.2 with 17; B = 4 at 32K, 82.4 with 8 against 95.0 with
+// 17. Larger batches fill the chip by themselves and keep the 2048-key
+// bound per split, which evens out ragged lengths (64 sequences of
+// 512-16384 keys run 9 splits each).
 int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   const int units = (max_len + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
   const int64_t heads = (int64_t)batch * n_heads;
@@ -100,6 +112,7 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
     return 1;
   }
   const int per_wave = batch * n_kv_heads;
+  if (2 * per_wave <= kTargetWorkgroups) return kTargetWorkgroups / per_wave;  // one wave
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
   const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work
   if (by_len > n) n = by_len;

@@ -797,6 +797,8 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 // one (non-temporal K: 25.7 against 25.3; default-policy V: 28.9). An fp32
 // query is split into fp16 high and low parts (two MFMAs per operand), so
 // the scores keep ~22 bits of the query.
+// Workgroups of one matrix-core launch that run at once: one per CU (256 CUs).
+constexpr int kMOneWave = 256;
 constexpr int kMWaves = 4;
 constexpr int kMThreads = kMWaves * 64;
 constexpr int kMWaveKeys = 16;                           // keys per wavefront per iteration
@@ -1271,8 +1273,16 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
     }
   }
   // One workgroup per KV head: the matrix-core kernel where it measured
-  // faster (see decode_mfma_kernel).
-  if (c.kernel < 0 && (s.group >= 5 || (s.group == 4 && c.batch >= 2))) return mfma();
+  // faster (see decode_mfma_kernel): G >= 5; G = 4 with a batch, or with
+  // long splits (at least 512 keys each) whose workgroups all fit the chip at
+  // once (B = 1, 32q/8kv, append + attend per step, 16K / 24K / 32K keys:
+  // 16.2 / 20.6 / 25.1 against 16.8 / 21.1 / 26.2 us on N(0,1) K/V, and
+  // 16.2 / 20.7 / 25.1 against 17.1 / 21.7 / 26.8 with 1% outliers, on two
+  // boxes; at 64K keys, 33 splits and 264 workgroups, 62.9 against 60.6).
+  const bool long_splits = (int64_t)c.span >= 512LL * c.nsplit &&
+                           (int64_t)c.batch * s.n_kv * c.nsplit <= kMOneWave;
+  if (c.kernel < 0 && (s.group >= 5 || (s.group == 4 && (c.batch >= 2 || long_splits))))
+    return mfma();
   switch (s.group) {
     case 1: return launch_qo<1>(s, a, c, stream);
     case 2: return launch_qo<2>(s, a, c, stream);

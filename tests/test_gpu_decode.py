@@ -586,3 +586,17 @@ def test_max_seq_last_position_fused_append(merge_separate):
     want = v_new[0, 0].astype(np.float32)
     for h in range(H):
         assert max_abs(o[0, h], want) < 1e-4, h
+
+
+def test_split_count_keeps_small_batches_in_one_wave():
+    """Past 2048 keys a launch of batch x 8 KV heads x splits workgroups
+    stays within one wave of 256 while the sequences alone fill at most half
+    of it (a partial second wave cost 37% at 64K keys); larger batches split
+    by length (at most 2048 keys per split)."""
+    cases = [  # (batch, max_len, expected splits)
+        (1, 65600, 32), (1, 131136, 32), (2, 32832, 16), (3, 32832, 10), (4, 32832, 8),
+        (16, 65600, 2), (20, 32832, 17), (64, 16448, 9), (1, 4160, 32),
+    ]
+    with nw.AttnContext(32, 8, 131136, max_batch=64) as ctx:
+        for B, L, n in cases:
+            assert ctx.decode_splits(B, L) == n, (B, L, ctx.decode_splits(B, L))

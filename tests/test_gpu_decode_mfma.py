@@ -201,16 +201,19 @@ def test_matrix_core_rising_and_negative_scores(offset):
 
 def test_default_kernel_choice():
     """Without nwd_set_decode_kernel a call that runs one workgroup per KV
-    head takes the matrix-core kernel for G >= 5, or G = 4 and batch >= 2,
-    and the dot-product kernel otherwise; a call that runs one workgroup per
-    query head takes the dot-product kernel. The default result equals the
-    chosen kernel's bits."""
+    head takes the matrix-core kernel for G >= 5, or G = 4 with batch >= 2 or
+    with splits of at least 512 keys whose workgroups fit 256 at once, and the
+    dot-product kernel otherwise; a call that runs one workgroup per query
+    head takes the dot-product kernel. The default result equals the chosen
+    kernel's bits."""
     cases = [  # (H, Hkv, B, L, splits, expected kernel)
         (64, 8, 1, 3000, 0, MFMA),
         (40, 8, 1, 20000, 32, MFMA),
         (40, 8, 1, 3000, 32, MFMA),
         (40, 8, 1, 1000, 0, VALU),   # 6 splits x 40 heads <= 256: one workgroup per query head
-        (32, 8, 1, 20000, 32, VALU),
+        (32, 8, 1, 20000, 32, MFMA),  # 625 keys per split, 256 workgroups
+        (32, 8, 1, 12000, 32, VALU),  # 375 keys per split
+        (32, 8, 1, 20000, 33, VALU),  # 264 workgroups
         (32, 8, 2, 3000, 0, MFMA),
         (32, 8, 9, 300, 0, MFMA),
         (16, 8, 1, 3000, 0, VALU),
