@@ -600,3 +600,34 @@ def test_split_count_keeps_small_batches_in_one_wave():
     with nw.AttnContext(32, 8, 131136, max_batch=64) as ctx:
         for B, L, n in cases:
             assert ctx.decode_splits(B, L) == n, (B, L, ctx.decode_splits(B, L))
+
+
+@pytest.mark.parametrize("B,P", [(1, 98304), (2, 40000)])
+def test_long_context_default_launch(B, P):
+    """Long contexts on the launch's own choices: one wave of splits (32 at
+    B = 1, 16 at B = 2) on the matrix-core split kernel (G = 4, splits of
+    512+ keys), fused append, against the oracle per sequence."""
+    H, Hkv = 32, 8
+    cap = P + 1
+    say(f"long context B={B} past={P} splits={256 // (8 * B)}")
+    g = rng(7 + B)
+    rows = [kv_rows(g, P + 1, Hkv, outlier_frac=0.01) for _ in range(B)]
+    q = normal_f16(g, (B, H, D))
+    with nw.AttnContext(H, Hkv, cap, max_batch=B) as ctx:
+        assert ctx.decode_splits(B, cap) == 256 // (8 * B)
+        kc = dev(to_cache([r[0][:P] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1][:P] for r in rows], Hkv, cap))
+        kn = dev(np.stack([r[0][P] for r in rows]))
+        vn = dev(np.stack([r[1][P] for r in rows]))
+        out = torch.empty((B, H, D), dtype=torch.float16, device="cuda")
+        ctx.append_decode(dev(q), kn, vn, kc, vc, pos_tensor([P] * B), out, B)
+        assert ctx.device_status() == nw.NWD_OK
+        got = out.float().cpu().numpy()
+        # the default launch is the matrix-core kernel's, bit for bit
+        ctx.set_decode_kernel(1)
+        forced = torch.empty_like(out)
+        ctx.decode(dev(q), kc, vc, pos_tensor([P] * B), forced, B)
+        assert torch.equal(forced, out)
+    for b in range(B):
+        want = oracle.sparse_attn_f32(f32(q[b]), f32(rows[b][0]), f32(rows[b][1]), threads=0)
+        assert max_abs(got[b], want) < TOL, b
