@@ -488,16 +488,27 @@ constexpr size_t kPrefillLds = (size_t)4 * kTileBytes;
 static_assert(kPrefillLds >= (size_t)4 * 64 * kRB * 34 * sizeof(float), "merge exchange fits");
 static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
 
-// Splits of each row tile's key range: enough workgroups to fill the chip
-// (256), at most 16, at least 3 key tiles per split (keys are bounded by
-// max_len), and as many as the workspace holds records for.
+// Splits of each row tile's key range. The launch runs in waves of 256
+// workgroups (one per CU), and a partial last wave costs a whole split's
+// time, so the split count fills one wave (256 / row tiles splits), or two
+// when one wave would hold a single split per row tile and the row tiles
+// are long (48+ key tiles); at most 16, at least 3 key tiles per split, and
+// as many as the workspace holds records for. Same box, us per call: 512
+// tokens onto 8192 at 40q/8kv (160 row tiles), 98.5 with 3 splits (two
+// waves) against 130.3 with 2 (the earlier rule, 320 workgroups) and 113.5
+// with 1; 256 onto 16384 (80 row tiles), 89.6 with 3 against 127.0 with 4;
+// 513 onto 1000 at 40q/8kv, 27.1 with 1 against 39.2 with 2; 128 onto 4096
+// at 40q/8kv, 25.3 against 36.1; 512 onto 2048 at 40q/8kv, 37.2 with 1
+// against 50.6 with 2 and 43.9 with 3; config 5 (128 row tiles) keeps 2,
+// 74.5 (81.3 with 4).
 static int prefill_splits(int64_t row_tiles, int64_t rows, int max_len, const Workspace& ws) {
-  int n = (int)((256 + row_tiles - 1) / row_tiles);
+  const int64_t key_tiles = (max_len + kPBN - 1) / kPBN;
+  int64_t n = 256 / row_tiles;
+  if (n <= 1 && row_tiles > 128 && key_tiles >= 48) n = 512 / row_tiles;
   if (n > 16) n = 16;
-  const int key_tiles = (max_len + kPBN - 1) / kPBN;
   if (n > key_tiles / 3) n = key_tiles / 3;
   while (n > 1 && rows * n > ws.records) --n;
-  return n < 1 ? 1 : n;
+  return n < 1 ? 1 : (int)n;
 }
 
 template <int G, bool kQ16, bool kO16>
