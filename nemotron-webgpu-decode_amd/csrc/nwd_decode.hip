@@ -766,10 +766,13 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 // 39.0 / 26.8). Batches at G = 4, N(0,1): B 2 x 8K 15.5-16.4 / 15.5-15.8,
 // 8 x 16K 98.6 / 89.6, 12 x 8K 65.0 / 61.0, 16 x 256 8.9 / 8.4, 16 x 8K
 // 90.3 / 83.4, 64 x 2K 86.8 / 81.3, 64 ragged 512..16K 422 / 409 (ties at
-// 4 x 8K, 8 x 4K, 16 x 2K). The launch takes it for one-workgroup-per-KV-
-// head calls with G >= 5, or G = 4 and batch >= 2 (at B = 1 and G = 4 the
-// dot-product kernel, which that shape was built for, stays faster);
-// nwd_set_decode_kernel forces either.
+// 4 x 8K, 8 x 4K, 16 x 2K). Timed as append + attend steps at B = 1 and
+// G = 4 on two more boxes it led from 16K keys up (16.2 / 20.6 / 25.1
+// against 16.8 / 21.1 / 26.2 us at 16K / 24K / 32K on N(0,1) K/V), while
+// the dot-product kernel stays ahead at 4K. The launch takes it for
+// one-workgroup-per-KV-head calls with G >= 5, or G = 4 with a batch or with
+// splits of 512+ keys in one wave (launch_decode); nwd_set_decode_kernel
+// forces either.
 // Four wavefronts, each owning one 16-key block of every 64-key workgroup
 // iteration (keys t0 + 64 it + 16 w ..), independent of each other inside
 // the loop:
