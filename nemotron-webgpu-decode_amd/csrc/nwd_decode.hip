@@ -152,137 +152,71 @@ __device__ inline f16x8 convert_src_run(const SrcRun& r, bool src16) {
 __device__ inline void wait_vm() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 
-// Splits the merge reads per pass: all loads of a pass are issued together,
-// one memory round trip (one pass for the usual 32 splits or fewer).
-constexpr int kMergeChunk = 32;
-// Threads that take part in a merge (the first 256 of the workgroup).
-constexpr int kMergeThreads = 256;
+// Splits one merge pass reads: all of a pass's loads are issued together, one
+// memory round trip (one pass for the usual 32 splits or fewer).
+constexpr int kMergePass = 32;
 
-// LDS floats merge_group uses: the per-wave partial outputs [4][G][32] x 4,
-// one (m, l) pair per thread and the pass's head max / sum [G] each.
-template <int G> constexpr int merge_lds_floats() { return G * (4 * 32 * 4 + 2) + 2 * kMergeThreads; }
-
-// Merges the nsplit records of the G heads of one (b, hkv) and writes the
-// normalised outputs. Called by every thread of the workgroup (256 or
-// more); threads t < 256 do the work. Thread t owns the 4-dim run
-// d4 = t % 32 of every head, for the splits s = j, j + 8, ... of a pass
-// (j = t / 32). Per pass:
-//   1. every (m, l) pair and every o run of the pass is requested at once;
-//   2. the (m, l) pairs go to LDS, and two heads per wavefront reduce their
-//      32 entries to the pass max Mp and sum Lp = sum l * 2^(m - Mp);
-//   3. each thread rescales its running sum to max(M, Mp) and adds its runs
-//      weighted by 2^(m - M). The running max M of a head is the same in
-//      every thread, so the 8 thread groups' sums add without rescaling
-//      (xor-32 lane exchange, then LDS across the 4 wavefronts).
-template <int G, bool kO16, int kPolicy>
-__device__ inline void merge_group(const float* __restrict__ part_o,
-                                   const float2* __restrict__ part_ml, void* __restrict__ out,
-                                   int64_t hrow0, int nsplit, float* lds, int64_t out_rows,
-                                   int64_t records, int* status) {
-  static_assert(G * kMergeChunk <= kMergeThreads, "one (m, l) pair per thread per pass");
-  constexpr int kPer = kMergeChunk / 8;  // splits per thread per head per pass
-  const int t = threadIdx.x;
-  const bool act = t < kMergeThreads;
-  const int lane = t & 63, wave = t >> 6;
-  const int d4 = t & 31, j = (t >> 5) & 7;
-  f32x4* lds_acc = reinterpret_cast<f32x4*>(lds);               // [4][G][32]
-  float2* lds_ml = reinterpret_cast<float2*>(lds + G * 512);     // [kMergeThreads]: [G][kMergeChunk], unused
-  float* lds_mp = lds + G * 512 + 2 * kMergeThreads;            // [G]
-  float* lds_lp = lds_mp + G;                                   // [G]
-  const int64_t rec0 = hrow0 * nsplit;  // record (g, s) is rec0 + g * nsplit + s
-  // uniform over the workgroup, so returning here skips every barrier below
-  if (!in_bounds(rec0, (int64_t)G * nsplit, records, status)) return;
+// Merges the nsplit records (m, l, o[D]) of one output row (b * n_heads +
+// head) and writes the normalised row; run by one whole wavefront. Lane l
+// owns dims 2l and 2l+1; per pass of up to 32 splits, lane s holds split
+// s's (m, l), every o record of the pass is requested at once (32 coalesced
+// 8-byte loads per lane), the pass maximum Mp is a wavefront reduction, the
+// running maximum M is raised to max(M, Mp) with the running sums rescaled,
+// and the splits' weights 2^(m_s - M) reach every lane by readlane, so
+// each lane adds its dims split by split in order with no LDS and no
+// barrier. Both merge forms call it, so they give the same bits. (Against
+// the earlier 256-thread merge, which combined eight thread groups' partial
+// sums through LDS, per call: 32K keys 24.5 against 24.9-25.0 us, 4K 8.6
+// against 9.0, 40q/8kv at 32K 24.7 against 25.1.)
+template <bool kO16, int kPolicy>
+__device__ inline void merge_row_wave(const float* __restrict__ part_o,
+                                      const float2* __restrict__ part_ml, void* __restrict__ out,
+                                      int64_t row, int nsplit, int64_t out_rows, int64_t records,
+                                      int* status) {
+  const int lane = threadIdx.x & 63;
+  const int64_t rec0 = row * nsplit;
+  // uniform over the wavefront
+  if (!in_bounds(rec0, nsplit, records, status)) return;
   const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(part_ml + rec0), 0,
-                                                      G * nsplit * 8, kBufferWord3);
+                                                      nsplit * 8, kBufferWord3);
   const auto r_o = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_o + rec0 * kHeadDim), 0,
-                                                     G * nsplit * kHeadDim * 4, kBufferWord3);
-
-  float M[G], Lr[G];
-  f32x4 acc[G];
+                                                     nsplit * kHeadDim * 4, kBufferWord3);
+  float M = kNegBig, L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergePass) {
+    const int ns = min(kMergePass, nsplit - s0);
+    // loads (indexes clamped in range; splits past the pass get no weight)
+    const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+        r_ml, (s0 + min(lane, ns - 1)) * 8, 0, kPolicy));
+    float2 ov[kMergePass];
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    M[g] = kNegBig;
-    Lr[g] = 0.f;
-    acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int s0 = 0; s0 < nsplit; s0 += kMergeChunk) {
-    const int ns = min(kMergeChunk, nsplit - s0);
-    // 1. Loads (indexes clamped in range; entries past the pass get no weight).
-    const int mg = (t & (kMergeThreads - 1)) / kMergeChunk, ms = t % kMergeChunk;
-    const bool mvalid = mg < G && ms < ns;
-    const float2 mlv = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
-        r_ml, (min(mg, G - 1) * nsplit + s0 + min(ms, ns - 1)) * 8, 0, kPolicy));
-    __builtin_amdgcn_sched_barrier(0);  // the (m, l) load is waited for first: issue it first
-    f32x4 ov[G][kPer];
+    for (int s = 0; s < kMergePass; ++s)
+      ov[s] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+          r_o, ((s0 + min(s, ns - 1)) * kHeadDim + 2 * lane) * 4, 0, kPolicy));
+    const float m = lane < ns ? ml.x : kNegBig;
+    const float mn = fmaxf(M, max_xor32(max32(m)));
+    const float w = lane < ns ? fast_exp2(m - mn) : 0.f;
+    const float alpha = fast_exp2(M - mn);
+    L = fmaf(L, alpha, sum64(ml.y * w));
+    a0 *= alpha;
+    a1 *= alpha;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int k = 0; k < kPer; ++k) {
-        const int s = s0 + min(j + 8 * k, ns - 1);
-        ov[g][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-            r_o, ((g * nsplit + s) * kHeadDim + d4 * 4) * 4, 0, kPolicy));
-      }
-    // 2. Pass max and sum per head.
-    if (act) lds_ml[t] = mvalid ? mlv : make_float2(kNegBig, 0.f);
-    __syncthreads();
-    {
-      const int g = 2 * wave + (lane >> 5);
-      if (act && g < G) {
-        const float2 e = lds_ml[g * kMergeChunk + (lane & 31)];
-        const float mp = max32(e.x);
-        const float lp = sum32(e.y * fast_exp2(e.x - mp));
-        if ((lane & 31) == 0) {
-          lds_mp[g] = mp;
-          lds_lp[g] = lp;
-        }
-      }
+    for (int s = 0; s < kMergePass; ++s) {
+      const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+      a0 = fmaf(ov[s].x, ws, a0);
+      a1 = fmaf(ov[s].y, ws, a1);
     }
-    __syncthreads();
-    // 3. Weighted sums of this thread's runs.
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float mp = lds_mp[g];
-      const float mn = fmaxf(M[g], mp);
-      const float a = fast_exp2(M[g] - mn);
-      Lr[g] = Lr[g] * a + lds_lp[g] * fast_exp2(mp - mn);
-      acc[g] *= a;
-#pragma unroll
-      for (int k = 0; k < kPer; ++k) {
-        const int sr = j + 8 * k;
-        const float w = sr < ns ? fast_exp2(lds_ml[g * kMergeChunk + sr].x - mn) : 0.f;
-        acc[g] += ov[g][k] * w;
-      }
-      M[g] = mn;
-    }
-    if (s0 + kMergeChunk < nsplit) __syncthreads();  // lds_ml is rewritten by the next pass
+    M = mn;
   }
-  // Sum the 8 thread groups: j and j ^ 1 share a wavefront (lane ^ 32).
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[g][i] = sum_xor32(acc[g][i]);
-    if (act && lane < 32) lds_acc[(wave * G + g) * 32 + d4] = acc[g];
-  }
-  __syncthreads();
-  if (t < G * 32) {
-    const int g = t / 32;
-    f32x4 o = lds_acc[g * 32 + d4];
-#pragma unroll
-    for (int w = 1; w < 4; ++w) o += lds_acc[(w * G + g) * 32 + d4];
-    float lt = Lr[0];
-#pragma unroll
-    for (int gg = 1; gg < G; ++gg) lt = gg == g ? Lr[gg] : lt;
-    const float inv = 1.f / lt;
-    const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
-    if (!in_bounds(at, 4, out_rows * kHeadDim, status)) return;
-    if constexpr (kO16) {
-      f16x4 v;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
-      *reinterpret_cast<f16x4*>(static_cast<f16*>(out) + at) = v;
-    } else {
-      *reinterpret_cast<f32x4*>(static_cast<float*>(out) + at) = o * inv;
-    }
+  const float inv = 1.f / L;
+  const int64_t at = row * kHeadDim + 2 * lane;
+  if (!in_bounds(at, 2, out_rows * kHeadDim, status)) return;
+  if constexpr (kO16) {
+    f16x2 v;
+    v[0] = (f16)(a0 * inv);
+    v[1] = (f16)(a1 * inv);
+    *reinterpret_cast<f16x2*>(static_cast<f16*>(out) + at) = v;
+  } else {
+    *reinterpret_cast<float2*>(static_cast<float*>(out) + at) = make_float2(a0 * inv, a1 * inv);
   }
 }
 
@@ -391,11 +325,10 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
 // dirty L2 line behind and no stale L2 line can serve them: the release
 // reduces to waiting for this thread's record stores (vmcnt(0)) before the
 // barrier that precedes the ticket, and the acquire to the sc1 loads in
-// merge_group, which are issued only after the ticket has returned (they
-// depend on it through lds_last). `lds` holds merge_lds_floats<G>() floats.
+// merge_row_wave, which are issued only after the ticket has returned (they
+// depend on it through lds_last). Wavefront w merges heads w, w + waves, ...
 template <int G, bool kO16>
-__device__ inline void merge_on_last_arrival(const DecodeArgs& a, float* lds, int* counter,
-                                             int64_t hrow0) {
+__device__ inline void merge_on_last_arrival(const DecodeArgs& a, int* counter, int64_t hrow0) {
   __shared__ int lds_last;
   wait_vm();
   __syncthreads();
@@ -405,8 +338,9 @@ __device__ inline void merge_on_last_arrival(const DecodeArgs& a, float* lds, in
   }
   __syncthreads();
   if (!lds_last) return;
-  merge_group<G, kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0, a.nsplit, lds,
-                                   (int64_t)a.batch * a.n_heads, a.records, a.status);
+  for (int g = (int)threadIdx.x >> 6; g < G; g += (int)blockDim.x >> 6)
+    merge_row_wave<kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0 + g, a.nsplit,
+                                     (int64_t)a.batch * a.n_heads, a.records, a.status);
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -419,7 +353,6 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
   constexpr int kTiles = C::kTiles;
-  static_assert(kThreads >= kMergeThreads, "merge_group needs 256 threads");
   static_assert(G * 32 <= kThreads, "one 4-dim run of each head per thread");
   // Row states written to LDS per wavefront (see the end of the kernel). The
   // rule depends on the shape's group size, not on the heads this
@@ -428,9 +361,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kRowSteps = G * kQsub * kWaves * kRows * (kHeadDim + 2) * 4 <= 48 * 1024 ? 0 : 1;
   constexpr int kRowStates = kRows >> kRowSteps;
   constexpr int kStates = kWaves * kRowStates;
-  constexpr int kMergeFloats = merge_lds_floats<G>();
-  constexpr int kStateFloats = kStates * G * (kHeadDim + 2);
-  constexpr int kLdsFloats = kMergeFloats > kStateFloats ? kMergeFloats : kStateFloats;
+  constexpr int kLdsFloats = kStates * G * (kHeadDim + 2);
   static_assert(kLdsFloats * 4 <= 64 * 1024, "static LDS of one workgroup");
 
   __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
@@ -747,7 +678,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     }
   }
   if (nsplit == 1 || !a.fused_merge) return;
-  merge_on_last_arrival<G, kO16>(a, lds, a.counters + b * (a.n_kv * kQsub) + hgrp,
+  merge_on_last_arrival<G, kO16>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
                                  (int64_t)b * a.n_heads + h0);
 }
 
@@ -834,8 +765,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   static_assert(G <= 16, "the heads of a group are the MFMA's 16 columns");
   static_assert(kMBlockLoads == 8, "wait counts below assume 8 loads per block");
   static_assert(G * 32 <= kMThreads, "one 4-dim run of each head per thread");
-  static_assert((size_t)kMWaves * G * (kHeadDim + 2) * 4 <= kMLdsBytes &&
-                    (size_t)merge_lds_floats<G>() * 4 <= kMLdsBytes,
+  static_assert((size_t)kMWaves * G * (kHeadDim + 2) * 4 <= kMLdsBytes,
                 "the end of the kernel reuses the ring");
   extern __shared__ __attribute__((aligned(16))) f16 dsmem[];
   char* lds = reinterpret_cast<char*>(dsmem);
@@ -1114,22 +1044,20 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
       *reinterpret_cast<f16x8*>(a.v_cache + at + 8 * lr) = nv;
   }
   if (nsplit == 1 || !a.fused_merge) return;
-  merge_on_last_arrival<G, kO16>(a, reinterpret_cast<float*>(lds), a.counters + b * a.n_kv + hkv,
+  merge_on_last_arrival<G, kO16>(a, a.counters + b * a.n_kv + hkv,
                                  hrow0);
 }
 
-// Separate merge: one 256-thread workgroup per (query head, sequence), the
-// head's records being those of a group of one. Four times the workgroups
-// of a per-KV-head merge, each with a quarter of the loads: 9.7 against
-// 10.8 us per 4K decode. (One thread per output dim looping over the splits,
-// with no LDS or barrier, measured slower: 9.9 against 9.35 us at 4K.)
+// Separate merge: one wavefront per (query head, sequence). (Earlier forms:
+// one 256-thread workgroup per KV head, 10.8 us per 4K decode, then per
+// query head, 9.7; one thread per output dim looping over the splits, its
+// loads one split at a time, 9.9 against 9.35.)
 template <bool kO16>
-__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(
+__global__ __launch_bounds__(64) void decode_merge_kernel(
     const float* __restrict__ part_o, const float2* __restrict__ part_ml,
     void* __restrict__ out, int n_heads, int nsplit, int64_t records, int* __restrict__ status) {
-  __shared__ __attribute__((aligned(16))) float lds[merge_lds_floats<1>()];
   const int h = blockIdx.x, b = blockIdx.y;
-  merge_group<1, kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit, lds,
+  merge_row_wave<kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit,
                           (int64_t)gridDim.y * n_heads, records, status);
 }
 
@@ -1163,7 +1091,7 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, v
     e = hipGetLastError();
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
-  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kMergeThreads, 0, stream>>>(
+  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
       a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
   return hipGetLastError();
 }
@@ -1208,7 +1136,7 @@ static hipError_t launch_mfma_t(const DecodeArgs& a, int batch, hipStream_t stre
     e = hipGetLastError();
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
-  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), kMergeThreads, 0, stream>>>(
+  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
       a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
   return hipGetLastError();
 }
