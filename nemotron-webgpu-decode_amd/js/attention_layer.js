@@ -205,7 +205,7 @@ class AttentionSlice {
   // (kvAppend), then query j attends keys 0 .. seq+j (prefill).
   prefillLayer(i, q, k, v) {
     if (!this.kCache.has(i)) throw new Error(`layer ${i} is not an attention layer`);
-    const n = this.chunkLen;
+    const n = this.openChunk('prefillLayer');
     expectF32(q, n * this.heads * this.headDim, 'prefillLayer q');
     expectF32(k, n * this.kvHeads * this.headDim, 'prefillLayer k');
     expectF32(v, n * this.kvHeads * this.headDim, 'prefillLayer v');
@@ -226,7 +226,7 @@ class AttentionSlice {
   prefillLayerFromHidden(i, hNorm, h) {
     const w = this.weights.get(i);
     if (!w) throw new Error(`layer ${i} has no weights (setLayerWeights)`);
-    const n = this.chunkLen;
+    const n = this.openChunk('prefillLayerFromHidden');
     addon.q4Gemv(this.ctx, hNorm, w.q, this.chunk.q, n, Q4_PLAIN);
     addon.q4Gemv(this.ctx, hNorm, w.k, this.chunk.k, n, Q4_PLAIN);
     addon.q4Gemv(this.ctx, hNorm, w.v, this.chunk.v, n, Q4_PLAIN);
@@ -238,15 +238,24 @@ class AttentionSlice {
   }
 
   // The last prefill's attention output, [n][heads][headDim] f32.
-  readPrefillO(out = new Float32Array(this.chunkLen * this.heads * this.headDim)) {
-    expectF32(out, this.chunkLen * this.heads * this.headDim, 'readPrefillO');
+  readPrefillO(out) {
+    const n = this.openChunk('readPrefillO') * this.heads * this.headDim;
+    if (out === undefined) out = new Float32Array(n);
+    expectF32(out, n, 'readPrefillO');
     this.checkStatus();
     addon.download(out, this.chunk.o);
     return out;
   }
 
   endPrefill() {
-    this.seq += this.chunkLen;
+    this.seq += this.openChunk('endPrefill');
+    this.chunkLen = 0;
+  }
+
+  // The token count of the chunk between beginPrefill and endPrefill.
+  openChunk(who) {
+    if (!this.chunkLen) throw new Error(`${who}: no prompt chunk open (beginPrefill)`);
+    return this.chunkLen;
   }
 
   // runtime.js:467: seq++ without waiting for the device.

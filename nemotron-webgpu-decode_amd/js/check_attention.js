@@ -90,6 +90,13 @@ function main() {
   // the maxSeq guard (runtime.js:448) must throw, not write past the cache
   let guard = 'no-throw';
   let prefillGuard = 'no-throw';
+  // a chunk call outside beginPrefill .. endPrefill must throw, not append
+  let chunkGuard = 'no-throw';
+  try {
+    slice.prefillLayer(slice.layers[0], new Float32Array(0), new Float32Array(0), new Float32Array(0));
+  } catch (e) {
+    chunkGuard = String(e.message);
+  }
   if (tokens === maxSeq) {
     try {
       slice.beginStep();
@@ -108,7 +115,7 @@ function main() {
   fs.writeFileSync(path.join(outDir, 'v.f32'), cat(vAll));
   fs.writeFileSync(path.join(outDir, 'o.f32'), cat(oAll));
   fs.writeFileSync(path.join(outDir, 'manifest.json'), JSON.stringify({
-    heads, kvHeads, headDim, tokens, maxSeq, layers: slice.layers, guard, prefillGuard, chunks,
+    heads, kvHeads, headDim, tokens, maxSeq, layers: slice.layers, guard, prefillGuard, chunkGuard, chunks,
   }));
   slice.destroy();
   console.log(`check_attention: ${tokens} tokens x ${slice.layers.length} layers written to ${outDir}`);

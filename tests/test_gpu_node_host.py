@@ -60,6 +60,7 @@ def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, ch
             want = oracle.sparse_attn_f32(q[t, li], kh[:t + 1, li], vh[:t + 1, li], threads=0)
             worst = max(worst, max_abs(o[t, li], want))
     assert worst < 2e-3, worst
+    assert "no prompt chunk open" in man["chunkGuard"]
     if tokens == max_seq:  # engine/runtime.js:448: the next step must throw
         assert "exceeds maxSeq" in man["guard"]
         assert "exceeds maxSeq" in man["prefillGuard"]
