@@ -87,8 +87,8 @@ int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
 // 7.0 against 8.2 at 1600, a tie at 2112, 12.2 against 10.1 at 4160).
 // Otherwise one split up to 256 keys (6.5 against 7.9 us at 153 keys), and
 // beyond, enough splits to fill the chip, even where that leaves splits with
-// no 128-key unit (an empty split costs less than the unused CUs: 8.0-8.9
-// against 8.5-9.7 us per step from 384 to 2048 keys). Measured on MI355X.
+// few keys (idle splits cost less than the unused CUs: 8.0-8.9 against
+// 8.5-9.7 us per step from 384 to 2048 keys). Measured on MI355X.
 //
 // Past that, the split count keeps every workgroup of the launch in one
 // wave of the chip (one per CU) while the sequences alone leave it at most

@@ -74,8 +74,13 @@ struct DecodeCfg {
   static_assert(kL == 8 || kL == 16, "rows of 8 or 16 lanes");
 };
 
-// Units the key range is split in (128 keys).
-constexpr int kUnitKeys = 128;
+// Units the key range is split in (16 keys, one matrix-core wavefront
+// block, two dot-product wavefront tiles). Each split's time is that of its
+// keys (a workgroup streams at the rate its own loads in flight allow), so
+// the slowest split sets the launch's time: small units keep the splits
+// within 16 keys of each other (4160 keys over 32 splits: 128-144 each,
+// where 128-key units gave one split 256).
+constexpr int kUnitKeys = 16;
 // How far (log2 units) a score may exceed the online softmax's reference
 // point before the reference moves (and the accumulators are rescaled).
 constexpr float kRescaleSlack = 8.f;
@@ -391,8 +396,8 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int row = lane / kLanes, col = lane % kLanes;
 
   const int nsplit = a.nsplit;
-  // This split's key range from the host bound: whole 128-key units spread
-  // evenly over the splits. Independent of the device position.
+  // This split's key range from the host bound: whole units spread evenly
+  // over the splits. Independent of the device position.
   const int units = (a.span + kUnitKeys - 1) / kUnitKeys;
   const int u0 = (int)((int64_t)split * units / nsplit);
   const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
@@ -741,7 +746,7 @@ constexpr int kMSlotBytes = kMWaveKeys * kHeadDim * 2;  // one V block: 4 KB
 constexpr int kMDepth = 2;                               // blocks in flight per wavefront
 constexpr size_t kMLdsBytes = (size_t)kMWaves * kMDepth * kMSlotBytes;
 constexpr int kMBlockLoads = 4 + kMSlotBytes / 1024;  // K fragments + V copies
-static_assert(kUnitKeys % kMBlockKeys == 0, "a split's range is whole workgroup iterations");
+static_assert(kUnitKeys % kMWaveKeys == 0, "a split's range is whole wavefront blocks");
 static_assert(kMBlockLoads * (kMDepth - 1) <= 63, "vmcnt counts at most 63 loads");
 static_assert(kMLdsBytes <= 160 * 1024, "LDS of one gfx950 CU");
 
