@@ -690,8 +690,9 @@ def library_prefill(torch, wl, steps: int = 16):
 
 def run_stream_read(torch, nw, launches: int):
     """The read ceiling of the decode-32k access pattern (csrc/bench/
-    nwd_stream_read.hip): the same 4 layer caches, 32 splits per KV head,
-    graph-replayed back to back."""
+    nwd_stream_read.hip): the same 4 layer caches, one workgroup per CU (32
+    splits per KV head; the decode itself runs 24 at this length, where the
+    plain read measured slower), graph-replayed back to back."""
     lib = ctypes.CDLL(str(BENCH_LIB))
     lib.nwd_bench_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_int, ctypes.c_int, ctypes.c_int,
@@ -699,7 +700,7 @@ def run_stream_read(torch, nw, launches: int):
     past, window, layers, dist, _ = WORKLOADS["decode-32k"]
     log(f"[bench] stream-read: {launches} launches")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
-    keys, splits = past + 1, wl.ctx.decode_splits(1, wl.cap)
+    keys, splits = past + 1, 256 // HKV
     out = torch.empty(HKV * splits * 256, dtype=torch.float32, device="cuda")
 
     class Reader:

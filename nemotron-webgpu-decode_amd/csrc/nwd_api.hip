@@ -112,7 +112,20 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
     return 1;
   }
   const int per_wave = batch * n_kv_heads;
-  if (2 * per_wave <= kTargetWorkgroups) return kTargetWorkgroups / per_wave;  // one wave
+  if (2 * per_wave <= kTargetWorkgroups) {  // one wave
+    // A single sequence with splits of 1024-3072 keys runs faster on three
+    // quarters of the wave: fewer merge records and less finishing-time skew,
+    // with ~192 workgroups already at the read ceiling. Decode-only call,
+    // 32q/8kv, 24 against 32 splits: 32K 24.05-24.13 against 24.31-24.55 us
+    // (40q: 24.26-24.28 against 24.79-24.87), 64K 41.41-42.01 against
+    // 42.04-42.87. Outside that range, or with more sequences, it loses:
+    // 4K 9.09 against 8.72-8.75, 8K 11.75 against 10.92-11.03, 96K 65.2-65.4
+    // against 64.0, 128K 84.3-84.4 against 83.4-83.5; B = 2 with 12 against
+    // 16 splits, 16K 26.26 against 25.70, 32K 45.43 against 45.54 (a tie).
+    const int n = kTargetWorkgroups / per_wave, n34 = 3 * n / 4;
+    if (batch == 1 && n34 >= 1 && max_len >= 1024 * n34 && max_len <= 3072 * n34) return n34;
+    return n;
+  }
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip
   const int by_len = (max_len + kMaxKeysPerSplit - 1) / kMaxKeysPerSplit;  // bound per-split work
   if (by_len > n) n = by_len;

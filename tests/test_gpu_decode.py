@@ -591,10 +591,13 @@ def test_max_seq_last_position_fused_append(merge_separate):
 def test_split_count_keeps_small_batches_in_one_wave():
     """Past 2048 keys a launch of batch x 8 KV heads x splits workgroups
     stays within one wave of 256 while the sequences alone fill at most half
-    of it (a partial second wave cost 37% at 64K keys); larger batches split
-    by length (at most 2048 keys per split)."""
+    of it (a partial second wave cost 37% at 64K keys), three quarters of it
+    for one sequence while the splits then hold 1024-3072 keys; larger
+    batches split by length (at most 2048 keys per split)."""
     cases = [  # (batch, max_len, expected splits)
-        (1, 65600, 32), (1, 131136, 32), (2, 32832, 16), (3, 32832, 10), (4, 32832, 8),
+        (1, 65600, 24), (1, 32832, 24), (1, 73728, 24), (1, 73729, 32), (1, 98305, 32),
+        (1, 131136, 32), (1, 24576, 24), (1, 24575, 32), (2, 32832, 16), (3, 32832, 10),
+        (4, 32832, 8),
         (16, 65600, 2), (20, 32832, 17), (64, 16448, 9), (1, 4160, 32),
     ]
     with nw.AttnContext(32, 8, 131136, max_batch=64) as ctx:
@@ -602,19 +605,20 @@ def test_split_count_keeps_small_batches_in_one_wave():
             assert ctx.decode_splits(B, L) == n, (B, L, ctx.decode_splits(B, L))
 
 
-@pytest.mark.parametrize("B,P", [(1, 98304), (2, 40000)])
-def test_long_context_default_launch(B, P):
+@pytest.mark.parametrize("B,P,splits", [(1, 98304, 32), (1, 40000, 24), (2, 40000, 16)])
+def test_long_context_default_launch(B, P, splits):
     """Long contexts on the launch's own choices: one wave of splits (32 at
-    B = 1, 16 at B = 2) on the matrix-core split kernel (G = 4, splits of
-    512+ keys), fused append, against the oracle per sequence."""
+    B = 1 past 72K keys, 16 at B = 2; three quarters of it, 24, for one
+    sequence of 40K) on the matrix-core split kernel (G = 4, splits of 512+
+    keys), fused append, against the oracle per sequence."""
     H, Hkv = 32, 8
     cap = P + 1
-    say(f"long context B={B} past={P} splits={256 // (8 * B)}")
+    say(f"long context B={B} past={P} splits={splits}")
     g = rng(7 + B)
     rows = [kv_rows(g, P + 1, Hkv, outlier_frac=0.01) for _ in range(B)]
     q = normal_f16(g, (B, H, D))
     with nw.AttnContext(H, Hkv, cap, max_batch=B) as ctx:
-        assert ctx.decode_splits(B, cap) == 256 // (8 * B)
+        assert ctx.decode_splits(B, cap) == splits
         kc = dev(to_cache([r[0][:P] for r in rows], Hkv, cap))
         vc = dev(to_cache([r[1][:P] for r in rows], Hkv, cap))
         kn = dev(np.stack([r[0][P] for r in rows]))
