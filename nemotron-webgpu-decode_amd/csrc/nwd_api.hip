@@ -121,9 +121,14 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
     // 42.04-42.87. Outside that range, or with more sequences, it loses:
     // 4K 9.09 against 8.72-8.75, 8K 11.75 against 10.92-11.03, 96K 65.2-65.4
     // against 64.0, 128K 84.3-84.4 against 83.4-83.5; B = 2 with 12 against
-    // 16 splits, 16K 26.26 against 25.70, 32K 45.43 against 45.54 (a tie).
+    // 16 splits, 16K 26.26 against 25.70, 32K 45.43 against 45.54 (a tie);
+    // and with groups under 4 query heads (the dot-product kernel's shapes;
+    // 32K: 8q 23.75-23.97 against 23.32-23.48, 16q 25.23-25.28 against
+    // 24.05-24.08), while 64q gains as 32q does (24.48-24.59 against 24.98-25.0).
     const int n = kTargetWorkgroups / per_wave, n34 = 3 * n / 4;
-    if (batch == 1 && n34 >= 1 && max_len >= 1024 * n34 && max_len <= 3072 * n34) return n34;
+    if (batch == 1 && n_heads >= 4 * n_kv_heads && n34 >= 1 && max_len >= 1024 * n34 &&
+        max_len <= 3072 * n34)
+      return n34;
     return n;
   }
   int n = (kTargetWorkgroups + per_wave - 1) / per_wave;              // fill the chip

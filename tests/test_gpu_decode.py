@@ -592,7 +592,8 @@ def test_split_count_keeps_small_batches_in_one_wave():
     """Past 2048 keys a launch of batch x 8 KV heads x splits workgroups
     stays within one wave of 256 while the sequences alone fill at most half
     of it (a partial second wave cost 37% at 64K keys), three quarters of it
-    for one sequence while the splits then hold 1024-3072 keys; larger
+    for one sequence with groups of 4+ query heads while the splits then hold
+    1024-3072 keys; larger
     batches split by length (at most 2048 keys per split)."""
     cases = [  # (batch, max_len, expected splits)
         (1, 65600, 24), (1, 32832, 24), (1, 73728, 24), (1, 73729, 32), (1, 98305, 32),
@@ -603,6 +604,10 @@ def test_split_count_keeps_small_batches_in_one_wave():
     with nw.AttnContext(32, 8, 131136, max_batch=64) as ctx:
         for B, L, n in cases:
             assert ctx.decode_splits(B, L) == n, (B, L, ctx.decode_splits(B, L))
+    # three quarters only for groups of 4+ query heads
+    for heads, n in ((8, 32), (16, 32), (40, 24), (64, 24)):
+        with nw.AttnContext(heads, 8, 32832) as ctx:
+            assert ctx.decode_splits(1, 32832) == n, (heads, ctx.decode_splits(1, 32832))
 
 
 @pytest.mark.parametrize("B,P,splits", [(1, 98304, 32), (1, 40000, 24), (2, 40000, 16)])
