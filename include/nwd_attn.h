@@ -147,8 +147,7 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new,
 
 /* Allocation-free form of nwd_append_decode, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc. It has no counterpart in the reference,
- * whose engine allocates everything once up front (engine/runtime.js:109-211).
+ * harnesses that forbid hipMalloc. It has no counterpart in the reference.
  * It takes the descriptor instead of a context and needs no nwd_create: the
  * split-K records live in a static 16 MiB device array of the library (one
  * per GPU, held until the process ends), so a call whose records would not
@@ -172,9 +171,11 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * pos0[b] .. pos0[b] + n_new - 1 (nwd_kv_append with n_tokens = n_new).
  * Query i of sequence b attends keys 0 .. pos0[b] + i. q and out are
  * [batch][n_new][n_heads][head_dim]. QK^T and PV run on fp16 MFMA with fp32
- * accumulation: an fp32 q is scaled by scale * log2(e) and rounded to fp16
- * as it is loaded, so it carries fp16 precision (nwd_decode_attn keeps an
- * fp32 q in fp32). max_len bounds pos0[b] + n_new (0 means max_seq). */
+ * accumulation: an fp16 q enters exact and its scores are scaled in fp32;
+ * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
+ * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
+ * makes nwd_device_status report NWD_ERR_DEVICE. max_len bounds
+ * pos0[b] + n_new (0 means max_seq). */
 int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
                      const void* v_cache, const int32_t* pos0, void* out,
                      int32_t batch, int32_t n_new, int32_t max_len,
@@ -216,6 +217,17 @@ int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
  * and merges; results agree within fp32 rounding (both accumulate in fp32),
  * not bit for bit. */
 int nwd_set_decode_kernel(nwd_ctx* ctx, int32_t kernel);
+
+/* Chooses how later decode calls lay the keys over the split workgroups
+ * (a tuning knob with no counterpart in the reference, whose one workgroup
+ * per query head reads every key, kernels/sparse_attn.wgsl:45-58): 0
+ * contiguous, each split owns one range of keys; 1 strided, split s owns
+ * the 64-key blocks (32 for the dot-product kernel) s, s + n_splits, ..., so
+ * the splits of a KV head read neighbouring blocks at any moment; -1
+ * restores the default: strided for batches of two or more sequences,
+ * contiguous for one (measured on MI355X). Results agree within fp32
+ * rounding (the keys a split sums differ), not bit for bit. */
+int nwd_set_decode_layout(nwd_ctx* ctx, int32_t layout);
 
 /* Measurement hook (no counterpart in the reference, whose split/merge
  * kernels are timed only as a whole step, bench/engine.js:70-137): while set,

@@ -76,3 +76,85 @@ extern "C" int nwd_bench_stream_read(const void* k, const void* v, int slabs, in
       static_cast<const char*>(k), static_cast<const char*>(v), cap, keys, splits, out);
   return (int)hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// A plain read of the same bytes with none of the decode's structure: the
+// 2 x slabs key ranges (K and V of each slab, keys [0, keys)) are cut into
+// chunks of kU x threads x 16 bytes, and a grid of `grid` workgroups walks
+// the chunks with a grid stride, each thread issuing its kU 16-byte loads of
+// a chunk at once (one 1 KB run per wavefront instruction) and summing them.
+// Occupancy, not software pipelining, keeps loads in flight: the launch
+// shape (threads per workgroup, workgroups, loads per thread) is free, so a
+// sweep of it gives a read ceiling that does not share the decode's grid.
+namespace {
+
+template <int kU, int kPolicy>
+__global__ void plain_read_kernel(const char* __restrict__ k, const char* __restrict__ v,
+                                  int64_t slab_stride, int64_t range_bytes, int64_t chunks_per_range,
+                                  int64_t chunks, float* __restrict__ out) {
+  const int tid = threadIdx.x, nt = blockDim.x;
+  const int64_t chunk_bytes = (int64_t)kU * nt * 16;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+    const int64_t range = c / chunks_per_range;  // 2 * slab + (0: K, 1: V)
+    const int64_t in_range = (c - range * chunks_per_range) * chunk_bytes;
+    const char* base = ((range & 1) ? v : k) + (range >> 1) * slab_stride + in_range;
+    const int64_t left = range_bytes - in_range;  // > 0
+    const auto r = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0,
+                                                     (int)(left < chunk_bytes ? left : chunk_bytes),
+                                                     kBufferWord3);
+    f32x4 t[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+      t[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           r, (uint32_t)((u * nt + tid) * 16), 0, kPolicy));
+#pragma unroll
+    for (int u = 0; u < kU; ++u) acc += t[u];
+  }
+  out[(int64_t)blockIdx.x * nt + tid] = acc[0] + acc[1] + acc[2] + acc[3];
+}
+
+template <int kU>
+hipError_t launch_plain(int nt_policy, dim3 grid, int threads, hipStream_t s, const char* k,
+                        const char* v, int64_t slab_stride, int64_t range_bytes, int64_t cpr,
+                        int64_t chunks, float* out) {
+  if (nt_policy)
+    plain_read_kernel<kU, kNonTemporal><<<grid, threads, 0, s>>>(k, v, slab_stride, range_bytes,
+                                                                 cpr, chunks, out);
+  else
+    plain_read_kernel<kU, 0><<<grid, threads, 0, s>>>(k, v, slab_stride, range_bytes, cpr, chunks,
+                                                      out);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Reads keys [0, keys) of `slabs` K and V slabs of `cap` fp16 rows each with
+// `grid` workgroups of `threads` threads, `unroll` 16-byte loads per thread
+// and chunk (1, 2, 4, 8 or 16), the non-temporal policy if `nt`. out needs
+// grid * threads floats. Returns a hipError_t code.
+extern "C" int nwd_bench_plain_read(const void* k, const void* v, int slabs, int cap, int keys,
+                                    int threads, int unroll, int grid, int nt, float* out,
+                                    void* stream) {
+  if (!k || !v || !out || slabs < 1 || cap < 1 || keys < 1 || keys > cap || grid < 1 ||
+      threads < 64 || threads > 1024 || threads % 64 != 0 ||
+      (int64_t)cap * kRowBytes > 0x7FFFFFFF)
+    return (int)hipErrorInvalidValue;
+  const int64_t chunk_bytes = (int64_t)unroll * threads * 16;
+  const int64_t range_bytes = (int64_t)keys * kRowBytes;
+  const int64_t cpr = (range_bytes + chunk_bytes - 1) / chunk_bytes;
+  const int64_t chunks = cpr * 2 * slabs;
+  const int64_t slab_stride = (int64_t)cap * kRowBytes;
+  const char* kp = static_cast<const char*>(k);
+  const char* vp = static_cast<const char*>(v);
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 g((unsigned)grid);
+  switch (unroll) {
+    case 1: return (int)launch_plain<1>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    case 2: return (int)launch_plain<2>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    case 4: return (int)launch_plain<4>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    case 8: return (int)launch_plain<8>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    case 16: return (int)launch_plain<16>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    default: return (int)hipErrorInvalidValue;
+  }
+}

@@ -35,6 +35,7 @@ struct nwd_ctx {
   int forced_splits;
   int separate_merge;  // 1 separate kernel, 0 in the split kernel, -1 default (separate)
   int decode_kernel;   // -1 the launch's choice, 0 dot-product, 1 matrix-core
+  int decode_layout;   // -1 the launch's choice, 0 contiguous key ranges, 1 strided blocks
   void* ev_start;      // hipEvent_t pair recorded around decode split kernels, or NULL
   void* ev_stop;
   int* status_host;    // pinned copy target of the device status word
@@ -187,6 +188,20 @@ nwd::Shape shape_of(const nwd_desc* d) {
   return sh;
 }
 
+// Key layout over the splits (DecodeCall::layout). A batch of sequences
+// takes the strided layout: the splits of a (sequence, KV head) then read
+// neighbouring key blocks at any moment instead of batch x KV heads x splits
+// separate streams (64 sequences of 512-16384 keys, append + attend, same
+// box: 387.6-387.8 against 405.9-418.2 us per step). One sequence keeps
+// contiguous ranges: there the strided layout tied at 32K keys (24.21-24.50
+// against 24.33-24.43 us per append + attend step), lost at 64K keys with
+// 24 splits (48.1-48.4 against 45.5-45.7) and at 1K keys (6.67 against
+// 6.49), and gained only in decode-only calls at 4K-16K.
+int default_layout(int batch, int max_len, int nsplit) {
+  (void)max_len;
+  return batch >= 2 && nsplit > 1 ? 1 : 0;
+}
+
 int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
   int cap = nwd::max_decode_splits(ctx->shape, ctx->ws, batch);
   if (cap > kMaxSplits) cap = kMaxSplits;
@@ -242,6 +257,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->forced_splits = 0;
   ctx->separate_merge = -1;
   ctx->decode_kernel = -1;
+  ctx->decode_layout = -1;
   ctx->ev_start = nullptr;
   ctx->ev_stop = nullptr;
   ctx->shape = shape_of(d);
@@ -383,6 +399,7 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   // store, ticket and record round trips).
   c.fused_merge = ctx->separate_merge == 0 ? 1 : 0;
   c.kernel = ctx->decode_kernel;
+  c.layout = ctx->decode_layout >= 0 ? ctx->decode_layout : default_layout(batch, len, c.nsplit);
   c.ev_start = ctx->ev_start;
   c.ev_stop = ctx->ev_stop;
   hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
@@ -451,6 +468,7 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   c.span = len;
   c.fused_merge = 0;
   c.kernel = -1;
+  c.layout = default_layout(batch, len, n);
   c.ev_start = nullptr;
   c.ev_stop = nullptr;
   hipError_t e = nwd::launch_decode(shape_of(desc), c, ws, (hipStream_t)stream);
@@ -469,6 +487,14 @@ int nwd_set_decode_kernel(nwd_ctx* ctx, int32_t kernel) {
   if (kernel < -1 || kernel > 1)
     return fail(ctx, NWD_ERR_INVALID, "nwd_set_decode_kernel: kernel %d is not -1, 0 or 1", kernel);
   ctx->decode_kernel = kernel;
+  return NWD_OK;
+}
+
+int nwd_set_decode_layout(nwd_ctx* ctx, int32_t layout) {
+  if (!ctx) return fail(nullptr, NWD_ERR_INVALID, "nwd_set_decode_layout: ctx is NULL");
+  if (layout < -1 || layout > 1)
+    return fail(ctx, NWD_ERR_INVALID, "nwd_set_decode_layout: layout %d is not -1, 0 or 1", layout);
+  ctx->decode_layout = layout;
   return NWD_OK;
 }
 
@@ -520,6 +546,12 @@ int nwd_device_status(nwd_ctx* ctx, void* stream) {
     return fail(ctx, NWD_ERR_DEVICE,
                 "a kernel of this bounds-checked build computed an address outside its "
                 "buffer; the access was skipped (status bits 0x%x)",
+                host);
+  if (host & nwd::kStatusQueryRange)
+    return fail(ctx, NWD_ERR_DEVICE,
+                "a query element left the fp16 range of the matrix-core kernels (prefill: "
+                "|q| * scale * log2(e) > 65504; decode with fp32 queries: |q| > 65504): "
+                "those outputs are not finite (status bits 0x%x)",
                 host);
   return fail(ctx, NWD_ERR_DEVICE,
               "a kernel saw a position outside [0, max_seq=%d): the cache was not written "

@@ -35,6 +35,10 @@ constexpr int kStreamPolicy = 2;
 // Status bits written by kernels into the context's device status word.
 constexpr int kStatusBadPos = 1;
 constexpr int kStatusOutOfBounds = 2;  // set only by bounds-checked builds
+// A query element of a matrix-core kernel left the fp16 range of its operand
+// (|q| scale log2(e) > 65504 in the prefill, |q| > 65504 for an fp32 query of
+// the matrix-core decode): those scores are not finite.
+constexpr int kStatusQueryRange = 4;
 
 // Bounds-checked builds (compiled with -DNWD_CHECK) check every kernel
 // store into an output, a cache or the split-K workspace, and the merges'

@@ -240,6 +240,7 @@ struct DecodeArgs {
   int* counters;      // [batch][n_kv] arrival tickets, zero between calls
   int batch, n_heads, n_kv, cap, nsplit;
   int span;           // host bound on L: keys [0, span) are partitioned
+  int strided;        // key layout over the splits: 0 contiguous ranges, 1 interleaved blocks
   int fused_merge;    // merge in the split kernel's last workgroup
   float qk_scale_log2;
   int* status;
@@ -292,8 +293,8 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
       // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
       const int64_t rec0 = hrow0 * nsplit + split;
       // the descriptors below stop stores past this head group's records;
-      // the head's nsplit records must lie inside the workspace
-      const bool rec_ok = in_bounds(rec0 + g * nsplit, nsplit, a.records, a.status);
+      // head g's nsplit records must lie inside the workspace
+      const bool rec_ok = in_bounds((hrow0 + g) * nsplit, nsplit, a.records, a.status);
       const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
                                                          G * nsplit * kHeadDim * 4, kBufferWord3);
       const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
@@ -396,12 +397,17 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int row = lane / kLanes, col = lane % kLanes;
 
   const int nsplit = a.nsplit;
-  // This split's key range from the host bound: whole units spread evenly
-  // over the splits. Independent of the device position.
+  // This split's keys (independent of the device position): iteration it
+  // covers keys t0 + it * it_keys .. + kBlockKeys. Contiguous layout: the
+  // split owns one range of whole units of the host bound, spread evenly over
+  // the splits. Strided layout: it owns the kBlockKeys blocks split,
+  // split + nsplit, ..., so at any moment the splits of a KV head read
+  // neighbouring blocks of its slab.
   const int units = (a.span + kUnitKeys - 1) / kUnitKeys;
   const int u0 = (int)((int64_t)split * units / nsplit);
   const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
-  const int t0 = u0 * kUnitKeys;
+  const int t0 = a.strided ? split * kBlockKeys : u0 * kUnitKeys;
+  const int it_keys = a.strided ? nsplit * kBlockKeys : kBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
 
   const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
@@ -423,7 +429,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   // zeros past the descriptor's end) and masked.
   auto load_tile = [&](Tile& tl, const __amdgpu_buffer_rsrc_t rk,
                        const __amdgpu_buffer_rsrc_t rv, int it) {
-    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
+    const int base = t0 + it * it_keys + wave * kWaveKeys + row;
 #pragma unroll
     for (int j = 0; j < kKpr; ++j) {
       const uint32_t off = (uint32_t)(base + j * kRows) * (kHeadDim * 2) + col * 16;
@@ -459,7 +465,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   // weight would be NaN). Later tiles are bounded by the split's last key.
   Tile tr[kTiles];
   {
-    const int own_end = split == nsplit - 1 ? a.cap : t1h;
+    const int own_end = a.strided || split == nsplit - 1 ? a.cap : t1h;
     const auto ek = slab_rsrc(a.k_cache, own_end), ev = slab_rsrc(a.v_cache, own_end);
 #pragma unroll
     for (int t = 0; t < kTiles - 1; ++t) load_tile(tr[t], ek, ev, t);
@@ -493,22 +499,23 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
   if (!pos_ok && tid == 0 && split == 0 && blockIdx.y == 0) atomicOr(a.status, kStatusBadPos);
   const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
-  // Keys this split attends: [t0, t1); the last split also takes any keys
-  // past the host bound.
-  const int t1 = split == nsplit - 1 ? L : min(t1h, L);
-  const int n_it = t1 > t0 ? (t1 - t0 + kBlockKeys - 1) / kBlockKeys : 0;
+  // Keys this split attends lie in [t0, t1); the last contiguous split also
+  // takes any keys past the host bound, and strided splits run to L.
+  const int t1 = a.strided || split == nsplit - 1 ? L : min(t1h, L);
+  const int n_it = t1 > t0 ? (t1 - t0 + it_keys - 1) / it_keys : 0;
   const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
 
   // Fused append: the split holding the new position substitutes the new
   // rows for the cache rows it loads, and writes them to the caches at the
   // end of the kernel.
   const int pnew = L - 1;
-  const bool owns_new = has_new && pos_ok && t0 <= pnew && pnew < t1;
+  const bool owns_new =
+      has_new && pos_ok && t0 <= pnew && pnew < t1 && (pnew - t0) % it_keys < kBlockKeys;
   // Only the iteration whose tile holds the new key substitutes it: a
   // substitution in every tile lengthened the owning workgroup's chain, the
   // critical path of the whole launch (32K keys: 28.8 against 25.8 us per
   // step with and without the append).
-  const int it_new = owns_new ? (pnew - t0) / kBlockKeys : -1;
+  const int it_new = owns_new ? (pnew - t0) / it_keys : -1;
   f16x8 nk[kRuns], nv[kRuns];
   if (owns_new) {
 #pragma unroll
@@ -546,7 +553,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
 
   auto compute_tile = [&](Tile& tl, int it) {
-    const int base = t0 + it * kBlockKeys + wave * kWaveKeys + row;
+    const int base = t0 + it * it_keys + wave * kWaveKeys + row;
     if (it == it_new) {
 #pragma unroll
       for (int j = 0; j < kKpr; ++j) {
@@ -783,10 +790,12 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const int lr = lane & 15, lq = lane >> 4;
   const int nsplit = a.nsplit;
 
+  // Key partition as in decode_split_kernel, in blocks of kMBlockKeys.
   const int units = (a.span + kUnitKeys - 1) / kUnitKeys;
   const int u0 = (int)((int64_t)split * units / nsplit);
   const int u1 = (int)((int64_t)(split + 1) * units / nsplit);
-  const int t0 = u0 * kUnitKeys;
+  const int t0 = a.strided ? split * kMBlockKeys : u0 * kUnitKeys;
+  const int it_keys = a.strided ? nsplit * kMBlockKeys : kMBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
   const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
   auto slab_rsrc = [&](f16* cache, int end_key) {
@@ -799,7 +808,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     f16x8 k[4];  // [32-dim block]
   };
   auto load_k = [&](KFrag& f, const __amdgpu_buffer_rsrc_t rk, int it) {
-    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+    const int key0 = t0 + it * it_keys + wave * kMWaveKeys;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const uint32_t off = (uint32_t)(key0 + lr) * (kHeadDim * 2) + db * 64 + lq * 16;
@@ -810,7 +819,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   // lane l fills physical chunk l % 16 of row 4i + l / 16, so it loads the
   // logical chunk the swizzle puts there.
   auto load_v = [&](const __amdgpu_buffer_rsrc_t rv, int it, int slot) {
-    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+    const int key0 = t0 + it * it_keys + wave * kMWaveKeys;
     char* dst = ring + slot * kMSlotBytes;
 #pragma unroll
     for (int i = 0; i < kMSlotBytes / 1024; ++i) {
@@ -840,7 +849,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   // so the wait counts below see whole blocks.
   KFrag kf[kMDepth];
   {
-    const int own_end = split == nsplit - 1 ? a.cap : t1h;
+    const int own_end = a.strided || split == nsplit - 1 ? a.cap : t1h;
     const auto ek = slab_rsrc(a.k_cache, own_end), ev = slab_rsrc(a.v_cache, own_end);
 #pragma unroll
     for (int t = 0; t < kMDepth - 1; ++t) {
@@ -853,6 +862,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   // Q^T: column lr is head h0 + lr; the rows past the group are zero.
   const int h0 = hkv * G;
   f16x8 qh[4], ql[kQ16 ? 1 : 4];
+  bool q_range = false;
   {
     const bool qv = lr < G;
     const int64_t qrow = ((int64_t)b * a.n_heads + h0 + (qv ? lr : 0)) * kHeadDim + 8 * lq;
@@ -869,26 +879,29 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
           const float x = qv ? (e < 4 ? x0[e] : x1[e - 4]) : 0.f;
           qh[db][e] = (f16)x;
           ql[db][e] = (f16)(x - (float)qh[db][e]);
+          q_range |= fabsf(x) > 65504.f;
         }
       }
     }
   }
+  if (!kQ16 && q_range && split == 0) atomicOr(a.status, kStatusQueryRange);
 
   const int pos_raw = a.pos[b];
   const bool pos_ok = pos_raw >= 0 && pos_raw < a.cap;
   if (!pos_ok && tid == 0 && split == 0 && hkv == 0) atomicOr(a.status, kStatusBadPos);
   const int L = pos_ok ? pos_raw + 1 : (pos_raw < 0 ? 1 : a.cap);
-  const int t1 = split == nsplit - 1 ? L : min(t1h, L);
-  const int n_it = t1 > t0 ? (t1 - t0 + kMBlockKeys - 1) / kMBlockKeys : 0;
+  const int t1 = a.strided || split == nsplit - 1 ? L : min(t1h, L);
+  const int n_it = t1 > t0 ? (t1 - t0 + it_keys - 1) / it_keys : 0;
   const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
 
   // Fused append: the wavefront whose block holds the new position
   // substitutes the new rows (K in its fragments, V in its LDS slot) and
   // writes them to the caches at the end.
   const int pnew = L - 1;
-  const bool owns_new = has_new && pos_ok && t0 <= pnew && pnew < t1;
-  const int it_new = owns_new ? (pnew - t0) / kMBlockKeys : -1;
-  const int w_new = owns_new ? (pnew - t0) % kMBlockKeys / kMWaveKeys : -1;
+  const bool owns_new =
+      has_new && pos_ok && t0 <= pnew && pnew < t1 && (pnew - t0) % it_keys < kMBlockKeys;
+  const int it_new = owns_new ? (pnew - t0) / it_keys : -1;
+  const int w_new = owns_new ? (pnew - t0) % it_keys / kMWaveKeys : -1;
   const int r_new = (pnew - t0) % kMWaveKeys;
   f16x8 nk[4], nv;
   if (owns_new) {
@@ -905,7 +918,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
 
   auto compute = [&](KFrag& f, int it, int slot) {
     wait_vm_keep<kMBlockLoads * (kMDepth - 1)>();  // block it's K fragments and V rows are in
-    const int key0 = t0 + it * kMBlockKeys + wave * kMWaveKeys;
+    const int key0 = t0 + it * it_keys + wave * kMWaveKeys;
     if (key0 >= t1) return;  // nothing of this block is attended
     char* vs = ring + slot * kMSlotBytes;
     const bool partial = key0 + kMWaveKeys > t1;
@@ -1179,6 +1192,7 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.span = c.span;
   a.counters = ws.counters;
   a.fused_merge = c.fused_merge;
+  a.strided = c.layout == 1;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
   // When one workgroup per (sequence, query head, split) fits the chip, each

@@ -42,6 +42,7 @@ struct DecodeCall {
   int span;  // host bound on the keys attended (max_len), partitions the splits
   int fused_merge;  // merge in the split kernel (else a separate merge kernel)
   int kernel;       // -1 the launch's choice, 0 dot-product (VALU), 1 matrix-core
+  int layout;       // keys over the splits: 0 contiguous ranges, 1 interleaved blocks
   void* ev_start;   // optional hipEvent_t pair recorded around the split kernel
   void* ev_stop;
 };

@@ -30,10 +30,13 @@
 //     in registers as the B operand), so each lane holds 4 consecutive keys
 //     of ONE row — its own softmax row;
 //   - causal mask only on tiles that cross a row's limit; online softmax in
-//     log2 units: the query rows are pre-scaled by scale * log2(e) and the
-//     QK^T MFMAs accumulate onto -m, so each weight is one v_exp of an MFMA
-//     output (the softmax's VALU work hides only partly behind the MFMAs,
-//     so VALU instructions per score are what the loop minimises); the row
+//     log2 units: fp16 query rows enter the MFMAs exact and each score is
+//     scaled by scale * log2(e) and moved by -m in one FMA; fp32 rows are
+//     pre-scaled and split into fp16 high and low parts (two QK^T MFMAs,
+//     the low parts read from LDS) that accumulate onto -m, so each weight
+//     is one v_exp of an MFMA output (the softmax's VALU work hides only
+//     partly behind the MFMAs, so VALU instructions per score are what the
+//     loop minimises); the row
 //     maximum is taken only for a row's first keys and when a weight
 //     overflows fp16 (seen as an infinite row sum), and the reference point
 //     m then moves lazily (only when the row maximum exceeds it by more
@@ -80,24 +83,28 @@ static_assert(4 * kStageInsts == 4 * kKB, "a tile's K and V copies fit one per t
 // chunks, and a transpose read (4 rows x 2 chunks per 16 lanes) 8.
 __device__ inline int kswz(int r) { return r & 15; }
 __device__ inline int vswz(int r) { return (r & 7) << 1; }
-// Eight query elements times s, rounded to fp16.
+// Eight query elements as MFMA operands. fp16 queries are taken as they are
+// (exact; the scale is applied to the fp32 scores). fp32 queries are scaled
+// by s: `hi` is the product rounded to fp16 and `lo` the rounding error
+// (x - hi, rounded to fp16), so hi + lo carries ~22 bits of the scaled
+// query and the MFMAs leave the scores in log2 units. `range` is set when a
+// scaled fp32 element leaves the fp16 range (its hi is then +-inf).
 template <bool kQ16>
-__device__ inline f16x8 load_q8_scaled(const void* q, int64_t elem, float s) {
-  f16x8 r;
+__device__ inline void load_q8(const void* q, int64_t elem, float s, f16x8& hi, f16x8& lo,
+                               bool& range) {
   if constexpr (kQ16) {
-    const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(q) + elem);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = (f16)((float)h[e] * s);
+    hi = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(q) + elem);
   } else {
     const f32x4* p = reinterpret_cast<const f32x4*>(static_cast<const float*>(q) + elem);
     const f32x4 a = p[0], b = p[1];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      r[e] = (f16)(a[e] * s);
-      r[4 + e] = (f16)(b[e] * s);
+    for (int e = 0; e < 8; ++e) {
+      const float x = (e < 4 ? a[e] : b[e - 4]) * s;
+      hi[e] = (f16)x;
+      lo[e] = (f16)(x - (float)hi[e]);
+      range |= fabsf(x) > 65504.f;
     }
   }
-  return r;
 }
 
 template <bool kO16>
@@ -126,10 +133,17 @@ struct PrefillArgs {
   int* status;
 };
 
+// LDS of a workgroup: K0 K1 V0 V1 tiles, 32 KB each; with fp32 queries also
+// the low halves of the workgroup's 128 query rows (32 KB, rows swizzled as
+// K rows), which do not fit the registers beside the high halves.
+constexpr int kQloOffset = 4 * kTileBytes;
+template <bool kQ16>
+constexpr size_t prefill_lds_bytes() { return (size_t)(kQ16 ? 4 : 5) * kTileBytes; }
+
 template <int G, bool kQ16, bool kO16>
 __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
-  char* lds = reinterpret_cast<char*>(smem);  // K0 K1 V0 V1, 32 KB each
+  char* lds = reinterpret_cast<char*>(smem);
 
   const int id = blockIdx.x;
   const int hkv = id % a.n_kv;
@@ -156,12 +170,22 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   const int t1 = (int)((int64_t)(split + 1) * ntiles_all / a.nsplit);
   const int kend_s = min(kend, t1 * kPBN);  // keys this split may load
 
-  // Query rows in registers, pre-scaled by scale * log2(e): the scores come
-  // out of the MFMAs in log2 units.
+  // Query rows in registers. fp32 rows are pre-scaled by scale * log2(e)
+  // (the scores come out of the MFMAs in log2 units), and the key-half-0
+  // wavefront of each row group writes their low halves to LDS (published by
+  // the barrier before the first tile); fp16 rows stay exact and their
+  // scores are scaled after the MFMAs.
   const float c = a.qk_scale_log2;
   const int r0 = mt * kPBM + rh * 32;
   int qi[kRB], gq[kRB], lim[kRB];
   f16x8 qf[kRB][4];
+  char* const qlo = lds + kQloOffset;
+  // LDS address of the low half of row block rb's fragment db (row rh*32 +
+  // rb*16 + lr of the workgroup, logical chunk 4 db + lq, K's swizzle)
+  auto qlo_at = [&](int rb, int db) {
+    return qlo + (rh * 32 + rb * 16 + lr) * kRowBytes + (((4 * db + lq) ^ lr) << 4);
+  };
+  bool q_range = false;
 #pragma unroll
   for (int rb = 0; rb < kRB; ++rb) {
     const int R = r0 + rb * 16 + lr;
@@ -172,14 +196,19 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     const int64_t qrow = (((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
+      f16x8 lo{};
       if (ok) {
-        qf[rb][db] = load_q8_scaled<kQ16>(a.q, qrow + db * 32 + 8 * lq, c);
+        load_q8<kQ16>(a.q, qrow + db * 32 + 8 * lq, c, qf[rb][db], lo, q_range);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) qf[rb][db][e] = (f16)0.f;
       }
+      if constexpr (!kQ16) {
+        if (kh == 0) *reinterpret_cast<f16x8*>(qlo_at(rb, db)) = lo;
+      }
     }
   }
+  if (q_range) atomicOr(a.status, kStatusQueryRange);
   const bool wave_has_pad = r0 + 31 >= total_rows;
   const int wave_min_lim = P0 + r0 / G;
 
@@ -227,11 +256,9 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     for (int j = 0; j < 8; ++j) o[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  if (t1 > t0) {
-    load_tile(t0, 0);
-    wait_tile();
-    __syncthreads();
-  }
+  if (t1 > t0) load_tile(t0, 0);
+  wait_tile();
+  __syncthreads();  // the first tile and the query low halves are in LDS
   for (int kt = t0; kt < t1; ++kt) {
     const int buf = (kt - t0) & 1;
     const char* ks = lds + buf * kTileBytes + kh * 64 * kRowBytes;
@@ -239,14 +266,16 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     const int k0 = kt * kPBN + kh * 64;
 
     // st[kb][rb][e] = score(key k0 + kb*16 + 4*lq + e, row rb*16 + lr) - mu[rb]
-    // in log2 units: the MFMAs accumulate onto -mu, the row's reference
-    // point (0 before the row has seen a key).
+    // in log2 units, mu being the row's reference point (0 before the row
+    // has seen a key): fp32 rows' MFMAs accumulate onto -mu, fp16 rows'
+    // scores q.k are scaled by c and moved by -mu in one FMA each.
     float mu[kRB];
     f32x4 c0[kRB], st[kKB][kRB];
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) {
       mu[rb] = m[rb] > kNegBig ? m[rb] : 0.f;
-      c0[rb] = f32x4{-mu[rb], -mu[rb], -mu[rb], -mu[rb]};
+      const float init = kQ16 ? 0.f : -mu[rb];
+      c0[rb] = f32x4{init, init, init, init};
     }
     // All 16 K fragments of this wavefront's 64 keys are read first (64
     // VGPRs), then the 32 MFMAs run on them: no MFMA waits on a read issued
@@ -268,12 +297,28 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every read ahead of the MFMAs
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db) {
+      f16x8 ql[kRB];
+      if constexpr (!kQ16) {
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) ql[rb] = *reinterpret_cast<const f16x8*>(qlo_at(rb, db));
+      }
+#pragma unroll
+      for (int kb = 0; kb < kKB; ++kb)
+#pragma unroll
+        for (int rb = 0; rb < kRB; ++rb) {
+          st[kb][rb] = mfma16x16x32(kf[db][kb], qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
+          if constexpr (!kQ16) st[kb][rb] = mfma16x16x32(kf[db][kb], ql[rb], st[kb][rb]);
+        }
+    }
+    if constexpr (kQ16) {
 #pragma unroll
       for (int kb = 0; kb < kKB; ++kb)
 #pragma unroll
         for (int rb = 0; rb < kRB; ++rb)
-          st[kb][rb] = mfma16x16x32(kf[db][kb], qf[rb][db], db == 0 ? c0[rb] : st[kb][rb]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) st[kb][rb][e] = fmaf(st[kb][rb][e], c, -mu[rb]);
+    }
     // The Vᵀ operands of this tile's PV product do not depend on the
     // softmax: all 16 (32 transpose reads) are requested now, and arrive
     // while the softmax runs.
@@ -484,9 +529,9 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
   store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / L));
 }
 
-constexpr size_t kPrefillLds = (size_t)4 * kTileBytes;
-static_assert(kPrefillLds >= (size_t)4 * 64 * kRB * 34 * sizeof(float), "merge exchange fits");
-static_assert(kPrefillLds <= 160 * 1024, "LDS of one gfx950 CU");
+static_assert(prefill_lds_bytes<true>() >= (size_t)4 * 64 * kRB * 34 * sizeof(float),
+              "merge exchange fits");
+static_assert(prefill_lds_bytes<false>() <= 160 * 1024, "LDS of one gfx950 CU");
 
 // Splits of each row tile's key range. The launch runs in waves of 256
 // workgroups (one per CU), and a partial last wave costs a whole split's
@@ -516,6 +561,7 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
                                    const int32_t* pos0, void* out, int batch, int n_new,
                                    int max_len, const Workspace& ws, hipStream_t stream) {
   auto kern = prefill_kernel<G, kQ16, kO16>;
+  constexpr size_t kPrefillLds = prefill_lds_bytes<kQ16>();
   // The dynamic LDS size exceeds the 64 KB default: raise the kernel's limit
   // once per device (the attribute is per device).
   static std::atomic<uint64_t> attr_set{0};

@@ -119,6 +119,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_set_decode_splits": (ctypes.c_int, [vp, i32]),
         "nwd_set_decode_merge": (ctypes.c_int, [vp, i32]),
         "nwd_set_decode_kernel": (ctypes.c_int, [vp, i32]),
+        "nwd_set_decode_layout": (ctypes.c_int, [vp, i32]),
         "nwd_set_kernel_events": (ctypes.c_int, [vp, vp, vp]),
         "nwd_q4_gemv": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight), vp, i32, i32, vp]),
         "nwd_qkv_append": (ctypes.c_int, [vp, vp, ctypes.POINTER(NwdQ4Weight),
@@ -251,6 +252,11 @@ class AttnContext:
         """0: the dot-product (VALU) split kernel; 1: the matrix-core (MFMA)
         one; None: the default choice (by group size and keys per split)."""
         self._check(self.lib.nwd_set_decode_kernel(self.handle, -1 if kernel is None else int(kernel)))
+
+    def set_decode_layout(self, layout):
+        """0: each split owns one contiguous key range; 1: split s owns the
+        key blocks s, s + n_splits, ...; None: the default choice."""
+        self._check(self.lib.nwd_set_decode_layout(self.handle, -1 if layout is None else int(layout)))
 
     def set_kernel_events(self, start, stop):
         """hipEvent_t handles (ints) recorded around every later decode call's

@@ -92,6 +92,38 @@ def test_decode_checked_build_matches(H, Hkv, lens, o_dtype, splits, separate):
               [out, kc, vc])
 
 
+@pytest.mark.parametrize("kernel,layout", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_decode_checked_build_full_workspace(kernel, layout):
+    """A context whose split-K workspace is filled exactly by one call: 8
+    query heads, max_seq 64, batch 1 give 2048 records, and 256 forced splits
+    use all of them (most splits hold no key). Every record store is in
+    bounds, so the checked build flags nothing and gives the product's bits,
+    with either merge form, both split kernels and both key layouts."""
+    say("check build full workspace", kernel, layout)
+    H, Hkv, cap = 8, 8, 64
+    prod, chk = _pair(H, Hkv, cap, o_dtype="f32")
+    with prod, chk:
+        assert prod.decode_splits(1, cap) >= 1
+        q = randn_f16((1, H, D), 21)
+        kc = randn_f16((1, Hkv, cap, D), 22)
+        vc = randn_f16((1, Hkv, cap, D), 23)
+        kn = randn_f16((1, Hkv, D), 24)
+        vn = randn_f16((1, Hkv, D), 25)
+        pos = pos_tensor([cap - 1])
+        out = torch.zeros((1, H, D), dtype=torch.float32, device="cuda")
+        for c in (prod, chk):
+            c.set_decode_splits(256)
+            c.set_decode_kernel(kernel)
+            c.set_decode_layout(layout)
+        assert prod.decode_splits(1, cap) == 256
+        for separate in (True, False):
+            for c in (prod, chk):
+                c.set_decode_merge(separate)
+            _same(lambda c, o: c.decode(q, kc, vc, pos, o, 1), prod, chk, [out])
+            _same(lambda c, o, k, v: c.append_decode(q, kn, vn, k, v, pos, o, 1), prod, chk,
+                  [out, kc, vc])
+
+
 def test_kv_append_checked_build_matches():
     say("check build kv_append")
     B, n_tok, cap, Hkv = 3, 5, 64, 8

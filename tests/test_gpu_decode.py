@@ -211,19 +211,22 @@ def test_config3_past32768_outliers_split_k(kernel):
         assert max_abs(outs[n], outs[0]) < 1e-3
 
 
+@pytest.mark.parametrize("layout", [0, 1])
 @pytest.mark.parametrize("kernel", [0, 1])
-def test_config4_ragged_batch64(kernel):
+def test_config4_ragged_batch64(kernel, layout):
     """64 sequences, past lengths U{512..16384}, one query each: one new token
     per sequence appended at pos = past and attended, both as nwd_kv_append +
     nwd_decode_attn and as the fused nwd_append_decode the benchmark times.
     The fused path writes the same cache bits and gives the same output bits;
     every sequence matches the oracle. On the dot-product split kernel and
-    on the matrix-core one (the default for this batch)."""
+    on the matrix-core one (the default for this batch), with each split
+    owning one key range (layout 0) and with the splits' key blocks
+    interleaved (layout 1, the default for batches)."""
     H, Hkv, B = 32, 8, 64
     g = rng(4)
     past = g.integers(512, 16385, size=B)
     cap = int(past.max()) + 1
-    say(f"config4 ragged B={B} cap={cap} sum_L={int(past.sum() + B)} kernel={kernel}")
+    say(f"config4 ragged B={B} cap={cap} sum_L={int(past.sum() + B)} kernel={kernel} layout={layout}")
     kc = randn_f16((B, Hkv, cap, D), 40)
     vc = randn_f16((B, Hkv, cap, D), 41)
     q = randn_f16((B, H, D), 42)
@@ -232,6 +235,7 @@ def test_config4_ragged_batch64(kernel):
     pos = pos_tensor(past.tolist())
     with nw.AttnContext(H, Hkv, cap, max_batch=B) as ctx:
         ctx.set_decode_kernel(kernel)
+        ctx.set_decode_layout(layout)
         kc2, vc2 = kc.clone(), vc.clone()
         ctx.kv_append(kn[:, None], vn[:, None], kc, vc, pos, B, 1)
         out = _decode(ctx, q, kc, vc, pos, B, max_len=cap)
@@ -250,6 +254,59 @@ def test_config4_ragged_batch64(kernel):
                                       threads=0)
         worst = max(worst, max_abs(out[b], want))
     assert worst < TOL, worst
+
+
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_strided_layout(kernel):
+    """Split s owning the key blocks s, s + n, ... (nwd_set_decode_layout 1)
+    against the oracle and against the contiguous layout: lengths around the
+    block sizes (32 keys for the dot-product kernel, 64 for the matrix-core
+    one), split counts that leave some splits without keys, the fused append
+    (same cache bits as nwd_kv_append, same output bits as the two calls),
+    both merge forms (same bits), a length bound below the true length,
+    32K keys with outliers, and NaN rows past L that must not leak."""
+    H, Hkv = 32, 8
+    for L, splits in ((1, 3), (33, 2), (64, 2), (65, 2), (129, 5), (1000, 0), (1000, 7),
+                      (5000, 0), (5000, 256), (32769, 0), (32769, 24)):
+        say(f"strided layout kernel={kernel} L={L} splits={splits}")
+        g = rng(700 + L + splits)
+        k, v = kv_rows(g, L, Hkv, outlier_frac=0.01 if L > 30000 else 0.0)
+        q = normal_f16(g, (1, H, D))
+        want = oracle.sparse_attn_f32(f32(q[0]), f32(k), f32(v), threads=0)
+        cap = L + 40
+        stale_k = to_cache([k[:L - 1]], Hkv, cap)
+        stale_v = to_cache([v[:L - 1]], Hkv, cap)
+        stale_k[:, :, L:, :] = np.uint16(0x7E00).view(np.float16)
+        stale_v[:, :, L:, :] = np.uint16(0x7E00).view(np.float16)
+        pos = pos_tensor([L - 1])
+        kn, vn = dev(k[L - 1:][None]), dev(v[L - 1:][None])
+        with nw.AttnContext(H, Hkv, cap, o_dtype="f32") as ctx:
+            ctx.set_decode_kernel(kernel)
+            ctx.set_decode_splits(splits)
+            outs = {}
+            for layout in (0, 1):
+                ctx.set_decode_layout(layout)
+                for sep in (True, False):
+                    ctx.set_decode_merge(sep)
+                    kc, vc = dev(stale_k), dev(stale_v)
+                    fused = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+                    ctx.append_decode(dev(q), kn, vn, kc, vc, pos, fused, 1, L)
+                    kc2, vc2 = dev(stale_k), dev(stale_v)
+                    ctx.kv_append(kn[:, None], vn[:, None], kc2, vc2, pos, 1, 1)
+                    assert torch.equal(kc.view(torch.int16), kc2.view(torch.int16))
+                    assert torch.equal(vc.view(torch.int16), vc2.view(torch.int16))
+                    two = _decode(ctx, dev(q), kc2, vc2, pos, 1, torch.float32, max_len=L)
+                    short = _decode(ctx, dev(q), kc2, vc2, pos, 1, torch.float32,
+                                    max_len=max(1, L // 3))
+                    assert ctx.device_status() == nw.NWD_OK
+                    f = host(fused)
+                    assert np.array_equal(f, two), (L, splits, layout, sep)
+                    assert max_abs(f[0], want) < TOL, (L, splits, layout, sep)
+                    assert max_abs(short[0], want) < TOL, (L, splits, layout, sep)
+                    if not sep:
+                        assert np.array_equal(f, outs[(layout, True)]), (L, splits, layout)
+                    outs[(layout, sep)] = f
+            assert max_abs(outs[(1, True)], outs[(0, True)]) < 1e-4
 
 
 @pytest.mark.parametrize("fill", [0x7E00, 0x7C00, 0xFC00])

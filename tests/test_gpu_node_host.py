@@ -99,16 +99,10 @@ def test_node_host_full_layer_from_hidden_state(tmp_path, mode):
     attn = np.fromfile(out / "attn.f32", np.float32).reshape(T, H, D)
     hout = np.fromfile(out / "hout.f32", np.float32).reshape(T, hid)
     k_rows, v_rows, worst = [], [], 0.0
-    # The prefill kernel's QK^T runs on fp16 MFMA inputs: each query row is
-    # scaled by c = scale * log2(e) and rounded to fp16 when it is loaded
-    # (the decode kernel keeps an fp32 query). The oracle is given the same
-    # rounded rows, fp16(q c) / c, which leaves its softmax and products as
-    # they are.
-    c = np.float32(1.0 / np.sqrt(np.float32(D))) * np.float32(np.log2(np.e))
+    # Both modes against the oracle on the same fp32 queries (the prefill
+    # keeps the scaled fp32 query as fp16 high and low parts).
     for t in range(T):
         q = oracle.q4_gemv_f32(hnorm[t], *wq).reshape(H, D)
-        if mode == "prefill":
-            q = (oracle.f16_to_f32(oracle.f32_to_f16((q * c).astype(np.float32))) / c).astype(np.float32)
         for rows, wm in ((k_rows, wk), (v_rows, wv)):
             rows.append(oracle.f16_to_f32(oracle.f32_to_f16(oracle.q4_gemv_f32(hnorm[t], *wm)))
                         .reshape(Hkv, D))

@@ -84,6 +84,105 @@ def test_prefill_batch_ragged_f32_io():
     assert _check_rows(out, q16, rows, pos0s, range(0, n_new, 3)) < TOL
 
 
+@pytest.mark.parametrize("sigma", [1.0, 4.0])
+def test_prefill_config5_offgrid_f32_queries(sigma):
+    """Config 5's shape (32q/8kv, 512 new tokens onto 8192) with fp32 queries
+    off the fp16 grid, as the engine's q projection produces them
+    (engine/runtime.js:120, kernels/sparse_attn.wgsl:19 reads f32 Q): every
+    query against the oracle run on the same fp32 query rows. sigma 4 gives
+    scores four times sharper than N(0, 1) rows, where a query rounded to
+    fp16 misses the bar."""
+    H, Hkv, P, n_new = 32, 8, 8192, 512
+    cap = P + n_new
+    say(f"config5 prefill fp32 off-grid queries sigma={sigma}")
+    g = rng(777 + int(sigma))
+    k, v = kv_rows(g, cap, Hkv)
+    q = (g.standard_normal((1, n_new, H, D)) * sigma).astype(np.float32)
+    assert not np.array_equal(q, f32(q.astype(np.float16)))
+    with nw.AttnContext(H, Hkv, cap, q_dtype="f32", o_dtype="f32") as ctx:
+        kc = dev(to_cache([k], Hkv, cap))
+        vc = dev(to_cache([v], Hkv, cap))
+        out = torch.empty((1, n_new, H, D), dtype=torch.float32, device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor([P]), out, 1, n_new, max_len=cap)
+        assert ctx.device_status() == nw.NWD_OK
+        got = out.cpu().numpy()[0]
+    kf, vf = f32(k), f32(v)
+    worst = 0.0
+    for i in range(n_new):
+        if i % 128 == 0:
+            say(f"  oracle queries {i}..{i + 127}")
+        want = oracle.sparse_attn_f32(q[0, i], kf[:P + i + 1], vf[:P + i + 1], threads=0)
+        worst = max(worst, max_abs(got[i], want))
+    say(f"  worst {worst:.2e}")
+    assert worst < TOL, worst
+
+
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_prefill_scaled_matches_sequential_decode(io):
+    """A non-default softmax scale (0.3, factor scale * log2 e = 0.43): the
+    prefill chunk against the token-by-token decode on the GPU and against
+    the float64 definition with that scale. fp16 queries are rounded once
+    more after the scaling in the prefill (the decode keeps them exact); the
+    bar is the same 2e-3."""
+    say(f"prefill scale 0.3 io={io} == sequential decode")
+    H, Hkv, P, n_new, scale = 32, 8, 300, 40, 0.3
+    cap = P + n_new
+    g = rng(94)
+    k, v = kv_rows(g, cap, Hkv)
+    q16 = normal_f16(g, (1, n_new, H, D))
+    qh = f32(q16) if io == "f32" else q16
+    if io == "f32":  # off the fp16 grid
+        qh = (qh + g.standard_normal(qh.shape).astype(np.float32) * 1e-3).astype(np.float32)
+    with nw.AttnContext(H, Hkv, cap, o_dtype="f32", q_dtype=io, scale=scale) as ctx:
+        kc, vc = dev(to_cache([k[:P]], Hkv, cap)), dev(to_cache([v[:P]], Hkv, cap))
+        seq = []
+        for i in range(n_new):
+            pos = pos_tensor([P + i])
+            ctx.kv_append(dev(k[P + i:P + i + 1][None]), dev(v[P + i:P + i + 1][None]), kc, vc, pos, 1, 1)
+            o = torch.empty((1, H, D), dtype=torch.float32, device="cuda")
+            ctx.decode(dev(qh[:, i]), kc, vc, pos, o, 1)
+            seq.append(o)
+        out = torch.empty((1, n_new, H, D), dtype=torch.float32, device="cuda")
+        ctx.prefill(dev(qh), kc, vc, pos_tensor([P]), out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    vs_decode = max_abs(got, torch.stack(seq, dim=1).cpu().numpy())
+    assert vs_decode < TOL, vs_decode
+    kf, vf, qf = f32(k), f32(v), np.asarray(qh, np.float32)
+    worst = 0.0
+    for i in (0, 7, 39):
+        want = oracle.attn_f64(qf[0, i], kf[:P + i + 1], vf[:P + i + 1], scale=scale)
+        worst = max(worst, max_abs(got[0, i], want))
+    assert worst < TOL, worst
+
+
+def test_prefill_query_range_flagged():
+    """An fp32 query whose scaled value leaves the fp16 range of the MFMA
+    operand (scale 8: factor 11.5, |q| = 8000) is reported by
+    nwd_device_status as NWD_ERR_DEVICE instead of passing silently; the
+    next call is clean. fp16 queries enter the MFMAs unscaled and are never
+    flagged."""
+    say("prefill query range flag")
+    H, Hkv, P, n_new = 8, 2, 64, 16
+    cap = P + n_new
+    g = rng(95)
+    k, v = kv_rows(g, cap, Hkv)
+    q = f32(normal_f16(g, (1, n_new, H, D)))
+    with nw.AttnContext(H, Hkv, cap, scale=8.0, q_dtype="f32", o_dtype="f32") as ctx:
+        kc, vc = dev(to_cache([k], Hkv, cap)), dev(to_cache([v], Hkv, cap))
+        out = torch.empty((1, n_new, H, D), dtype=torch.float32, device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor([P]), out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        big = q.copy()
+        big[0, 3, 5, 17] = np.float32(8000.0)
+        ctx.prefill(dev(big), kc, vc, pos_tensor([P]), out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_ERR_DEVICE
+        assert "fp16 range" in ctx.last_error()
+        ctx.prefill(dev(q), kc, vc, pos_tensor([P]), out, 1, n_new)
+        assert ctx.device_status() == nw.NWD_OK
+
+
 def test_prefill_from_empty_cache_is_causal():
     """pos0 = 0: query 0 sees only itself, so O = V[0] up to fp16 P rounding."""
     say("prefill from empty cache")
