@@ -189,9 +189,12 @@ class RaggedWorkload:
 
 class PrefillWorkload:
     """Causal chunked prefill: 512 new tokens appended at 8192 (one
-    nwd_kv_append of 512 rows) then nwd_prefill_attn over them."""
+    nwd_kv_append of 512 rows) then nwd_prefill_attn over them. q_dtype
+    "f32" gives fp32 queries and outputs (the engine's activations,
+    engine/runtime.js:120-123), the query rows off the fp16 grid."""
 
-    def __init__(self, torch, nw, past: int = 8192, n_new: int = 512, seed: int = 5):
+    def __init__(self, torch, nw, past: int = 8192, n_new: int = 512, seed: int = 5,
+                 q_dtype: str = "f16"):
         self.past, self.n_new, self.cap = past, n_new, past + n_new
         tg = torch.Generator(device="cuda")
         tg.manual_seed(seed)
@@ -202,11 +205,13 @@ class PrefillWorkload:
         self.kc = rnd(1, HKV, self.cap, D)
         self.vc = rnd(1, HKV, self.cap, D)
         self.q = rnd(1, n_new, H, D)
+        if q_dtype == "f32":
+            self.q = self.q.float() + 1e-3 * torch.randn(self.q.shape, generator=tg, device="cuda")
         self.knew = rnd(1, n_new, HKV, D)
         self.vnew = rnd(1, n_new, HKV, D)
         self.out = torch.empty_like(self.q)
         self.pos0 = torch.tensor([past], dtype=torch.int32, device="cuda")
-        self.ctx = nw.AttnContext(H, HKV, self.cap)
+        self.ctx = nw.AttnContext(H, HKV, self.cap, q_dtype=q_dtype, o_dtype=q_dtype)
 
     def step(self, s: int, stream, append=True):
         if append:
@@ -321,11 +326,21 @@ def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
             "cores": threads, "kind": "port", "sample": f"{done} calls, one layer's weights"}
 
 
-def time_graph(torch, wl, steps: int, warmup: int, append=True, reps: int = 1):
+def time_graph(torch, wl, steps: int, warmup: int, append=True, reps: int = 1,
+               preroll: int = 32):
     """Warm up eagerly, capture `steps` steps into a HIP graph, replay it once
     untimed and `reps` times timed. Returns (wall seconds, device ms) of the
     timed replay, the median one when reps > 1 (the first replays after a
-    capture can run at lower clocks)."""
+    capture can run at lower clocks).
+
+    A freshly captured graph is first replayed untimed for at least 30 ms:
+    its first replays run slower (decode-32k: 26.2-26.4 against 24.5 us per
+    step over the first ~20 ms after capture, ~1 us more per dispatch). Each
+    timed replay is preceded by an untimed pre-roll graph of the same
+    workload's steps (min(steps, preroll) of them), launched just before the
+    start event, so the GPU is busy while the host launches the timed graph.
+    Each graph launch still costs ~9 us of GPU time (its per-step share is
+    ~0.45 us at 20 steps, ~0.04 us at 256), which the timed region holds."""
     stream = torch.cuda.Stream()
     with torch.cuda.stream(stream):
         for s in range(warmup):
@@ -335,13 +350,24 @@ def time_graph(torch, wl, steps: int, warmup: int, append=True, reps: int = 1):
     with torch.cuda.graph(graph, stream=stream):
         for s in range(steps):
             wl.step(s, stream, append)
+    pre = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(pre, stream=stream):
+        for s in range(min(steps, preroll)):
+            wl.step(s, stream, append)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     runs = []
     with torch.cuda.stream(stream):  # replay() launches on the current stream
-        graph.replay()
-        torch.cuda.synchronize()
+        t_settle = time.perf_counter()
+        while True:
+            graph.replay()
+            pre.replay()
+            torch.cuda.synchronize()
+            if time.perf_counter() - t_settle > 0.03:
+                break
         for _ in range(reps):
+            torch.cuda.synchronize()
             t0 = time.perf_counter()
+            pre.replay()
             start.record(stream)
             graph.replay()
             end.record(stream)
@@ -351,16 +377,43 @@ def time_graph(torch, wl, steps: int, warmup: int, append=True, reps: int = 1):
     return runs[len(runs) // 2]
 
 
-def time_eager(torch, wl, steps: int):
+def warm_up(torch, wl, seconds: float = 0.25, append=True):
+    """Runs the workload's steps eagerly for `seconds` before anything is
+    timed: the first timed graph of a process otherwise meets a GPU whose
+    clocks have not settled (26.6 against 24.9 us per decode-32k step for the
+    same 20-step graph, first against later replays)."""
+    stream = torch.cuda.Stream()
+    t0, s = time.perf_counter(), 0
+    with torch.cuda.stream(stream):
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(16):
+                wl.step(s, stream, append)
+                s += 1
+            stream.synchronize()
+
+
+def time_eager(torch, wl, steps: int, append=True, reps: int = 1, preroll: int = 16):
+    """Exactly `steps` steps issued as ordinary calls (the way the engine's
+    token loop issues them), timed with events on their stream; each run is
+    preceded by `preroll` untimed calls of the same steps, so the GPU holds a
+    backlog of ~preroll steps while the host issues the timed ones and never
+    waits for the host. Returns the median device ms over `reps` runs."""
     stream = torch.cuda.Stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    for s in range(steps):
-        wl.step(s, stream)
-    end.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(end)
+    runs = []
+    with torch.cuda.stream(stream):
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            for s in range(preroll):
+                wl.step(s, stream, append)
+            start.record(stream)
+            for s in range(steps):
+                wl.step(s, stream, append)
+            end.record(stream)
+            torch.cuda.synchronize()
+            runs.append(start.elapsed_time(end))
+    runs.sort()
+    return runs[len(runs) // 2]
 
 
 def split_kernel_us(torch, hip: Hip, wl, calls: int):
@@ -392,10 +445,43 @@ def split_kernel_us(torch, hip: Hip, wl, calls: int):
     return sum(tot) / len(tot)
 
 
-def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "normal"):
+def host_info() -> dict:
+    """The host the CPU baselines ran on: logical CPUs, CPU model, and the
+    OpenMP threads the oracle uses."""
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu_model": model, "threads": oracle.max_threads()}
+
+
+def _oracle_kv(g, n: int, dist: str):
+    """Token-major [n][Hkv][D] f32 keys or values of a workload's distribution."""
+    import numpy as np
+
+    x = g.standard_normal((n, HKV, D), dtype=np.float32)
+    if dist == "outliers":
+        hit = g.random((n, HKV, D)) < 0.01
+        x[hit] = np.where(g.random(int(hit.sum())) < 0.5, -8.0, 8.0)
+    elif dist == "head-scale":
+        x *= g.uniform(0.5, 2.0, HKV).astype(np.float32)[None, :, None]
+    return x
+
+
+def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "normal",
+                 order=None):
     """The oracle (op-for-op CPU restatement of kernels/sparse_attn.wgsl +
     kv_append.wgsl, f32, per-head workgroups over OpenMP threads) on the same
-    workload shape, for as many steps of the window as fit in `budget_s`."""
+    workload shape: append+attend steps at positions past + i, i taken from
+    `order` (default 0, 1, ..., window - 1, repeated), for `budget_s` seconds
+    (at least one step)."""
     import numpy as np
 
     sys.path.insert(0, str(ROOT / "oracle"))
@@ -404,23 +490,17 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "no
     threads = oracle.max_threads()
     g = np.random.Generator(np.random.PCG64(7))
     cap = past + window
-
-    def kv():
-        x = g.standard_normal((cap, HKV, D), dtype=np.float32)
-        if dist == "outliers":
-            hit = g.random((cap, HKV, D)) < 0.01
-            x[hit] = np.where(g.random(int(hit.sum())) < 0.5, -8.0, 8.0)
-        return x
-
-    k, v = kv(), kv()
+    k, v = _oracle_kv(g, cap, dist), _oracle_kv(g, cap, dist)
     q = g.standard_normal((window, H, D), dtype=np.float32)
     kc = np.zeros(cap * HKV * D, np.float32)
     vc = np.zeros(cap * HKV * D, np.float32)
-    kc[: past * HKV * D] = k[:past].reshape(-1)
-    vc[: past * HKV * D] = v[:past].reshape(-1)
-    done, nbytes = 0, 0
+    kc[: cap * HKV * D] = k.reshape(-1)  # rows past a step's position are never read
+    vc[: cap * HKV * D] = v.reshape(-1)
+    order = list(order) if order is not None else list(range(window))
+    done, nbytes, seen = 0, 0, set()
     t0 = time.perf_counter()
-    for i in range(window):
+    while done == 0 or time.perf_counter() - t0 < budget_s:
+        i = order[done % len(order)]
         p = past + i
         oracle.kv_append_f32(k[p], kc, p, HKV, D)
         oracle.kv_append_f32(v[p], vc, p, HKV, D)
@@ -429,8 +509,7 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "no
                                vc[: L * HKV * D].reshape(L, HKV, D), threads=0)
         done += 1
         nbytes += kv_bytes(L)
-        if time.perf_counter() - t0 > budget_s:
-            break
+        seen.add(i)
     dt = time.perf_counter() - t0
     return {
         "value": round(nbytes / dt / 1e9, 3),
@@ -438,9 +517,58 @@ def cpu_baseline(past: int, window: int, budget_s: float = 20.0, dist: str = "no
         "us_per_step": round(dt / done * 1e6, 1),
         "cores": threads,
         "kind": "port",
-        "sample": f"{done} of the {window} append+attend steps at past {past} "
-                  f"(L = {past + 1}..{past + done}), one layer, f32 token-major cache",
+        "sample": f"{done} append+attend steps over {len(seen)} of the {window} positions "
+                  f"past {past} (L = {past + 1}..{past + window}), one layer, f32 token-major cache",
     }
+
+
+def cpu_baseline_ragged(budget_s: float = 6.0, batch: int = 64, seed: int = 4):
+    """The oracle on ragged-64 steps: each step appends one row to each of the
+    64 sequences and attends its past_b + 1 keys (the lengths of the GPU
+    workload; the K/V of every sequence are prefixes of one random cache)."""
+    import numpy as np
+
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import oracle
+
+    past = np.random.Generator(np.random.PCG64(seed)).integers(512, 16385, size=batch)
+    g = np.random.Generator(np.random.PCG64(8))
+    cap = int(past.max()) + 1
+    k, v = _oracle_kv(g, cap, "normal"), _oracle_kv(g, cap, "normal")
+    q = g.standard_normal((batch, H, D), dtype=np.float32)
+    kc, vc = k.reshape(-1).copy(), v.reshape(-1).copy()
+    done, nbytes = 0, 0
+    t0 = time.perf_counter()
+    while done == 0 or time.perf_counter() - t0 < budget_s:
+        for b in range(batch):
+            p = int(past[b])
+            oracle.kv_append_f32(k[p], kc, p, HKV, D)
+            oracle.kv_append_f32(v[p], vc, p, HKV, D)
+            L = p + 1
+            oracle.sparse_attn_f32(q[b], kc[: L * HKV * D].reshape(L, HKV, D),
+                                   vc[: L * HKV * D].reshape(L, HKV, D), threads=0)
+            nbytes += kv_bytes(L)
+        done += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes / dt / 1e9, 3), "unit": "GB/s",
+            "us_per_step": round(dt / done * 1e6, 1), "cores": oracle.max_threads(),
+            "kind": "port",
+            "sample": f"{done} step(s) of 64 sequences, past U{{512..16384}} (seed {seed}), "
+                      "one layer, f32 token-major caches"}
+
+
+def cpu_baseline_prefill(budget_s: float = 8.0, past: int = 8192, n_new: int = 512):
+    """The reference's prefill of prefill-512 on the host: the token loop of
+    engine/runtime.js:640-643, one append+attend step per prompt token
+    (L = past + 1 .. past + n_new), through the oracle. As many of the 512
+    steps as fit in the budget are run, every 8th token first so the sample
+    spans the chunk; the chunk's time is the mean step time x 512."""
+    order = [i for r in range(8) for i in range(r, n_new, 8)]
+    r = cpu_baseline(past, n_new, budget_s=budget_s, order=order)
+    per = r["us_per_step"]
+    return {"value": round(per * n_new / 1e3, 2), "unit": "ms per 512-token chunk",
+            "us_per_step": per, "cores": r["cores"], "kind": "port",
+            "sample": r["sample"].replace("append+attend steps", "token steps of the chunk")}
 
 
 WORKLOADS = {
@@ -471,6 +599,8 @@ EXTRA_WORKLOADS = {
                    "kv_append of 512 rows + fp16-MFMA prefill per step",
     "stream-read": "stream-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
                    "rotated) read with the split kernel's access pattern and nothing else",
+    "plain-read": "plain-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
+                  "rotated) read by a grid-stride kernel, the fastest of several launch shapes",
     "mfma-ceiling": "mfma-ceiling: 256 x 512-thread workgroups of 16x16x32 fp16 MFMAs only, "
                     "v_exp_f32 only (one per two MFMAs, the prefill's ratio), both, v_fma_f32 "
                     "only (one per MFMA) and MFMAs with FMAs",
@@ -485,7 +615,8 @@ EXTRA_WORKLOADS = {
 # shortens the headline's timed region).
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,
                    "decode-153": 1024, "ragged-64": 64,
-                   "prefill-512": 32, "stream-read": 64}
+                   "prefill-512": 32, "stream-read": 64, "plain-read": 64,
+                   "qkv-append": 256, "o-proj": 256, "lm-head": 32}
 
 
 def hbm_roofline(achieved_gbs: float, kernel: str, algorithmic_bytes: float, traffic):
@@ -508,9 +639,23 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     heads = WORKLOADS[name][5] if len(WORKLOADS[name]) > 5 else H
     log(f"[bench] {name}: past={past} window={window} layers={layers} heads={heads}, {steps} steps")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist, heads=heads)
-    # median of 3 timed replays, each of exactly `steps` steps
-    wall, ms = time_graph(torch, wl, steps, warmup, reps=3)
-    us_step = ms * 1e3 / steps
+    warm_up(torch, wl)
+    # The step, timed two ways over exactly `steps` append+attend steps: as
+    # calls issued the way the engine's token loop issues them (median of 5
+    # runs, behind a pre-roll so the GPU holds a backlog), and replayed from a
+    # HIP graph (median of 3). Each method adds a launch cost that is not the
+    # step's: a graph launch ~9 us of GPU time per replay (0.45 us per step at
+    # 20 steps), and calls leave the GPU waiting on the host where a step is
+    # shorter than the host's ~5-7 us per call (short contexts). us_per_step
+    # is the lower of the two; step_timing names it.
+    t0 = time.perf_counter()
+    ms = time_eager(torch, wl, steps, reps=5)
+    wall = time.perf_counter() - t0
+    calls_us_step = ms * 1e3 / steps
+    _, ms_g = time_graph(torch, wl, steps, warmup, reps=3)
+    graph_us_step = ms_g * 1e3 / steps
+    us_step = min(calls_us_step, graph_us_step)
+    step_timing = "calls" if calls_us_step <= graph_us_step else "graph"
     mean_b = wl.mean_kv_bytes(steps)
     # the decode call alone (split + merge kernels), same rotation
     n_dec = dec_steps or steps
@@ -518,8 +663,8 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     dec_us = ms_dec * 1e3 / n_dec
     dec_b = wl.mean_kv_bytes(n_dec)
     split_us = split_kernel_us(torch, hip, wl, 128)
-    n_eager = min(steps, 512)
-    eager_us = time_eager(torch, wl, n_eager) * 1e3 / n_eager
+    n_eager = min(max(steps, 256), 512)
+    eager_us = time_eager(torch, wl, n_eager, reps=3) * 1e3 / n_eager
     splits = wl.ctx.decode_splits(1, wl.cap)
     forced = {}
     for n in other_splits:
@@ -539,7 +684,8 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
         "workload": name, "desc": desc, "past": past, "window": window, "layers": layers,
         "steps": steps, "us_per_step": us_step, "gbs": mean_b / (us_step * 1e-6) / 1e9,
         "decode_us": dec_us, "decode_gbs": dec_b / (dec_us * 1e-6) / 1e9,
-        "split_kernel_us": split_us, "eager_us_per_step": eager_us, "mean_kv_bytes": mean_b,
+        "split_kernel_us": split_us, "eager_us_per_step": eager_us, "graph_us_per_step": graph_us_step,
+        "calls_us_per_step": calls_us_step, "step_timing": step_timing, "mean_kv_bytes": mean_b,
         "wall_s": wall, "splits": splits,
     }
     if forced:
@@ -571,8 +717,10 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
     res["call_roofline"] = {"achieved": round(res["decode_gbs"], 1),
                             "frac": round(res["decode_gbs"] / HBM_PEAK_GBS, 4),
                             "us": round(dec_us, 3)}
-    log(f"[bench] {name}: step {us_step:.3f} us ({res['gbs']:.1f} GB/s), decode call {dec_us:.3f} us "
-        f"({res['decode_gbs']:.1f} GB/s), split kernel {split_us:.3f} us, eager step {eager_us:.3f} us")
+    log(f"[bench] {name}: step {us_step:.3f} us ({res['gbs']:.1f} GB/s; calls {calls_us_step:.3f}, "
+        f"graph-replayed {graph_us_step:.3f}), "
+        f"decode call {dec_us:.3f} us ({res['decode_gbs']:.1f} GB/s), split kernel {split_us:.3f} us, "
+        f"{n_eager} calls {eager_us:.3f} us per step")
     wl.ctx.close()
     del wl
     torch.cuda.empty_cache()
@@ -582,6 +730,7 @@ def run_decode(torch, nw, hip, name: str, steps: int, warmup: int, dec_steps: in
 def run_ragged(torch, nw, steps: int, warmup: int):
     log(f"[bench] ragged-64: {steps} steps")
     wl = RaggedWorkload(torch, nw)
+    warm_up(torch, wl)
     wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
     _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
     us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
@@ -610,9 +759,9 @@ def run_ragged(torch, nw, steps: int, warmup: int):
     return res
 
 
-def run_prefill(torch, nw, steps: int, warmup: int):
-    log(f"[bench] prefill-512: {steps} steps")
-    wl = PrefillWorkload(torch, nw)
+def run_prefill(torch, nw, steps: int, warmup: int, q_dtype: str = "f16", library=True):
+    log(f"[bench] prefill-512 ({q_dtype} queries): {steps} steps")
+    wl = PrefillWorkload(torch, nw, q_dtype=q_dtype)
     # The matrix cores' clock settles over the first milliseconds of this
     # load (the first timed graph ran 4-5 us per step slower than later ones):
     # one untimed pass of the same graph first.
@@ -621,19 +770,20 @@ def run_prefill(torch, nw, steps: int, warmup: int):
     _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
     us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
     tflops = wl.flops() / (us_main * 1e-6) / 1e12
-    res = {"workload": "prefill-512", "desc": EXTRA_WORKLOADS["prefill-512"],
+    res = {"workload": "prefill-512", "desc": EXTRA_WORKLOADS["prefill-512"], "q_dtype": q_dtype,
            "us_per_step": us_step, "prefill_us": us_main, "wall_s": wall, "flops": wl.flops(),
            "roofline": {"bound": "mfma", "kernel": "nwd_prefill_attn (prefill + split merge)",
                         "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                         "traffic": measured_traffic("prefill-512"), "algorithmic_flops": wl.flops()}}
-    log(f"[bench] prefill-512: step {us_step:.1f} us (kv_append + prefill), prefill {us_main:.1f} us "
-        f"({tflops:.1f} TFLOP/s)")
-    lib = library_prefill(torch, wl)
-    if "us" in lib:
-        lib["nwd_speedup"] = lib["us"] / us_main
-    res["library_baseline"] = lib
-    log(f"[bench] prefill-512 through torch's fused attention: {lib}")
+    log(f"[bench] prefill-512 ({q_dtype}): step {us_step:.1f} us (kv_append + prefill), prefill "
+        f"{us_main:.1f} us ({tflops:.1f} TFLOP/s)")
+    if library:
+        lib = library_prefill(torch, wl)
+        if "us" in lib:
+            lib["nwd_speedup"] = lib["us"] / us_main
+        res["library_baseline"] = lib
+        log(f"[bench] prefill-512 through torch's fused attention: {lib}")
     wl.ctx.close()
     del wl
     torch.cuda.empty_cache()
@@ -724,6 +874,60 @@ def run_stream_read(torch, nw, launches: int):
     return res
 
 
+# Launch shapes of the plain read (threads per workgroup, 16-byte loads in
+# flight per thread, workgroups): 2 to 4 wavefronts per SIMD, 4-8 KB in flight
+# per wavefront, the best of a sweep of 96 shapes on MI355X among them.
+PLAIN_READ_SHAPES = ((512, 4, 256), (256, 4, 512), (256, 8, 512), (256, 4, 1024),
+                     (1024, 4, 256), (256, 2, 1024))
+
+
+def run_plain_read(torch, nw, launches: int):
+    """An independent read ceiling: the decode-32k bytes (the same 4 layer
+    caches, 134 MB per launch) read by a grid-stride kernel that shares
+    nothing with the decode's grid (csrc/bench/nwd_stream_read.hip,
+    plain_read_kernel): every workgroup walks chunks spread over all the
+    bytes, many wavefronts per CU, non-temporal loads. Each shape of
+    PLAIN_READ_SHAPES is graph-replayed; the fastest is the ceiling."""
+    lib = ctypes.CDLL(str(BENCH_LIB))
+    lib.nwd_bench_plain_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 7 + [
+        ctypes.c_void_p, ctypes.c_void_p]
+    past, window, layers, dist, _ = WORKLOADS["decode-32k"]
+    log(f"[bench] plain-read: {len(PLAIN_READ_SHAPES)} shapes x {launches} launches")
+    wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
+    keys = past + 1
+    out = torch.empty(max(t * g for t, _, g in PLAIN_READ_SHAPES), dtype=torch.float32,
+                      device="cuda")
+    b = kv_bytes(keys)
+
+    class Reader:
+        def __init__(self, shape):
+            self.shape = shape
+
+        def step(self, s, stream, append=True):
+            t, u, g = self.shape
+            rc = lib.nwd_bench_plain_read(wl.kc[s % layers].data_ptr(), wl.vc[s % layers].data_ptr(),
+                                          HKV, wl.cap, keys, t, u, g, 1, out.data_ptr(),
+                                          stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"nwd_bench_plain_read: hip error {rc}")
+
+    by_shape = {}
+    for shape in PLAIN_READ_SHAPES:
+        _, ms = time_graph(torch, Reader(shape), launches, 8, reps=3)
+        by_shape["x".join(map(str, shape))] = ms * 1e3 / launches
+    best = min(by_shape, key=by_shape.get)
+    us = by_shape[best]
+    res = {"workload": "plain-read", "desc": EXTRA_WORKLOADS["plain-read"], "us_per_launch": us,
+           "bytes": b, "gbs": b / (us * 1e-6) / 1e9, "frac": b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "best_shape": best, "us_by_shape_threads_x_loads_x_workgroups": by_shape}
+    log(f"[bench] plain-read: {us:.3f} us per 134 MB launch ({res['gbs']:.1f} GB/s), shape {best}; "
+        f"{ {k: round(v, 2) for k, v in by_shape.items()} }")
+    wl.ctx.close()
+    del wl, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def run_mfma_ceiling(torch, iters: int = 2048, launches: int = 5):
     """The matrix-core ceiling under load and how much of the prefill's
     exponential work hides under its MFMAs (csrc/bench/nwd_mfma_ceiling.hip):
@@ -780,17 +984,22 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
     """One 4-bit projection workload: us per call and weight-stream GB/s."""
     log(f"[bench] {name}: {steps} steps")
     wl = Q4LayerWorkload(torch, nw, name)
+    warm_up(torch, wl, 0.1)
     wall, ms = time_graph(torch, wl, steps, warmup, reps=5)
     us = ms * 1e3 / steps
     gbs = wl.bytes_per_step() / (us * 1e-6) / 1e9
+    kernel = {"qkv-append": "qkv_append_kernel (q/k/v 4-bit GEMVs, k/v into the fp16 caches)",
+              "o-proj": "q4_gemv_kernel (accumulate epilogue: o_proj + residual)",
+              "lm-head": "q4w_argmax_kernel + argmax_merge_kernel (lm_head + greedy pick)"}[name]
     res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "us_per_step": us,
            "bytes_per_step": wl.bytes_per_step(), "gbs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS,
-           "traffic": measured_traffic(name), "wall_s": wall}
+           "traffic": measured_traffic(name), "wall_s": wall,
+           "roofline": hbm_roofline(gbs, kernel, wl.bytes_per_step(), measured_traffic(name))}
     wl.ctx.close()
     del wl
     torch.cuda.empty_cache()
     if cpu:
-        res["cpu_baseline"] = q4_cpu_baseline(name)
+        res["cpu_baseline"] = q4_cpu_baseline(name, budget_s=4.0)
     log(f"[bench] {name}: {res}")
     return res
 
@@ -878,6 +1087,8 @@ def main():
             r = run_prefill(torch, nw, args.steps, args.warmup)
         elif w == "stream-read":
             r = run_stream_read(torch, nw, args.steps)
+        elif w == "plain-read":
+            r = run_plain_read(torch, nw, args.steps)
         elif w == "mfma-ceiling":
             r = run_mfma_ceiling(torch)
         else:
@@ -896,18 +1107,39 @@ def main():
         "decode-4k": run_decode(torch, nw, hip, "decode-4k", SECONDARY_STEPS["decode-4k"], 32),
         "ragged-64": run_ragged(torch, nw, SECONDARY_STEPS["ragged-64"], 8),
         "prefill-512": run_prefill(torch, nw, SECONDARY_STEPS["prefill-512"], 4),
+        "prefill-512-f32q": run_prefill(torch, nw, SECONDARY_STEPS["prefill-512"], 4, q_dtype="f32",
+                                        library=False),
     }
+    # the attention layer's 4-bit projections and the step's lm_head with its
+    # greedy pick (the rows around the path), each with its roofline
+    for q4 in ("qkv-append", "o-proj", "lm-head"):
+        configs[q4] = run_q4(torch, nw, q4, SECONDARY_STEPS[q4], 8, cpu=not args.no_cpu_baseline)
     stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
+    plain = run_plain_read(torch, nw, SECONDARY_STEPS["plain-read"])
     ceiling = run_mfma_ceiling(torch)
-    pre = configs["prefill-512"]["roofline"]
-    pre["frac_of_mfma_ceiling"] = pre["achieved"] / ceiling["mfma_tflops"]
+    for k in ("prefill-512", "prefill-512-f32q"):
+        pre = configs[k]["roofline"]
+        pre["frac_of_mfma_ceiling"] = pre["achieved"] / ceiling["mfma_tflops"]
+    for k in ("decode-32k-nano",):
+        configs[k]["frac_of_plain_read"] = plain["us_per_launch"] / configs[k]["decode_us"]
     copy_gbs = copy_bandwidth(torch)
     log(f"[bench] device copy {copy_gbs} GB/s (read+write)")
     cpu = None
     if not args.no_cpu_baseline:
-        log("[bench] cpu baseline (decode-32k)")
+        host = host_info()
+        log(f"[bench] cpu baselines on {host}")
         cpu = cpu_baseline(head["past"], head["window"], dist="outliers")
-        log(f"[bench] cpu: {cpu}")
+        cpu.update(host)
+        log(f"[bench] cpu decode-32k: {cpu}")
+        per_config = {
+            "decode-153": lambda: cpu_baseline(152, 1, budget_s=3.0),
+            "decode-4k": lambda: cpu_baseline(4096, 64, budget_s=5.0, dist="head-scale"),
+            "ragged-64": cpu_baseline_ragged,
+            "prefill-512": cpu_baseline_prefill,
+        }
+        for k, fn in per_config.items():
+            configs[k]["cpu_baseline"] = dict(fn(), **host)
+            log(f"[bench] cpu {k}: {configs[k]['cpu_baseline']}")
 
     us_step, gbs = head["us_per_step"], head["gbs"]
     line = {
@@ -931,23 +1163,35 @@ def main():
             "batch": 1, "n_heads": H, "n_kv_heads": HKV, "head_dim": D,
             "past": head["past"], "window": head["window"],
             "layers": head["layers"], "decode_splits": head["splits"],
-            "timing": "median of 3 HIP graph replays of exactly `steps` append+attend steps "
-                      "each, hipEvents on the launching stream",
+            "timing": "exactly `steps` append+attend steps timed with hipEvents on their "
+                      "stream after a 0.25 s warm-up, two ways: as calls issued like a token "
+                      "loop (median of 5 runs, behind 16 untimed calls so the GPU never waits "
+                      "for the host) and replayed from a HIP graph (median of 3, behind an "
+                      "untimed pre-roll graph); us_per_step is the lower, step_timing names it",
         },
+        "step_timing": head["step_timing"],
+        "calls_us_per_step": round(head["calls_us_per_step"], 3),
+        "graph_us_per_step": round(head["graph_us_per_step"], 3),
         "eager_us_per_step": round(head["eager_us_per_step"], 3),
         "roofline": rounded(head["roofline"]),
         "decode_call": {"us": round(head["decode_us"], 3), "gbs": round(head["decode_gbs"], 1),
                         "frac": round(head["decode_gbs"] / HBM_PEAK_GBS, 4),
                         "split_kernel_us": round(head["split_kernel_us"], 3),
                         "split_kernel": head["split_kernel"],
-                        "us_by_kernel": rounded(head.get("decode_us_by_kernel", {}))},
+                        "us_by_kernel": rounded(head.get("decode_us_by_kernel", {})),
+                        # the call against the fastest plain read of the same bytes
+                        "frac_of_plain_read": round(plain["us_per_launch"] / head["decode_us"], 4),
+                        "split_kernel_frac_of_plain_read":
+                            round(plain["us_per_launch"] / head["kernel_us"], 4)},
         "cpu_baseline": cpu,
         "configs": {k: rounded({kk: vv for kk, vv in v.items() if kk != "mean_kv_bytes"})
                     for k, v in configs.items()},
         "stream_read": rounded(stream),
+        "plain_read": rounded(plain),
         "mfma_ceiling": rounded(ceiling),
         "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(head["wall_s"], 4),
+        "library_source_sha256": nw.source_hash(),
     }
     print(json.dumps(line), flush=True)
 

@@ -20,6 +20,7 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -63,8 +64,29 @@ FILE_FLAGS = {"nwd_prefill.hip": ["-fno-honor-nans"]}
 ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer"]
 
 
+def source_files() -> list:
+    """The files nwd_source_hash covers: csrc/**/*.hip and *.h in name
+    order, then include/nwd_attn.h."""
+    files = sorted(p for p in CSRC.rglob("*") if p.suffix in (".hip", ".h"))
+    return files + [INCLUDE / "nwd_attn.h"]
+
+
+def source_hash() -> str:
+    """SHA-256 over each source file's path (relative to the repository
+    root), a NUL and its bytes; the value nwd_source_hash() returns for a
+    library built from these files."""
+    h = hashlib.sha256()
+    root = PKG.parent
+    for f in source_files():
+        h.update(f.relative_to(root).as_posix().encode() + b"\0")
+        h.update(f.read_bytes())
+    return h.hexdigest()
+
+
 def _compile(src: Path, objdir: Path = OBJ, extra: tuple = ()) -> Path:
     out = objdir / (src.stem + ".o")
+    if src.name == "nwd_api.hip":
+        extra = (*extra, f'-DNWD_SOURCE_HASH="{source_hash()}"')
     cmd = [HIPCC, *DEVICE_FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o",
            str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)

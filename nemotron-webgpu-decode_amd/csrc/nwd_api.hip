@@ -319,6 +319,11 @@ void nwd_destroy(nwd_ctx* ctx) {
   delete ctx;
 }
 
+#ifndef NWD_SOURCE_HASH
+#error "build with -DNWD_SOURCE_HASH=\"<sha256 of the sources>\" (build.py does)"
+#endif
+const char* nwd_source_hash(void) { return NWD_SOURCE_HASH; }
+
 const char* nwd_last_error(const nwd_ctx* ctx) {
   return ctx ? ctx->err.c_str() : g_create_err.c_str();
 }

@@ -505,9 +505,12 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int n_it = t1 > t0 ? (t1 - t0 + it_keys - 1) / it_keys : 0;
   const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
 
-  // Fused append: the split holding the new position substitutes the new
-  // rows for the cache rows it loads, and writes them to the caches at the
-  // end of the kernel.
+  // Fused append: the split holding the new position writes the new rows to
+  // the caches as soon as the position is known (no other split reads that
+  // row, and this split's own loads of it are replaced, so the store may
+  // land at any time; issued here it overlaps the stream instead of adding a
+  // store round trip after the epilogue), and substitutes them for the cache
+  // rows it loads.
   const int pnew = L - 1;
   const bool owns_new =
       has_new && pos_ok && t0 <= pnew && pnew < t1 && (pnew - t0) % it_keys < kBlockKeys;
@@ -522,6 +525,18 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     for (int i = 0; i < kRuns; ++i) {
       nk[i] = convert_src_run(nk_raw[i], a.new16);
       nv[i] = convert_src_run(nv_raw[i], a.new16);
+    }
+    // the lanes of row 0 of wavefront 0 hold the runs of the new K row, those
+    // of row 1 the V row's
+    if (wave == 0 && row < 2 && sub == 0) {
+#pragma unroll
+      for (int i = 0; i < kRuns; ++i) {
+        const int64_t at = slab + (int64_t)pnew * kHeadDim + (col + i * kLanes) * 8;
+        if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kHeadDim, a.status)) {
+          f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
+          *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
+        }
+      }
     }
   }
 
@@ -677,18 +692,6 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   __syncthreads();
 
   store_split_states<G, kO16, kStates>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0, split);
-  // The new rows go to the caches last: the lanes of row 0 of wavefront 0
-  // hold the 16 runs of the new K row in nk, those of row 1 the V row's.
-  if (owns_new && wave == 0 && row < 2 && sub == 0) {
-#pragma unroll
-    for (int i = 0; i < kRuns; ++i) {
-      const int64_t at = slab + (int64_t)pnew * kHeadDim + (col + i * kLanes) * 8;
-      if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kHeadDim, a.status)) {
-        f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
-        *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
-      }
-    }
-  }
   if (nsplit == 1 || !a.fused_merge) return;
   merge_on_last_arrival<G, kO16>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
                                  (int64_t)b * a.n_heads + h0);
@@ -894,9 +897,11 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const int n_it = t1 > t0 ? (t1 - t0 + it_keys - 1) / it_keys : 0;
   const auto rk = slab_rsrc(a.k_cache, max(t1, 0)), rv = slab_rsrc(a.v_cache, max(t1, 0));
 
-  // Fused append: the wavefront whose block holds the new position
-  // substitutes the new rows (K in its fragments, V in its LDS slot) and
-  // writes them to the caches at the end.
+  // Fused append: the wavefront whose block holds the new position writes
+  // the new rows to the caches as soon as the position is known (as in
+  // decode_split_kernel) and substitutes them (K in its fragments, V in its
+  // LDS slot). Its stores are older than the next block's loads, so the
+  // block waits below cover them.
   const int pnew = L - 1;
   const bool owns_new =
       has_new && pos_ok && t0 <= pnew && pnew < t1 && (pnew - t0) % it_keys < kMBlockKeys;
@@ -908,6 +913,21 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
 #pragma unroll
     for (int db = 0; db < 4; ++db) nk[db] = convert_src_run(nk_raw[db], a.new16);
     nv = convert_src_run(nv_raw, a.new16);
+    // K chunks 4 db + lq from the lanes of key row 0, V chunk lr from lane
+    // group 0
+    if (wave == w_new) {
+      const int64_t at = slab + (int64_t)pnew * kHeadDim;
+      const int64_t cache_elems = (int64_t)a.batch * a.n_kv * a.cap * kHeadDim;
+      if (lr == 0) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const int64_t e = at + db * 32 + 8 * lq;
+          if (in_bounds(e, 8, cache_elems, a.status)) *reinterpret_cast<f16x8*>(a.k_cache + e) = nk[db];
+        }
+      }
+      if (lq == 0 && in_bounds(at + 8 * lr, 8, cache_elems, a.status))
+        *reinterpret_cast<f16x8*>(a.v_cache + at + 8 * lr) = nv;
+    }
   }
 
   const float c = a.qk_scale_log2;
@@ -1046,21 +1066,6 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   __syncthreads();
   const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
   store_split_states<G, kO16, kMWaves>(a, lds_o, lds_ml, hrow0, split);
-  // The new rows to the caches: K chunks 4 db + lq from the lanes of key
-  // row 0, V chunk lr from lane group 0.
-  if (owns_new && wave == w_new) {
-    const int64_t at = slab + (int64_t)pnew * kHeadDim;
-    const int64_t cache_elems = (int64_t)a.batch * a.n_kv * a.cap * kHeadDim;
-    if (lr == 0) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int64_t e = at + db * 32 + 8 * lq;
-        if (in_bounds(e, 8, cache_elems, a.status)) *reinterpret_cast<f16x8*>(a.k_cache + e) = nk[db];
-      }
-    }
-    if (lq == 0 && in_bounds(at + 8 * lr, 8, cache_elems, a.status))
-      *reinterpret_cast<f16x8*>(a.v_cache + at + 8 * lr) = nv;
-  }
   if (nsplit == 1 || !a.fused_merge) return;
   merge_on_last_arrival<G, kO16>(a, a.counters + b * a.n_kv + hkv,
                                  hrow0);

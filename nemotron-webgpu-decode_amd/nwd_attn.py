@@ -106,6 +106,7 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
         "nwd_create": (ctypes.c_int, [ctypes.POINTER(NwdDesc), ctypes.POINTER(vp)]),
         "nwd_destroy": (None, [vp]),
         "nwd_last_error": (ctypes.c_char_p, [vp]),
+        "nwd_source_hash": (ctypes.c_char_p, []),
         "nwd_cache_bytes": (ctypes.c_size_t, [vp]),
         "nwd_cache_offset": (i64, [vp, i32, i32, i32, i32]),
         "nwd_kv_append": (ctypes.c_int, [vp, vp, vp, vp, vp, vp, i32, i32, vp]),
@@ -136,6 +137,12 @@ def load_library(path: Optional[os.PathLike] = None) -> ctypes.CDLL:
     if path is None:
         _lib = lib
     return lib
+
+
+def source_hash(lib: Optional[ctypes.CDLL] = None) -> str:
+    """nwd_source_hash() of the loaded library (the hash of the sources it
+    was built from; build.source_hash() gives that of the sources on disk)."""
+    return (lib or load_library()).nwd_source_hash().decode()
 
 
 _others: dict = {}

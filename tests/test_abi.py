@@ -76,3 +76,15 @@ def test_null_arguments(lib):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="build the HIP library"):
         nw.load_library(tmp_path / "libnwd_attn.so")
+
+
+def test_library_matches_the_sources_on_disk(lib):
+    """nwd_source_hash() of the built library equals the hash of csrc/ and
+    include/nwd_attn.h as they are now, so the tested library is the one these
+    sources build (build.py embeds it at compile time)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("nwd_build_for_hash", nw.PKG_DIR / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    assert nw.source_hash(lib) == build.source_hash(), "rebuild: python nemotron-webgpu-decode_amd/build.py"
+    assert len(nw.source_hash(lib)) == 64

@@ -37,6 +37,18 @@ def _decode(ctx, q, kc, vc, pos, batch, out_dtype=torch.float16, max_len=0):
     return out.float().cpu().numpy()
 
 
+def test_loaded_library_matches_sources():
+    """The library these GPU tests load was built from the sources on disk
+    (nwd_source_hash against build.source_hash), so their evidence is tied to
+    this tree."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("nwd_build_for_hash", nw.PKG_DIR / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    say(f"library sources sha256 {nw.source_hash()[:16]}")
+    assert nw.source_hash() == build.source_hash()
+
+
 # -------------------------------------------------------------- kv_append ---
 
 def test_kv_append_bit_exact_f16():
