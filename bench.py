@@ -597,6 +597,9 @@ EXTRA_WORKLOADS = {
                  "append+attend per step",
     "prefill-512": "prefill-512: B=1, 512 new tokens onto 8192 cached, causal in the chunk, "
                    "kv_append of 512 rows + fp16-MFMA prefill per step",
+    "prefill-512-f32q": "prefill-512-f32q: prefill-512 with fp32 queries off the fp16 grid and "
+                        "fp32 outputs (the engine's activations), the query as fp16 high and low "
+                        "parts in the QK^T MFMAs",
     "stream-read": "stream-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
                    "rotated) read with the split kernel's access pattern and nothing else",
     "plain-read": "plain-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
@@ -770,12 +773,13 @@ def run_prefill(torch, nw, steps: int, warmup: int, q_dtype: str = "f16", librar
     _, ms_main = time_graph(torch, wl, steps, 0, append=False, reps=5)
     us_step, us_main = ms * 1e3 / steps, ms_main * 1e3 / steps
     tflops = wl.flops() / (us_main * 1e-6) / 1e12
-    res = {"workload": "prefill-512", "desc": EXTRA_WORKLOADS["prefill-512"], "q_dtype": q_dtype,
+    name = "prefill-512" if q_dtype == "f16" else "prefill-512-f32q"
+    res = {"workload": name, "desc": EXTRA_WORKLOADS[name], "q_dtype": q_dtype,
            "us_per_step": us_step, "prefill_us": us_main, "wall_s": wall, "flops": wl.flops(),
            "roofline": {"bound": "mfma", "kernel": "nwd_prefill_attn (prefill + split merge)",
                         "achieved": round(tflops, 1), "peak": MFMA_F16_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
-                        "traffic": measured_traffic("prefill-512"), "algorithmic_flops": wl.flops()}}
+                        "traffic": measured_traffic(name), "algorithmic_flops": wl.flops()}}
     log(f"[bench] prefill-512 ({q_dtype}): step {us_step:.1f} us (kv_append + prefill), prefill "
         f"{us_main:.1f} us ({tflops:.1f} TFLOP/s)")
     if library:
@@ -1085,6 +1089,8 @@ def main():
             r = run_ragged(torch, nw, args.steps, args.warmup)
         elif w == "prefill-512":
             r = run_prefill(torch, nw, args.steps, args.warmup)
+        elif w == "prefill-512-f32q":
+            r = run_prefill(torch, nw, args.steps, args.warmup, q_dtype="f32", library=False)
         elif w == "stream-read":
             r = run_stream_read(torch, nw, args.steps)
         elif w == "plain-read":
