@@ -894,7 +894,7 @@ def run_plain_read(torch, nw, launches: int):
     PLAIN_READ_SHAPES is graph-replayed; the fastest is the ceiling."""
     lib = ctypes.CDLL(str(BENCH_LIB))
     lib.nwd_bench_plain_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 7 + [
-        ctypes.c_void_p, ctypes.c_void_p]
+        ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int]
     past, window, layers, dist, _ = WORKLOADS["decode-32k"]
     log(f"[bench] plain-read: {len(PLAIN_READ_SHAPES)} shapes x {launches} launches")
     wl = DecodeWorkload(torch, nw, past, window, layers, seed=1234, dist=dist)
@@ -911,7 +911,7 @@ def run_plain_read(torch, nw, launches: int):
             t, u, g = self.shape
             rc = lib.nwd_bench_plain_read(wl.kc[s % layers].data_ptr(), wl.vc[s % layers].data_ptr(),
                                           HKV, wl.cap, keys, t, u, g, 1, out.data_ptr(),
-                                          stream.cuda_stream)
+                                          stream.cuda_stream, 0)
             if rc != 0:
                 raise RuntimeError(f"nwd_bench_plain_read: hip error {rc}")
 
@@ -1006,6 +1006,34 @@ def run_q4(torch, nw, name: str, steps: int, warmup: int, cpu: bool):
         res["cpu_baseline"] = q4_cpu_baseline(name, budget_s=4.0)
     log(f"[bench] {name}: {res}")
     return res
+
+
+def run_node_layer(past: int = 4096, steps: int = 64, warmup: int = 8):
+    """The attention layers of a decode step driven from Node.js over the
+    N-API addon (js/bench_layer.js: per token, the 4 attention layers of the
+    Nano-4B shape, each qkv_append + append-decode + o_proj with the residual,
+    as engine/runtime.js:386-393 and :447-469 dispatch them), run as a child
+    process; None when node or the addon is absent."""
+    import shutil
+    import subprocess
+
+    node = shutil.which("node")
+    script = ROOT / "nemotron-webgpu-decode_amd" / "js" / "bench_layer.js"
+    addon = ROOT / "nemotron-webgpu-decode_amd" / "lib" / "nwd_napi.node"
+    if not node or not addon.exists():
+        return None
+    log(f"[bench] node-layer: past {past}, {steps} tokens")
+    res = subprocess.run([node, str(script), str(past), str(steps), str(warmup)], capture_output=True,
+                         text=True, timeout=180)
+    if res.returncode != 0:
+        log(f"[bench] node-layer failed: {res.stderr[-500:]}")
+        return {"error": res.stderr[-300:]}
+    r = json.loads(res.stdout.strip().splitlines()[-1])
+    r["desc"] = ("node-layer: Nano-4B 40q/8kv, past 4096, a token's 4 attention layers from the "
+                 "hidden state (q/k/v 4-bit + append + decode + o_proj + residual), every call "
+                 "from JavaScript (eager) or the token replayed as a HIP graph")
+    log(f"[bench] node-layer: {r}")
+    return r
 
 
 def measured_traffic(name: str):
@@ -1120,6 +1148,9 @@ def main():
     # greedy pick (the rows around the path), each with its roofline
     for q4 in ("qkv-append", "o-proj", "lm-head"):
         configs[q4] = run_q4(torch, nw, q4, SECONDARY_STEPS[q4], 8, cpu=not args.no_cpu_baseline)
+    node_layer = run_node_layer()
+    if node_layer is not None:
+        configs["node-layer"] = node_layer
     stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
     plain = run_plain_read(torch, nw, SECONDARY_STEPS["plain-read"])
     ceiling = run_mfma_ceiling(torch)

@@ -91,11 +91,21 @@ namespace {
 template <int kU, int kPolicy>
 __global__ void plain_read_kernel(const char* __restrict__ k, const char* __restrict__ v,
                                   int64_t slab_stride, int64_t range_bytes, int64_t chunks_per_range,
-                                  int64_t chunks, float* __restrict__ out) {
+                                  int64_t chunks, float* __restrict__ out, int per_range) {
   const int tid = threadIdx.x, nt = blockDim.x;
   const int64_t chunk_bytes = (int64_t)kU * nt * 16;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t c = blockIdx.x; c < chunks; c += gridDim.x) {
+  // per_range: the workgroups are dealt to the 2 x slabs ranges (workgroup w
+  // reads range w % ranges only), each range swept by its own workgroups
+  // with a grid stride, so that as many regions are read at once as the
+  // decode reads (K and V of every KV head); otherwise one sweep of all.
+  const int64_t ranges = chunks / chunks_per_range;
+  const int64_t g_per = gridDim.x / ranges;
+  const int64_t c0 = per_range ? (blockIdx.x % ranges) * chunks_per_range + blockIdx.x / ranges
+                               : (int64_t)blockIdx.x;
+  const int64_t c_end = per_range ? (blockIdx.x % ranges + 1) * chunks_per_range : chunks;
+  const int64_t c_step = per_range ? g_per : (int64_t)gridDim.x;
+  for (int64_t c = c0; c < c_end; c += c_step) {
     const int64_t range = c / chunks_per_range;  // 2 * slab + (0: K, 1: V)
     const int64_t in_range = (c - range * chunks_per_range) * chunk_bytes;
     const char* base = ((range & 1) ? v : k) + (range >> 1) * slab_stride + in_range;
@@ -117,13 +127,13 @@ __global__ void plain_read_kernel(const char* __restrict__ k, const char* __rest
 template <int kU>
 hipError_t launch_plain(int nt_policy, dim3 grid, int threads, hipStream_t s, const char* k,
                         const char* v, int64_t slab_stride, int64_t range_bytes, int64_t cpr,
-                        int64_t chunks, float* out) {
+                        int64_t chunks, float* out, int per_range) {
   if (nt_policy)
     plain_read_kernel<kU, kNonTemporal><<<grid, threads, 0, s>>>(k, v, slab_stride, range_bytes,
-                                                                 cpr, chunks, out);
+                                                                 cpr, chunks, out, per_range);
   else
     plain_read_kernel<kU, 0><<<grid, threads, 0, s>>>(k, v, slab_stride, range_bytes, cpr, chunks,
-                                                      out);
+                                                      out, per_range);
   return hipGetLastError();
 }
 
@@ -131,14 +141,15 @@ hipError_t launch_plain(int nt_policy, dim3 grid, int threads, hipStream_t s, co
 
 // Reads keys [0, keys) of `slabs` K and V slabs of `cap` fp16 rows each with
 // `grid` workgroups of `threads` threads, `unroll` 16-byte loads per thread
-// and chunk (1, 2, 4, 8 or 16), the non-temporal policy if `nt`. out needs
-// grid * threads floats. Returns a hipError_t code.
+// and chunk (1, 2, 4, 8 or 16), the non-temporal policy if `nt`; with
+// per_range, grid must be a multiple of 2 x slabs and each workgroup sweeps
+// one range. out needs grid * threads floats. Returns a hipError_t code.
 extern "C" int nwd_bench_plain_read(const void* k, const void* v, int slabs, int cap, int keys,
                                     int threads, int unroll, int grid, int nt, float* out,
-                                    void* stream) {
+                                    void* stream, int per_range) {
   if (!k || !v || !out || slabs < 1 || cap < 1 || keys < 1 || keys > cap || grid < 1 ||
       threads < 64 || threads > 1024 || threads % 64 != 0 ||
-      (int64_t)cap * kRowBytes > 0x7FFFFFFF)
+      (int64_t)cap * kRowBytes > 0x7FFFFFFF || (per_range && grid % (2 * slabs) != 0))
     return (int)hipErrorInvalidValue;
   const int64_t chunk_bytes = (int64_t)unroll * threads * 16;
   const int64_t range_bytes = (int64_t)keys * kRowBytes;
@@ -150,11 +161,11 @@ extern "C" int nwd_bench_plain_read(const void* k, const void* v, int slabs, int
   hipStream_t s = (hipStream_t)stream;
   const dim3 g((unsigned)grid);
   switch (unroll) {
-    case 1: return (int)launch_plain<1>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
-    case 2: return (int)launch_plain<2>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
-    case 4: return (int)launch_plain<4>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
-    case 8: return (int)launch_plain<8>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
-    case 16: return (int)launch_plain<16>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out);
+    case 1: return (int)launch_plain<1>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out, per_range);
+    case 2: return (int)launch_plain<2>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out, per_range);
+    case 4: return (int)launch_plain<4>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out, per_range);
+    case 8: return (int)launch_plain<8>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out, per_range);
+    case 16: return (int)launch_plain<16>(nt, g, threads, s, kp, vp, slab_stride, range_bytes, cpr, chunks, out, per_range);
     default: return (int)hipErrorInvalidValue;
   }
 }
