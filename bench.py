@@ -604,6 +604,8 @@ EXTRA_WORKLOADS = {
                    "rotated) read with the split kernel's access pattern and nothing else",
     "plain-read": "plain-read: the decode-32k K/V bytes (134 MB per launch, 4 layer caches "
                   "rotated) read by a grid-stride kernel, the fastest of several launch shapes",
+    "launch-gap": "launch-gap: back-to-back launches of an empty kernel (one store per "
+                  "workgroup) with the decode's split and merge grids: the per-kernel floor",
     "mfma-ceiling": "mfma-ceiling: 256 x 512-thread workgroups of 16x16x32 fp16 MFMAs only, "
                     "v_exp_f32 only (one per two MFMAs, the prefill's ratio), both, v_fma_f32 "
                     "only (one per MFMA) and MFMAs with FMAs",
@@ -932,6 +934,38 @@ def run_plain_read(torch, nw, launches: int):
     return res
 
 
+def run_launch_gap(torch, launches: int = 512):
+    """What a kernel boundary costs on the GPU (csrc/bench/nwd_stream_read.hip,
+    empty_kernel): `launches` launches of a kernel whose workgroups only
+    store one int, back to back in a HIP graph and as calls, with the decode
+    split kernel's grid (192 x 256 threads), the merge's (32 x 64) and one
+    workgroup. The graph figure is the per-launch floor of each kernel of a
+    decode call (split, then merge)."""
+    lib = ctypes.CDLL(str(BENCH_LIB))
+    lib.nwd_bench_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    sink = torch.empty(256, dtype=torch.int32, device="cuda")
+    log(f"[bench] launch-gap: {launches} empty launches per shape")
+
+    class Empty:
+        def __init__(self, wgs, threads):
+            self.shape = (wgs, threads)
+
+        def step(self, s, stream, append=True):
+            rc = lib.nwd_bench_empty(self.shape[0], self.shape[1], sink.data_ptr(), stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"nwd_bench_empty: hip error {rc}")
+
+    res = {"workload": "launch-gap", "desc": EXTRA_WORKLOADS["launch-gap"]}
+    for name, shape in (("split_grid_192x256", (192, 256)), ("merge_grid_32x64", (32, 64)),
+                        ("one_workgroup", (1, 64))):
+        _, ms = time_graph(torch, Empty(*shape), launches, 16, reps=3)
+        ms_calls = time_eager(torch, Empty(*shape), launches, reps=3)
+        res[name] = {"graph_us_per_launch": ms * 1e3 / launches,
+                     "calls_us_per_launch": ms_calls * 1e3 / launches}
+    log(f"[bench] launch-gap: {rounded(res)}")
+    return res
+
+
 def run_mfma_ceiling(torch, iters: int = 2048, launches: int = 5):
     """The matrix-core ceiling under load and how much of the prefill's
     exponential work hides under its MFMAs (csrc/bench/nwd_mfma_ceiling.hip):
@@ -1125,6 +1159,8 @@ def main():
             r = run_plain_read(torch, nw, args.steps)
         elif w == "mfma-ceiling":
             r = run_mfma_ceiling(torch)
+        elif w == "launch-gap":
+            r = run_launch_gap(torch)
         else:
             r = run_q4(torch, nw, w, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         print(json.dumps(rounded(r)), flush=True)
@@ -1153,6 +1189,7 @@ def main():
         configs["node-layer"] = node_layer
     stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
     plain = run_plain_read(torch, nw, SECONDARY_STEPS["plain-read"])
+    gap = run_launch_gap(torch)
     ceiling = run_mfma_ceiling(torch)
     for k in ("prefill-512", "prefill-512-f32q"):
         pre = configs[k]["roofline"]
@@ -1225,6 +1262,7 @@ def main():
                     for k, v in configs.items()},
         "stream_read": rounded(stream),
         "plain_read": rounded(plain),
+        "launch_gap": rounded(gap),
         "mfma_ceiling": rounded(ceiling),
         "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(head["wall_s"], 4),

@@ -169,3 +169,23 @@ extern "C" int nwd_bench_plain_read(const void* k, const void* v, int slabs, int
     default: return (int)hipErrorInvalidValue;
   }
 }
+
+// ---------------------------------------------------------------------------
+// The cost of a kernel launch itself: a kernel whose workgroups do nothing
+// but one store per workgroup, launched back to back. Its time per launch in
+// a HIP graph is the dispatch-to-dispatch floor any kernel boundary pays
+// (end of the previous kernel, cache release, dispatch of the next).
+namespace {
+__global__ void empty_kernel(int* __restrict__ sink) {
+  if (threadIdx.x == 0 && sink) sink[blockIdx.x] = (int)blockIdx.x;
+}
+}  // namespace
+
+// `workgroups` workgroups of `threads` threads; sink (optional) needs
+// `workgroups` ints. Returns a hipError_t code.
+extern "C" int nwd_bench_empty(int workgroups, int threads, int* sink, void* stream) {
+  if (workgroups < 1 || threads < 64 || threads > 1024 || threads % 64 != 0)
+    return (int)hipErrorInvalidValue;
+  empty_kernel<<<workgroups, threads, 0, (hipStream_t)stream>>>(sink);
+  return (int)hipGetLastError();
+}
