@@ -93,8 +93,8 @@ void nwd_destroy(nwd_ctx* ctx);
 const char* nwd_last_error(const nwd_ctx* ctx);
 
 /* SHA-256 (hex) of the sources this library was built from: every file under
- * csrc/ (its .hip and .h files, in name order, each as its relative path,
- * a NUL, its bytes) and include/nwd_attn.h. A provenance check with no
+ * csrc/ (its .hip and .h files, not those of csrc/bench/, in name order,
+ * each as its relative path, a NUL, its bytes) and include/nwd_attn.h. A provenance check with no
  * counterpart in the reference: a host compares it with the sources on disk
  * to know that the library it loaded is the one those sources build. */
 const char* nwd_source_hash(void);

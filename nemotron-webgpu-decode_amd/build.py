@@ -65,9 +65,10 @@ ASAN_HOST_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omi
 
 
 def source_files() -> list:
-    """The files nwd_source_hash covers: csrc/**/*.hip and *.h in name
-    order, then include/nwd_attn.h."""
-    files = sorted(p for p in CSRC.rglob("*") if p.suffix in (".hip", ".h"))
+    """The files nwd_source_hash covers, those libnwd_attn.so is built from:
+    csrc/*.hip and *.h in name order, then include/nwd_attn.h (the measurement
+    kernels under csrc/bench/ go to another library)."""
+    files = sorted(p for p in CSRC.glob("*") if p.suffix in (".hip", ".h"))
     return files + [INCLUDE / "nwd_attn.h"]
 
 
