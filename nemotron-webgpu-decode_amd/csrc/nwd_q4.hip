@@ -192,17 +192,19 @@ __global__ __launch_bounds__(kQ4Threads) void q4_gemv_kernel(const float* __rest
   Q4Part<kSplit> pt(n_blocks);
   const int col0 = pt.col0;
   if (kSplit == 1 && col0 >= m.n) return;  // whole wavefront (no barrier follows)
+  float* yb = y + (int64_t)b * m.n;
+  // The residual is requested with the weights, not after the reduction,
+  // where it would add a dependent memory round trip to the chain.
+  float prev[kQ4Cols];
+  if constexpr (kEpi == kQ4Accumulate) {
+#pragma unroll
+    for (int c = 0; c < kQ4Cols; ++c) prev[c] = yb[min(col0 + c, m.n - 1)];
+  }
   Q4Act<kSlots> a;
   q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, pt.first, pt.end, a);
   float r[kQ4Cols];
   q4_columns<kSlots>(m, n_blocks, pt.first, pt.end, col0, a, r);
   if (!pt.reduce(r) || col0 >= m.n) return;
-  float* yb = y + (int64_t)b * m.n;
-  float prev[kQ4Cols];
-  if constexpr (kEpi == kQ4Accumulate) {
-#pragma unroll
-    for (int c = 0; c < kQ4Cols; ++c) prev[c] = col0 + c < m.n ? yb[col0 + c] : 0.f;
-  }
 #pragma unroll
   for (int c = 0; c < kQ4Cols; ++c) {
     float v = r[c];
@@ -425,6 +427,7 @@ __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
     }
   }
   const Q4Mat& m = which == 0 ? mq : (which == 1 ? mk : mv);
+  const int p = which == 0 ? 0 : pos[b];  // requested before the weights, as the residual above
   Q4Act<kSlots> a;
   q4_load_act<kSlots>(x + (int64_t)b * n_blocks * 32, pt.first, pt.end, a);
   float r[kQ4Cols];
@@ -445,7 +448,6 @@ __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
   // kv_append (kernels/kv_append.wgsl:12-18) of this row's 4 values, rounded
   // to fp16, at position pos[b]; a position outside the cache writes nothing
   // and is reported through the status word.
-  const int p = pos[b];
   if (p < 0 || p >= cap) {
     if (col0 == 0) atomicOr(status, kStatusBadPos);  // once per projection
     return;
