@@ -296,6 +296,58 @@ class Q4LayerWorkload:
         return self.weight_bytes + self.io_bytes
 
 
+class GeneralWorkload:
+    """Decode-only calls on a shape of the general kernels (nwd_general.hip):
+    `layers` caches of `past` random fp16 tokens (rotated so the K/V reads
+    come from HBM), one fp16 query per call attending all `past` keys."""
+
+    def __init__(self, torch, nw, heads: int, kv_heads: int, head_dim: int, past: int,
+                 layers: int = 8, seed: int = 7):
+        self.heads, self.kv_heads, self.head_dim, self.past = heads, kv_heads, head_dim, past
+        self.layers = layers
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+
+        def rnd(*shape):
+            return torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32).to(torch.float16)
+
+        self.kc = [rnd(1, kv_heads, past, head_dim) for _ in range(layers)]
+        self.vc = [rnd(1, kv_heads, past, head_dim) for _ in range(layers)]
+        self.q = rnd(1, heads, head_dim)
+        self.out = torch.empty(1, heads, head_dim, dtype=torch.float16, device="cuda")
+        self.pos = torch.tensor([past - 1], dtype=torch.int32, device="cuda")
+        self.ctx = nw.AttnContext(heads, kv_heads, past, head_dim=head_dim)
+
+    def step(self, s: int, stream, append=False):
+        layer = s % self.layers
+        self.ctx.decode(self.q, self.kc[layer], self.vc[layer], self.pos, self.out, 1, self.past,
+                        stream)
+
+    def kv_bytes(self) -> int:
+        return self.past * self.kv_heads * self.head_dim * 2 * 2
+
+
+def run_general(torch, nw, steps: int = 128, warmup: int = 8):
+    """The general-shape kernels on three head layouts the kernels built for
+    head_dim 128 with groups 1/2/4/5/8 do not cover: us per decode call
+    (graph-replayed), K/V GB/s and the fraction of the HBM peak."""
+    res = {}
+    for name, (heads, kv_heads, head_dim, past, desc) in GENERAL_SHAPES.items():
+        log(f"[bench] {name}: {heads}q/{kv_heads}kv/d{head_dim}, {past} keys, {steps} calls")
+        wl = GeneralWorkload(torch, nw, heads, kv_heads, head_dim, past)
+        warm_up(torch, wl, 0.1, append=False)
+        _, ms = time_graph(torch, wl, steps, warmup, append=False, reps=3)
+        us = ms * 1e3 / steps
+        gbs = wl.kv_bytes() / (us * 1e-6) / 1e9
+        res[name] = {"desc": desc, "us_per_call": us, "kv_bytes": wl.kv_bytes(), "gbs": gbs,
+                     "hbm_frac": gbs / HBM_PEAK_GBS, "splits": wl.ctx.decode_splits(1, past)}
+        log(f"[bench] {name}: {res[name]}")
+        wl.ctx.close()
+        del wl
+        torch.cuda.empty_cache()
+    return res
+
+
 def q4_cpu_baseline(kind: str, budget_s: float = 10.0):
     """The oracle's restatement of kernels/matmul_nbits_sg.wgsl on the host's
     cores for one layer's projections of the same shapes (random weights)."""
@@ -618,6 +670,17 @@ EXTRA_WORKLOADS = {
 }
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
+# Shapes of the general-shape kernels (nwd_general.hip), decode-only, B = 1:
+# name: (n_heads, n_kv_heads, head_dim, keys, description)
+GENERAL_SHAPES = {
+    "general-g7-32k": (28, 4, 128, 32768, "B=1, 28q/4kv/d128 (group 7: the Qwen2.5-7B head "
+                       "layout), 32768 keys, fp16 I/O, decode call"),
+    "general-d256-8k": (16, 8, 256, 8192, "B=1, 16q/8kv/d256 (group 2, head size 256: the "
+                        "Gemma-2-9B layout), 8192 keys, fp16 I/O, decode call"),
+    "general-d96-4k": (32, 32, 96, 4096, "B=1, 32q/32kv/d96 (group 1, head size 96: the "
+                       "Phi-3-mini layout), 4096 keys, fp16 I/O, decode call"),
+}
+
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,
                    "decode-153": 1024, "ragged-64": 64,
                    "prefill-512": 32, "stream-read": 64, "plain-read": 64,
@@ -1119,7 +1182,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=16)
-    ap.add_argument("--workload", choices=["all"] + sorted(WORKLOADS) + sorted(EXTRA_WORKLOADS),
+    ap.add_argument("--workload", choices=["all", "general"] + sorted(WORKLOADS) + sorted(EXTRA_WORKLOADS),
                     default="all", help="all (default): the headline and every configuration; "
                     "a name: that workload alone (profiling)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -1161,6 +1224,8 @@ def main():
             r = run_mfma_ceiling(torch)
         elif w == "launch-gap":
             r = run_launch_gap(torch)
+        elif w == "general":
+            r = run_general(torch, nw)
         else:
             r = run_q4(torch, nw, w, args.steps, args.warmup, cpu=not args.no_cpu_baseline)
         print(json.dumps(rounded(r)), flush=True)
@@ -1187,6 +1252,7 @@ def main():
     node_layer = run_node_layer()
     if node_layer is not None:
         configs["node-layer"] = node_layer
+    general = run_general(torch, nw)
     stream = run_stream_read(torch, nw, SECONDARY_STEPS["stream-read"])
     plain = run_plain_read(torch, nw, SECONDARY_STEPS["plain-read"])
     gap = run_launch_gap(torch)
@@ -1263,6 +1329,7 @@ def main():
         "stream_read": rounded(stream),
         "plain_read": rounded(plain),
         "launch_gap": rounded(gap),
+        "general_shapes": rounded(general),
         "mfma_ceiling": rounded(ceiling),
         "device_copy_gbs": copy_gbs,
         "wall_s_timed": round(head["wall_s"], 4),

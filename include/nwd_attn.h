@@ -64,9 +64,14 @@ enum { NWD_F32 = 0, NWD_F16 = 1 };
 typedef struct nwd_desc {
   int32_t n_heads;     /* H, query heads (32 in the benchmark shapes, 40 in
                           the Nano-4B model, engine/config.js:10)           */
-  int32_t n_kv_heads;  /* Hkv; H must be a multiple of Hkv and the group
-                          H/Hkv one of 1, 2, 4, 5, 8 (sparse_attn.wgsl:38)  */
-  int32_t head_dim;    /* D; 128 (engine/config.js:12)                      */
+  int32_t n_kv_heads;  /* Hkv; H must be a multiple of Hkv, any group
+                          G = H/Hkv (sparse_attn.wgsl:38-39)                */
+  int32_t head_dim;    /* D, 1 .. 512 (128 in engine/config.js:12). D = 128
+                          with G one of 1, 2, 4, 5, 8 runs the kernels built
+                          for those shapes; every other (D, G) the general
+                          kernels, with the same contract and cache layout
+                          (one workgroup per output row, K/V re-read per
+                          query head: a coverage path, not a fast one)       */
   int32_t max_seq;     /* cache capacity in tokens per sequence, at most
                           4194304 (2^22)                                    */
   int32_t max_batch;   /* sequences per call                                */
@@ -181,7 +186,10 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * accumulation: an fp16 q enters exact and its scores are scaled in fp32;
  * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
  * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
- * makes nwd_device_status report NWD_ERR_DEVICE. max_len bounds
+ * makes nwd_device_status report NWD_ERR_DEVICE. The general shapes (see
+ * nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
+ * outside the cache (pos0[b] < 0 or pos0[b] + n_new > max_seq) is flagged in
+ * the device status and run at the nearest valid pos0. max_len bounds
  * pos0[b] + n_new (0 means max_seq). */
 int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache,
                      const void* v_cache, const int32_t* pos0, void* out,
@@ -200,8 +208,9 @@ int nwd_device_status(nwd_ctx* ctx, void* stream);
 int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len);
 
 /* Overrides the split count chosen by nwd_decode_attn (0 restores the
- * automatic choice). Values are clamped to [1, 256]. Results do not depend on
- * it beyond fp32 reordering. */
+ * automatic choice); on the general shapes (see nwd_desc.head_dim) it also
+ * sets nwd_prefill_attn's. Values are clamped to [1, 256]. Results do not
+ * depend on it beyond fp32 reordering. */
 int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 
 /* Chooses where split-K records are merged: 1 in a separate merge kernel
@@ -210,7 +219,8 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * last workgroup of each (sequence, kv head) to finish (of each (sequence,
  * query head) when the call runs one workgroup per query head); negative restores the
  * default, the separate kernel (measured faster on MI355X at 4K and 32K
- * keys). Same results, bit for bit. */
+ * keys). Same results, bit for bit. The general shapes always use the
+ * separate merge; this and the two knobs below do not apply to them. */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
 /* Chooses the split kernel of later decode calls (the workgroup form of
@@ -290,7 +300,9 @@ int nwd_q4_gemv(nwd_ctx* ctx, const float* a, const nwd_q4_weight* w, float* y,
  * input of nwd_decode_attn); the new k and v rows are rounded to fp16 (to
  * nearest even, as nwd_kv_append does) into the caches at pos[b]. A position
  * outside [0, max_seq) writes no cache row and sets the device status
- * (nwd_device_status). batch <= max_batch. */
+ * (nwd_device_status). batch <= max_batch. head_dim must be a multiple of 4
+ * and n_heads * head_dim, n_kv_heads * head_dim multiples of 16 (a
+ * workgroup's 16 columns lie in one of q, k, v); else NWD_ERR_UNSUPPORTED. */
 int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq,
                    const nwd_q4_weight* wk, const nwd_q4_weight* wv, void* q_out,
                    void* k_cache, void* v_cache, const int32_t* pos, int32_t batch,

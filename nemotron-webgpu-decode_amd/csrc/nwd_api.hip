@@ -39,6 +39,7 @@ struct nwd_ctx {
   void* ev_start;      // hipEvent_t pair recorded around decode split kernels, or NULL
   void* ev_stop;
   int* status_host;    // pinned copy target of the device status word
+  int64_t o_floats;    // floats allocated for ws.part_o
   std::string err;
 };
 
@@ -71,8 +72,6 @@ int fail(nwd_ctx* ctx, int code, const char* fmt, ...) {
 int hip_fail(nwd_ctx* ctx, const char* what, hipError_t e) {
   return fail(ctx, NWD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
-
-bool group_supported(int g) { return g == 1 || g == 2 || g == 4 || g == 5 || g == 8; }
 
 int resolve_len(const nwd_ctx* ctx, int32_t max_len) {
   return max_len <= 0 ? ctx->desc.max_seq : max_len;
@@ -138,6 +137,23 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   return n < 1 ? 1 : n;
 }
 
+// Split count of the general-shape kernels (nwd_general.hip: one workgroup
+// per split and `units` (sequence, query, KV head, head chunk)): about 1024
+// workgroups when the units alone are fewer, with at least 256 keys per split.
+int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
+  const int gp = nwd::general_heads_per_workgroup(s.head_dim, s.group);
+  return (int64_t)batch * n_new * s.n_kv * ((s.group + gp - 1) / gp);
+}
+
+int general_splits(int64_t units, int max_len) {
+  if (units >= 1024) return 1;
+  int n = (int)((1024 + units - 1) / units);
+  const int by_len = (max_len + 255) / 256;
+  if (n > by_len) n = by_len;
+  if (n > kMaxSplits) n = kMaxSplits;
+  return n < 1 ? 1 : n;
+}
+
 // Validates a descriptor (the checks nwd_create and the allocation-free
 // entry point share); failures name `who`.
 int check_desc(const nwd_desc* d, const char* who) {
@@ -151,13 +167,9 @@ int check_desc(const nwd_desc* d, const char* who) {
   if (d->n_heads % d->n_kv_heads != 0)
     return fail(nullptr, NWD_ERR_INVALID, "%s: n_heads %d is not a multiple of n_kv_heads %d",
                 who, d->n_heads, d->n_kv_heads);
-  const int group = d->n_heads / d->n_kv_heads;
-  if (!group_supported(group))
-    return fail(nullptr, NWD_ERR_UNSUPPORTED,
-                "%s: group size n_heads/n_kv_heads = %d is not one of 1, 2, 4, 5, 8", who, group);
-  if (d->head_dim != nwd::kHeadDim)
-    return fail(nullptr, NWD_ERR_UNSUPPORTED, "%s: head_dim %d is not supported (only 128)", who,
-                d->head_dim);
+  if (d->head_dim > nwd::kMaxHeadDim)
+    return fail(nullptr, NWD_ERR_UNSUPPORTED, "%s: head_dim %d exceeds %d", who, d->head_dim,
+                nwd::kMaxHeadDim);
   for (int t : {d->q_dtype, d->o_dtype, d->kv_dtype})
     if (t != NWD_F16 && t != NWD_F32)
       return fail(nullptr, NWD_ERR_INVALID, "%s: dtype %d is neither NWD_F16 nor NWD_F32", who, t);
@@ -185,6 +197,10 @@ nwd::Shape shape_of(const nwd_desc* d) {
   sh.o16 = d->o_dtype == NWD_F16;
   sh.kv16 = d->kv_dtype == NWD_F16;
   sh.qk_scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
+  sh.head_dim = d->head_dim;
+  // D = 128 with a group of 1, 2, 4, 5 or 8 runs the specialised kernels
+  // (nwd_decode.hip, nwd_prefill.hip); every other shape the general ones.
+  sh.general = d->head_dim != nwd::kHeadDim || !nwd::specialised_group(sh.group);
   return sh;
 }
 
@@ -209,12 +225,17 @@ int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
   return n < 1 ? 1 : n;
 }
 
-// Records the static scratch holds: a 256-byte status slot, then (m, l)
-// pairs and o[128] rows, each area 256-byte aligned.
-constexpr int64_t kScratchRecords = (int64_t)(kScratchBytes - 512) / (8 + nwd::kHeadDim * 4);
+// Records the static scratch holds for head size D: a 256-byte status
+// slot, then (m, l) pairs and o[D] rows, each area 256-byte aligned.
 constexpr size_t kScratchMlOffset = 256;
-constexpr size_t kScratchOOffset = kScratchMlOffset + ((kScratchRecords * 8 + 255) / 256) * 256;
-static_assert(kScratchOOffset + (size_t)kScratchRecords * nwd::kHeadDim * 4 <= kScratchBytes,
+constexpr int64_t scratch_records(int D) { return (int64_t)(kScratchBytes - 512) / (8 + D * 4); }
+constexpr size_t scratch_o_offset(int D) {
+  return kScratchMlOffset + (size_t)((scratch_records(D) * 8 + 255) / 256) * 256;
+}
+constexpr bool scratch_fits(int D) {
+  return scratch_o_offset(D) + (size_t)scratch_records(D) * D * 4 <= kScratchBytes;
+}
+static_assert(scratch_fits(1) && scratch_fits(nwd::kHeadDim) && scratch_fits(nwd::kMaxHeadDim),
               "records fit the scratch");
 
 constexpr int kMaxDevices = 64;
@@ -251,6 +272,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   *out_ctx = nullptr;
   if (int rc = check_desc(d, "nwd_create")) return rc;
   const int group = d->n_heads / d->n_kv_heads;
+  const int o_dim = d->head_dim > nwd::kHeadDim ? d->head_dim : nwd::kHeadDim;
 
   nwd_ctx* ctx = new nwd_ctx();
   ctx->desc = *d;
@@ -288,7 +310,10 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   // head) in the per-query-head form (at most kSubSplitMaxWorkgroups).
   size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
   if (n_counters < (size_t)nwd::kSubSplitMaxWorkgroups) n_counters = nwd::kSubSplitMaxWorkgroups;
-  e = hipMalloc(&ctx->ws.part_o, ctx->ws.records * nwd::kHeadDim * sizeof(float));
+  // o rows of max(D, 128) floats: the general kernels' records of D floats
+  // and the argmax records (which reuse part_o) both fit.
+  ctx->o_floats = ctx->ws.records * o_dim;
+  e = hipMalloc(&ctx->ws.part_o, ctx->o_floats * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
@@ -338,7 +363,8 @@ int64_t nwd_cache_offset(const nwd_ctx* ctx, int32_t b, int32_t t, int32_t h, in
   if (!ctx || b < 0 || b >= ctx->desc.max_batch || t < 0 || t >= ctx->desc.max_seq || h < 0 ||
       h >= ctx->desc.n_kv_heads || d < 0 || d >= ctx->desc.head_dim)
     return -1;
-  return nwd::cache_index(b, t, h, d, ctx->desc.n_kv_heads, ctx->desc.max_seq);
+  return nwd::cache_index_d(b, t, h, d, ctx->desc.n_kv_heads, ctx->desc.max_seq,
+                            ctx->desc.head_dim);
 }
 
 int nwd_kv_append(nwd_ctx* ctx, const void* k_new, const void* v_new, void* k_cache,
@@ -364,7 +390,8 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len) {
   int len = resolve_len(ctx, max_len);
   if (len > ctx->desc.max_seq) len = ctx->desc.max_seq;
   int n = ctx->forced_splits > 0 ? ctx->forced_splits
-                                 : auto_splits(ctx->desc.n_heads, ctx->desc.n_kv_heads, batch, len);
+          : ctx->shape.general     ? general_splits(general_units(ctx->shape, batch, 1), len)
+                                   : auto_splits(ctx->desc.n_heads, ctx->desc.n_kv_heads, batch, len);
   return clamp_splits(ctx, batch, n);
 }
 
@@ -388,6 +415,20 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   if (len > ctx->desc.max_seq)
     return fail(ctx, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
                 ctx->desc.max_seq);
+  if (ctx->shape.general) {
+    // General shapes: the append (if any) as its own launch, then the
+    // general attention kernel and its merge.
+    hipError_t e = hipSuccess;
+    if (k_new)
+      e = nwd::launch_kv_append(ctx->shape, k_new, v_new, k_cache, v_cache, pos, batch, 1,
+                                ctx->ws.status, (hipStream_t)stream);
+    if (e == hipSuccess)
+      e = nwd::launch_general_attn(ctx->shape, q, k_cache, v_cache, pos, out, batch, 1, 0, len,
+                                   nwd_decode_splits(ctx, batch, len), ctx->ws, ctx->ev_start,
+                                   ctx->ev_stop, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(ctx, who, e);
+    return NWD_OK;
+  }
   nwd::DecodeCall c;
   c.q = q;
   c.k_cache = k_cache;
@@ -443,21 +484,24 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   if (len > desc->max_seq)
     return fail(nullptr, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
                 desc->max_seq);
-  int n = auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
+  const nwd::Shape sh = shape_of(desc);
+  int n = sh.general ? general_splits(general_units(sh, batch, 1), len)
+                     : auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
   if (n > kMaxSplits) n = kMaxSplits;
   const int64_t records = n > 1 ? (int64_t)batch * desc->n_heads * n : 0;
-  if (records > kScratchRecords)
+  const int64_t have = scratch_records(desc->head_dim);
+  if (records > have)
     return fail(nullptr, NWD_ERR_CAPACITY,
                 "%s: %d sequences x %d heads x %d splits need %lld split records; the static "
-                "scratch holds %lld (%zu bytes)",
-                who, batch, desc->n_heads, n, (long long)records, (long long)kScratchRecords,
-                kScratchBytes);
+                "scratch holds %lld at head_dim %d (%zu bytes)",
+                who, batch, desc->n_heads, n, (long long)records, (long long)have,
+                desc->head_dim, kScratchBytes);
   unsigned char* base = nullptr;
   if (int rc = scratch_address(who, &base)) return rc;
   nwd::Workspace ws;
   ws.part_ml = reinterpret_cast<float2*>(base + kScratchMlOffset);
-  ws.part_o = reinterpret_cast<float*>(base + kScratchOOffset);
-  ws.records = kScratchRecords;
+  ws.part_o = reinterpret_cast<float*>(base + scratch_o_offset(desc->head_dim));
+  ws.records = have;
   ws.counters = nullptr;  // the separate merge kernel takes no arrival tickets
   ws.status = status ? status : reinterpret_cast<int*>(base);
   nwd::DecodeCall c;
@@ -476,7 +520,16 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   c.layout = default_layout(batch, len, n);
   c.ev_start = nullptr;
   c.ev_stop = nullptr;
-  hipError_t e = nwd::launch_decode(shape_of(desc), c, ws, (hipStream_t)stream);
+  hipError_t e = hipSuccess;
+  if (sh.general) {
+    e = nwd::launch_kv_append(sh, k_new, v_new, k_cache, v_cache, pos, batch, 1, ws.status,
+                              (hipStream_t)stream);
+    if (e == hipSuccess)
+      e = nwd::launch_general_attn(sh, q, k_cache, v_cache, pos, out, batch, 1, 0, len, n, ws,
+                                   nullptr, nullptr, (hipStream_t)stream);
+  } else {
+    e = nwd::launch_decode(sh, c, ws, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return fail(nullptr, NWD_ERR_HIP, "%s: %s", who, hipGetErrorString(e));
   return NWD_OK;
 }
@@ -528,8 +581,23 @@ int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const voi
   if (len > ctx->desc.max_seq || len < n_new)
     return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: max_len %d outside [n_new, max_seq=%d]",
                 len, ctx->desc.max_seq);
-  hipError_t e = nwd::launch_prefill(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new,
-                                     len, ctx->ws, (hipStream_t)stream);
+  hipError_t e;
+  if (ctx->shape.general) {
+    const int64_t rows = (int64_t)batch * n_new * ctx->desc.n_heads;
+    if (rows > 0x7FFFFFFF)
+      return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: %lld output rows exceed 2^31 - 1",
+                  (long long)rows);
+    int n = ctx->forced_splits > 0 ? ctx->forced_splits
+                                   : general_splits(general_units(ctx->shape, batch, n_new), len);
+    const int64_t fit = ctx->ws.records / rows;
+    if (n > fit) n = (int)fit;
+    if (n < 1) n = 1;
+    e = nwd::launch_general_attn(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new, 1, len,
+                                 n, ctx->ws, nullptr, nullptr, (hipStream_t)stream);
+  } else {
+    e = nwd::launch_prefill(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new, len,
+                            ctx->ws, (hipStream_t)stream);
+  }
   if (e == hipErrorNotSupported)
     return fail(ctx, NWD_ERR_UNSUPPORTED, "nwd_prefill_attn: this shape is not built");
   if (e != hipSuccess) return hip_fail(ctx, "nwd_prefill_attn: launch", e);
@@ -621,6 +689,13 @@ int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq, const 
                 wq->n_blocks, wk->n_blocks, wv->n_blocks);
   if (!x || !q_out || !k_cache || !v_cache || !pos)
     return fail(ctx, NWD_ERR_INVALID, "%s: null buffer", who);
+  // A workgroup's 16 columns must lie in one of the q, k, v ranges and a
+  // wavefront's 4 in one head.
+  if (ctx->desc.head_dim % 4 != 0 || dq % 16 != 0 || dkv % 16 != 0)
+    return fail(ctx, NWD_ERR_UNSUPPORTED,
+                "%s: head_dim %d needs n_heads * head_dim and n_kv_heads * head_dim to be "
+                "multiples of 16 and head_dim a multiple of 4",
+                who, ctx->desc.head_dim);
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(q_out) % 16 != 0)
     return fail(ctx, NWD_ERR_INVALID, "%s: x and q_out must be 16-byte aligned", who);
   if (batch < 1 || batch > ctx->desc.max_batch)
@@ -636,7 +711,7 @@ int nwd_qkv_append(nwd_ctx* ctx, const float* x, const nwd_q4_weight* wq, const 
 // The argmax records live in the split-K workspace (calls on a context are
 // stream-ordered, so they never overlap a decode's use of it).
 static unsigned long long* argmax_records(nwd_ctx* ctx, const char* who, int64_t count, int* rc) {
-  const int64_t have = ctx->ws.records * nwd::kHeadDim * (int64_t)sizeof(float) / 8;
+  const int64_t have = ctx->o_floats * (int64_t)sizeof(float) / 8;
   if (count > have) {
     *rc = fail(ctx, NWD_ERR_CAPACITY, "%s: %lld partial records exceed the workspace (%lld)", who,
                (long long)count, (long long)have);

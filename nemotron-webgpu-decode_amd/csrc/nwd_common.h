@@ -64,6 +64,11 @@ __host__ __device__ inline int64_t cache_index(int b, int t, int h, int d,
                                                int n_kv, int cap) {
   return ((int64_t)(b * n_kv + h) * cap + t) * kHeadDim + d;
 }
+// The same for a head size D known at run time (the general-shape kernels).
+__host__ __device__ inline int64_t cache_index_d(int b, int t, int h, int d, int n_kv, int cap,
+                                                 int D) {
+  return ((int64_t)(b * n_kv + h) * cap + t) * D + d;
+}
 
 // DPP lane moves inside a row of 16 lanes (data-parallel primitives, no LDS).
 template <int kCtrl>

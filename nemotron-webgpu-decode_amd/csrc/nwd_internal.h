@@ -16,7 +16,15 @@ struct Shape {
   int o16;         // O is fp16 (else fp32)
   int kv16;        // new K/V rows are fp16 (else fp32)
   float qk_scale;  // softmax scale (1/sqrt(D) by default)
+  int head_dim;    // D
+  int general;     // D or the group is outside the specialised kernels' set
 };
+
+// Head sizes the general-shape kernels take (sparse_attn.wgsl:12-17 takes
+// any; a row of q and the partial output stay in LDS).
+constexpr int kMaxHeadDim = 512;
+// Group sizes the specialised kernels are built for (D = 128).
+inline bool specialised_group(int g) { return g == 1 || g == 2 || g == 4 || g == 5 || g == 8; }
 
 // Split-K workspace owned by the context.
 struct Workspace {
@@ -71,6 +79,22 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
 // Largest decode split count supported for `batch` sequences by `ws`.
 int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
+// Query heads one general-shape workgroup serves (the same K/V rows read once
+// for all of them): up to 8 at D <= 128, 4 at D <= 256, 2 beyond, 1 when D
+// is not a multiple of 8; never more than the group.
+int general_heads_per_workgroup(int head_dim, int group);
+
+// Decode (prefill = 0, n_new = 1, pos = the newest token's index) or causal
+// prefill (prefill = 1, pos = pos0) of the general-shape kernels over rows
+// [batch][n_new][H]: one workgroup per split and chunk of a group's heads,
+// split-K records of D floats per row in ws, then a merge launch when
+// nsplit > 1. span bounds the keys from the host side and partitions the
+// splits.
+hipError_t launch_general_attn(const Shape& s, const void* q, const void* k_cache,
+                               const void* v_cache, const int32_t* pos, void* out, int batch,
+                               int n_new, int prefill, int span, int nsplit, const Workspace& ws,
+                               void* ev_start, void* ev_stop, hipStream_t stream);
+
 // One 4-bit projection [K -> n] in the reference's format (K = 32 * n_blocks).
 struct Q4Mat {
   const uint8_t* quant;   // [n][n_blocks][16]
@@ -91,7 +115,7 @@ hipError_t launch_q4_gemv(const float* x, const Q4Mat& w, int n_blocks, float* y
 
 // The attention layer's q/k/v projections of x [batch][K] with the new K/V
 // rows rounded to fp16 straight into the caches at pos[b] (q to q_out,
-// [batch][H][128] in the context's q dtype).
+// [batch][H][D] in the context's q dtype).
 hipError_t launch_qkv_append(const Shape& s, const float* x, const Q4Mat& wq, const Q4Mat& wk,
                              const Q4Mat& wv, int n_blocks, void* q_out, void* k_cache,
                              void* v_cache, const int32_t* pos, int batch, int* status,

@@ -406,14 +406,15 @@ __global__ __launch_bounds__(kQ4wThreads, 2) void q4w_argmax_kernel(
   }
 }
 
-// Columns [0, Nq) are q, [Nq, Nq + Nkv) k, [Nq + Nkv, Nq + 2 Nkv) v; every
-// range is a multiple of 128 (whole heads), so a workgroup's 16 columns lie
-// in one of them.
+// Columns [0, Nq) are q, [Nq, Nq + Nkv) k, [Nq + Nkv, Nq + 2 Nkv) v, with
+// Nq = H * D and Nkv = Hkv * D. The host accepts only shapes where both are
+// multiples of 16 and D of 4, so a workgroup's 16 columns lie in one range
+// and a wavefront's 4 in one head (at D = 128 always).
 template <int kSlots, int kSplit, bool kQ16>
 __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
     const float* __restrict__ x, const Q4Mat mq, const Q4Mat mk, const Q4Mat mv, int n_blocks,
     void* __restrict__ q_out, f16* __restrict__ k_cache, f16* __restrict__ v_cache,
-    const int32_t* __restrict__ pos, int n_kv, int cap, int* __restrict__ status) {
+    const int32_t* __restrict__ pos, int n_kv, int D, int cap, int* __restrict__ status) {
   const int b = blockIdx.y;
   Q4Part<kSplit> pt(n_blocks);
   int col0 = pt.col0;
@@ -456,8 +457,8 @@ __global__ __launch_bounds__(kQ4Threads) void qkv_append_kernel(
 #pragma unroll
   for (int c = 0; c < kQ4Cols; ++c) h[c] = (f16)r[c];
   f16* cache = which == 1 ? k_cache : v_cache;
-  const int64_t at = cache_index(b, p, col0 / kHeadDim, col0 % kHeadDim, n_kv, cap);
-  if (!in_bounds(at, kQ4Cols, (int64_t)gridDim.y * n_kv * cap * kHeadDim, status)) return;
+  const int64_t at = cache_index_d(b, p, col0 / D, col0 % D, n_kv, cap, D);
+  if (!in_bounds(at, kQ4Cols, (int64_t)gridDim.y * n_kv * cap * D, status)) return;
   *reinterpret_cast<f16x4*>(cache + at) = h;
 }
 
@@ -508,10 +509,10 @@ hipError_t launch_qkv_slots(const Shape& s, const float* x, const Q4Mat& wq, con
   f16* vc = static_cast<f16*>(v_cache);
   if (s.q16)
     qkv_append_kernel<kSlots, kSplit, true><<<grid, kQ4Threads, 0, stream>>>(
-        x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.cap, status);
+        x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.head_dim, s.cap, status);
   else
     qkv_append_kernel<kSlots, kSplit, false><<<grid, kQ4Threads, 0, stream>>>(
-        x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.cap, status);
+        x, wq, wk, wv, n_blocks, q_out, kc, vc, pos, s.n_kv, s.head_dim, s.cap, status);
   return hipGetLastError();
 }
 

@@ -54,8 +54,8 @@ static void cpu_checks() {
   };
   const Bad bad[] = {
       {0, 0, NWD_ERR_INVALID},           {1, -1, NWD_ERR_INVALID},
-      {0, 30, NWD_ERR_INVALID},          {0, 24, NWD_ERR_UNSUPPORTED},
-      {0, 96, NWD_ERR_UNSUPPORTED},      {2, 64, NWD_ERR_UNSUPPORTED},
+      {0, 30, NWD_ERR_INVALID},          {2, 0, NWD_ERR_INVALID},
+      {2, 513, NWD_ERR_UNSUPPORTED},
       {3, 0, NWD_ERR_INVALID},           {3, (1 << 22) + 1, NWD_ERR_UNSUPPORTED},
       {4, 0, NWD_ERR_INVALID},           {5, 7, NWD_ERR_INVALID},
   };
@@ -110,10 +110,10 @@ static void cpu_checks() {
          NWD_ERR_INVALID, "nwd_lm_head_argmax(NULL)", nullptr);
   // the allocation-free entry point validates its descriptor on the host
   nwd_desc d = make_desc(32, 8, 4096, 1);
-  d.n_heads = 24;
+  d.head_dim = 513;
   expect(nwd_append_decode_noalloc(&d, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                    nullptr, 1, 0, nullptr, nullptr),
-         NWD_ERR_UNSUPPORTED, "nwd_append_decode_noalloc(group 3)", nullptr);
+         NWD_ERR_UNSUPPORTED, "nwd_append_decode_noalloc(head_dim 513)", nullptr);
   expect(nwd_append_decode_noalloc(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                                    nullptr, 1, 0, nullptr, nullptr),
          NWD_ERR_INVALID, "nwd_append_decode_noalloc(NULL)", nullptr);
@@ -154,10 +154,13 @@ struct Q4 {
   }
 };
 
-// One context of group g through every entry point: batch 2, 512 positions.
-static void gpu_cycle(int group) {
-  const int hkv = 8, h = hkv * group, batch = 2, max_seq = 512, d = 128;
-  const nwd_desc desc = make_desc(h, hkv, max_seq, batch);
+// One context of group g and head size d through every entry point: batch
+// 2, 512 positions (d = 128 with groups 1, 2, 4, 5, 8 runs the specialised
+// kernels, the other shapes the general ones).
+static void gpu_cycle(int group, int d) {
+  const int hkv = 8, h = hkv * group, batch = 2, max_seq = 512;
+  nwd_desc desc = make_desc(h, hkv, max_seq, batch);
+  desc.head_dim = d;
   nwd_ctx* ctx = nullptr;
   expect(nwd_create(&desc, &ctx), NWD_OK, "nwd_create", nullptr);
   if (!ctx) return;
@@ -254,11 +257,12 @@ int main(int argc, char** argv) {
   std::printf("nwd_abi_asan: cpu checks: %d calls, %d failed\n", g_calls, g_failed);
   std::fflush(stdout);
   if (gpu) {
-    for (int g : {1, 2, 4, 5, 8}) {
+    const int shapes[][2] = {{1, 128}, {2, 128}, {4, 128}, {5, 128}, {8, 128}, {3, 96}, {2, 100}};
+    for (const auto& gd : shapes) {
       const int before = g_calls;
-      gpu_cycle(g);
-      std::printf("nwd_abi_asan: gpu cycle group %d: %d calls, %d failed so far\n", g,
-                  g_calls - before, g_failed);
+      gpu_cycle(gd[0], gd[1]);
+      std::printf("nwd_abi_asan: gpu cycle group %d head_dim %d: %d calls, %d failed so far\n",
+                  gd[0], gd[1], g_calls - before, g_failed);
       std::fflush(stdout);
     }
   }

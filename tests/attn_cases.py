@@ -47,9 +47,10 @@ def kv_rows(g: np.random.Generator, L: int, n_kv: int, head_scale=None, outlier_
 
 
 def to_cache(rows_per_seq, n_kv: int, cap: int) -> np.ndarray:
-    """List of [L_b][n_kv][D] fp16 -> head-major cache [B][n_kv][cap][D]."""
+    """List of [L_b][n_kv][D] fp16 -> head-major cache [B][n_kv][cap][D]
+    (D taken from the rows)."""
     B = len(rows_per_seq)
-    c = np.zeros((B, n_kv, cap, D), np.float16)
+    c = np.zeros((B, n_kv, cap, rows_per_seq[0].shape[2]), np.float16)
     for b, r in enumerate(rows_per_seq):
         c[b, :, : r.shape[0], :] = np.transpose(r, (1, 0, 2))
     return c

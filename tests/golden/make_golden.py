@@ -25,6 +25,13 @@ CASES = [
     ("mha_8q8kv_L1", 8, 8, 128, 1, 1003),          # one key: O == V[0]
     ("g8_8q1kv_L300", 8, 1, 128, 300, 1004),       # group 8, > 256 keys
     ("g2_4q2kv_L65", 4, 2, 128, 65, 1005),         # one past a 64-key tile
+    # shapes of the general kernels (any head size, any group)
+    ("g3_6q2kv_d96_L200", 6, 2, 96, 200, 1006),    # group 3, head_dim 96
+    ("d64_8q2kv_L129", 8, 2, 64, 129, 1007),       # head_dim 64
+    ("d100_3q3kv_L70", 3, 3, 100, 70, 1008),       # head_dim not a multiple of 8
+    ("d256_4q1kv_L90", 4, 1, 256, 90, 1009),       # head_dim 256
+    ("g7_7q1kv_d32_L33", 7, 1, 32, 33, 1010),      # group 7
+    ("d1_2q1kv_L5", 2, 1, 1, 5, 1011),             # head_dim 1
 ]
 
 

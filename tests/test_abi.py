@@ -39,9 +39,8 @@ def _desc(**kw):
     (dict(n_heads=0), nw.NWD_ERR_INVALID),
     (dict(n_kv_heads=-1), nw.NWD_ERR_INVALID),
     (dict(n_heads=30), nw.NWD_ERR_INVALID),          # not a multiple of 8
-    (dict(n_heads=24), nw.NWD_ERR_UNSUPPORTED),      # group 3
-    (dict(n_heads=96), nw.NWD_ERR_UNSUPPORTED),      # group 12
-    (dict(head_dim=64), nw.NWD_ERR_UNSUPPORTED),
+    (dict(head_dim=0), nw.NWD_ERR_INVALID),
+    (dict(head_dim=513), nw.NWD_ERR_UNSUPPORTED),    # past the general kernels' 512
     (dict(max_seq=0), nw.NWD_ERR_INVALID),
     (dict(max_seq=(1 << 22) + 1), nw.NWD_ERR_UNSUPPORTED),  # slab byte offsets need 31 bits
     (dict(max_batch=0), nw.NWD_ERR_INVALID),
@@ -88,3 +87,31 @@ def test_library_matches_the_sources_on_disk(lib):
     spec.loader.exec_module(build)
     assert nw.source_hash(lib) == build.source_hash(), "rebuild: python nemotron-webgpu-decode_amd/build.py"
     assert len(nw.source_hash(lib)) == 64
+
+
+@pytest.mark.parametrize("kw", [dict(n_heads=24), dict(n_heads=96), dict(head_dim=64),
+                                dict(head_dim=100), dict(head_dim=512), dict(n_heads=8, n_kv_heads=8,
+                                                                              head_dim=1)])
+def test_general_shapes_pass_validation(lib, kw):
+    """Any group (24/8 = 3, 96/8 = 12) and any head size up to 512 pass the
+    descriptor checks (the reference's Params take both,
+    kernels/sparse_attn.wgsl:12-17). nwd_create then gets as far as the
+    device: without a GPU it fails there, not on the shape."""
+    h = ctypes.c_void_p(1234)
+    rc = lib.nwd_create(ctypes.byref(_desc(**kw)), ctypes.byref(h))
+    assert rc not in (nw.NWD_ERR_INVALID, nw.NWD_ERR_UNSUPPORTED), lib.nwd_last_error(None)
+
+
+def test_noalloc_accepts_general_shapes(lib):
+    """The allocation-free entry point takes the general shapes too: its split
+    records (at most ~2048 of head_dim floats for them) always fit the 16 MiB
+    scratch, even at head_dim 512, so the call gets past every host check to
+    the device (which this container lacks)."""
+    p = ctypes.c_void_p(8)
+    for kw in (dict(head_dim=512, n_heads=64, n_kv_heads=8, max_batch=64),
+               dict(head_dim=64, n_heads=6, n_kv_heads=2, max_batch=1)):
+        d = _desc(max_seq=32768, **kw)
+        rc = lib.nwd_append_decode_noalloc(ctypes.byref(d), p, p, p, p, p, p, p, d.max_batch, 32768,
+                                           None, None)
+        assert rc not in (nw.NWD_ERR_INVALID, nw.NWD_ERR_UNSUPPORTED, nw.NWD_ERR_CAPACITY), \
+            lib.nwd_last_error(None)

@@ -190,9 +190,42 @@ def test_q4_checked_build_matches():
         _same(lambda c, i: c.argmax(logits, 50000, i, B), prod, chk, [ids])
 
 
+
+@pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1)])
+def test_general_checked_build_matches(Dh, H, Hkv):
+    """The general-shape kernels in the checked build: append, decode with
+    the workspace filled exactly (max_seq 64 gives H * 256 records, and 256
+    forced splits use them all, most with no key), append + decode, and a
+    split prefill; nothing flagged, the product build's bits."""
+    say("check build general", Dh, H, Hkv)
+    cap, B = 64, 1
+    prod, chk = _pair(H, Hkv, cap, head_dim=Dh, o_dtype="f32")
+    with prod, chk:
+        q = randn_f16((B, H, Dh), 31)
+        kc = randn_f16((B, Hkv, cap, Dh), 32)
+        vc = randn_f16((B, Hkv, cap, Dh), 33)
+        kn = randn_f16((B, 3, Hkv, Dh), 34)
+        vn = randn_f16((B, 3, Hkv, Dh), 35)
+        pos = pos_tensor([cap - 3])
+        out = torch.zeros((B, H, Dh), dtype=torch.float32, device="cuda")
+        _same(lambda c, k, v: c.kv_append(kn, vn, k, v, pos, B, 3), prod, chk, [kc, vc])
+        for c in (prod, chk):
+            c.set_decode_splits(256)
+        assert prod.decode_splits(B, cap) == 256
+        _same(lambda c, o: c.decode(q, kc, vc, pos, o, B), prod, chk, [out])
+        _same(lambda c, o, k, v: c.append_decode(q, kn[:, 0], vn[:, 0], k, v, pos, o, B), prod, chk,
+              [out, kc, vc])
+        for c in (prod, chk):
+            c.set_decode_splits(4)
+        n_new = 9
+        qp = randn_f16((B, n_new, H, Dh), 36)
+        op = torch.zeros((B, n_new, H, Dh), dtype=torch.float32, device="cuda")
+        _same(lambda c, o: c.prefill(qp, kc, vc, pos_tensor([20]), o, B, n_new), prod, chk, [op])
+
 def test_asan_host_driver_on_gpu():
     """Host code under AddressSanitizer, with the kernels running: one
-    context per group through every entry point, then released. Leak
+    context per group (and two general shapes) through every entry point,
+    then released. Leak
     checking is off here: the HIP runtime keeps allocations until exit."""
     if not ASAN_DRIVER.exists():
         pytest.fail(f"{ASAN_DRIVER} is missing: python nemotron-webgpu-decode_amd/build.py "
@@ -204,4 +237,7 @@ def test_asan_host_driver_on_gpu():
     print(res.stdout[-2000:], res.stderr[-4000:], flush=True)
     assert res.returncode == 0, res.stderr[-4000:]
     assert "AddressSanitizer" not in res.stderr
-    assert "gpu cycle group 8" in res.stdout and "0 failed so far" in res.stdout.splitlines()[-1]
+    assert "gpu cycle group 8 head_dim 128" in res.stdout
+    assert "gpu cycle group 3 head_dim 96" in res.stdout  # the general kernels' host paths
+    assert "gpu cycle group 2 head_dim 100" in res.stdout
+    assert "0 failed so far" in res.stdout.splitlines()[-1]

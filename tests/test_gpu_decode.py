@@ -31,7 +31,7 @@ def _gpu():
 
 def _decode(ctx, q, kc, vc, pos, batch, out_dtype=torch.float16, max_len=0):
     H = ctx.desc.n_heads
-    out = torch.empty((batch, H, D), dtype=out_dtype, device="cuda")
+    out = torch.empty((batch, H, ctx.desc.head_dim), dtype=out_dtype, device="cuda")
     ctx.decode(q, kc, vc, pos, out, batch, max_len)
     torch.cuda.synchronize()
     return out.float().cpu().numpy()
@@ -118,7 +118,7 @@ def test_golden_vectors():
         say("golden", name)
         H, Dq = q.shape
         L, Hkv, _ = k.shape
-        with nw.AttnContext(H, Hkv, L + 3, o_dtype="f32") as ctx:
+        with nw.AttnContext(H, Hkv, L + 3, head_dim=Dq, o_dtype="f32") as ctx:
             kc = dev(to_cache([k], Hkv, L + 3))
             vc = dev(to_cache([v], Hkv, L + 3))
             got = _decode(ctx, dev(q[None]), kc, vc, pos_tensor([L - 1]), 1, torch.float32)[0]

@@ -50,8 +50,9 @@ class DevQ4:
         return gemv_f64(a, self.quant, self.scales, self.zp)
 
 
-def _ctx(H=32, Hkv=8, cap=64, B=1, q="f32"):
-    return nw.AttnContext(H, Hkv, cap, max_batch=B, q_dtype=q, o_dtype="f32", kv_dtype="f32")
+def _ctx(H=32, Hkv=8, cap=64, B=1, q="f32", Dh=D):
+    return nw.AttnContext(H, Hkv, cap, head_dim=Dh, max_batch=B, q_dtype=q, o_dtype="f32",
+                          kv_dtype="f32")
 
 
 @pytest.mark.parametrize("n,n_blocks,batch", [
@@ -106,19 +107,22 @@ def _ulp_f16(x: np.ndarray) -> np.ndarray:
     return np.abs((np.nextafter(h, np.float16(np.inf)) - h).astype(np.float64))
 
 
-@pytest.mark.parametrize("H,Hkv,q", [(40, 8, "f32"), (32, 8, "f16"), (16, 4, "f32")])
-def test_qkv_append_matches_float64(H, Hkv, q):
-    say(f"qkv_append H={H} Hkv={Hkv} q={q}")
+@pytest.mark.parametrize("H,Hkv,q,Dh", [(40, 8, "f32", 128), (32, 8, "f16", 128), (16, 4, "f32", 128),
+                                        (12, 4, "f32", 64), (6, 2, "f16", 96)])
+def test_qkv_append_matches_float64(H, Hkv, q, Dh):
+    """Also at head sizes 64 and 96 (groups 3), the cache rows placed with
+    the context's head size."""
+    say(f"qkv_append H={H} Hkv={Hkv} q={q} D={Dh}")
     g = rng(400 + H)
     B, cap, nb = 2, 48, HIDDEN // 32
-    wq, wk, wv = DevQ4(g, H * D, nb), DevQ4(g, Hkv * D, nb), DevQ4(g, Hkv * D, nb)
+    wq, wk, wv = DevQ4(g, H * Dh, nb), DevQ4(g, Hkv * Dh, nb), DevQ4(g, Hkv * Dh, nb)
     x = g.standard_normal((B, HIDDEN)).astype(np.float32)
     pos = [5, cap - 1]
     canary = -7.5
-    with _ctx(H, Hkv, cap, B, q) as ctx:
-        kc = torch.full((B, Hkv, cap, D), canary, dtype=torch.float16, device="cuda")
+    with _ctx(H, Hkv, cap, B, q, Dh) as ctx:
+        kc = torch.full((B, Hkv, cap, Dh), canary, dtype=torch.float16, device="cuda")
         vc = kc.clone()
-        q_out = torch.empty((B, H, D), dtype=torch.float32 if q == "f32" else torch.float16,
+        q_out = torch.empty((B, H, Dh), dtype=torch.float32 if q == "f32" else torch.float16,
                             device="cuda")
         ctx.qkv_append(dev(x), wq.w, wk.w, wv.w, q_out, kc, vc, pos_tensor(pos), B)
         assert ctx.device_status() == nw.NWD_OK
@@ -217,3 +221,13 @@ def test_q4_host_validation():
                 call()
             assert e.value.code == code, (i, e.value)
         assert ctx.device_status() == nw.NWD_OK
+    # head size 100 with 2 KV heads: 200 k columns do not split into whole
+    # 16-column workgroups, so the fused projection refuses the shape
+    with _ctx(4, 2, 16, Dh=100) as ctx:
+        wq, wk = DevQ4(g, 400, 4), DevQ4(g, 200, 4)
+        buf = torch.zeros((1, 400), dtype=torch.float32, device="cuda")
+        kc = torch.zeros((1, 2, 16, 100), dtype=torch.float16, device="cuda")
+        x = torch.zeros((1, 128), dtype=torch.float32, device="cuda")
+        with pytest.raises(nw.NwdError) as e:
+            ctx.qkv_append(x, wq.w, wk.w, wk.w, buf, kc, kc, pos_tensor([0]), 1)
+        assert e.value.code == nw.NWD_ERR_UNSUPPORTED and "multiples of 16" in str(e.value)

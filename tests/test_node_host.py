@@ -34,7 +34,7 @@ def test_create_errors_are_thrown_with_the_library_message():
     out = _node("""
 const a = require('../lib/nwd_napi.node');
 const msgs = [];
-for (const d of [{nHeads: 30, nKvHeads: 8, maxSeq: 16}, {nHeads: 24, nKvHeads: 8, maxSeq: 16},
+for (const d of [{nHeads: 30, nKvHeads: 8, maxSeq: 16}, {nHeads: 24, nKvHeads: 8, headDim: 513, maxSeq: 16},
                  {nHeads: 32, nKvHeads: 8, maxSeq: 0}]) {
   try { a.create(d); msgs.push('no-throw'); } catch (e) { msgs.push(e.message); }
 }
@@ -47,7 +47,7 @@ console.log(JSON.stringify(msgs));
 """)
     m = json.loads(out)
     assert "not a multiple of n_kv_heads" in m[0]
-    assert "group size" in m[1]
+    assert "head_dim 513 exceeds 512" in m[1]
     assert "sizes must be positive" in m[2]
     assert m[3].startswith("decode:")
     assert m[4].startswith("q4Gemv:") and m[5].startswith("qkvAppend:")

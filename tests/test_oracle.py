@@ -124,7 +124,7 @@ def test_golden_vectors():
         assert max_abs(o64, want) < 1e-12, name
         assert max_abs(o32, want) < 1e-5, name
         n += 1
-    assert n == 5
+    assert n == 11  # 5 at head_dim 128, 6 of other head sizes and groups
 
 
 def test_special_cases():

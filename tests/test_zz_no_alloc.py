@@ -72,6 +72,48 @@ def test_noalloc_matches_context_entry_point():
         assert ctx.device_status() == nw.NWD_OK
 
 
+
+def test_noalloc_general_shape_matches_context_entry_point():
+    """The same on a shape of the general kernels (head_dim 96, group 3):
+    its records of 96 floats in the scratch, two calls in a row (the second
+    smaller), bit-identical to nwd_append_decode."""
+    H, Hkv, Dg, cap = 6, 2, 96, 4096
+    g = rng(910)
+    cases = [(2, [4000, 1500], 0), (1, [200], 256)]
+    with nw.AttnContext(H, Hkv, cap, head_dim=Dg, max_batch=2) as ctx:
+        desc = ctx.desc
+        status = torch.zeros(1, dtype=torch.int32, device="cuda")
+        for B, past, max_len in cases:
+            say(f"noalloc general B={B} past={past} splits={ctx.decode_splits(B, max_len)}")
+            rows = [[g.standard_normal((p, Hkv, Dg), dtype=np.float32).astype(np.float16)
+                     for _ in range(2)] for p in past]
+            q = g.standard_normal((B, H, Dg), dtype=np.float32).astype(np.float16)
+            kn, vn = (g.standard_normal((B, Hkv, Dg), dtype=np.float32).astype(np.float16)
+                      for _ in range(2))
+            res = []
+            for noalloc in (True, False):
+                kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+                vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+                out = torch.empty((B, H, Dg), dtype=torch.float16, device="cuda")
+                if noalloc:
+                    nw.append_decode_noalloc(desc, dev(q), dev(kn), dev(vn), kc, vc, pos_tensor(past),
+                                             out, B, max_len, status)
+                else:
+                    ctx.append_decode(dev(q), dev(kn), dev(vn), kc, vc, pos_tensor(past), out, B,
+                                      max_len)
+                torch.cuda.synchronize()
+                res.append((out, kc, vc))
+            assert int(status.item()) == 0
+            for a, b in zip(*res):
+                assert torch.equal(a, b), (B, past)
+            got = host(res[0][0]).astype(np.float32)
+            for b in range(B):
+                L = past[b] + 1
+                kk = f32(from_cache(host(res[0][1]), b, L))
+                vv = f32(from_cache(host(res[0][2]), b, L))
+                assert max_abs(got[b], oracle.sparse_attn_f32(f32(q[b]), kk, vv)) < 2e-3, b
+        assert ctx.device_status() == nw.NWD_OK
+
 def test_noalloc_rejects_calls_beyond_the_scratch():
     say("noalloc capacity check")
     H, Hkv, cap, B = 32, 8, 16384, 128
