@@ -13,23 +13,13 @@
 // A 256-thread workgroup serves one split of the keys of one (sequence,
 // query) for gp query heads of one group (gp = G up to 8 at D <= 128, up to
 // 4 at D <= 256, 2 beyond; one when D is not a multiple of 8), so the K/V
-// rows are read once for all of them. Keys go in tiles of 64:
-//   - scores: four threads per key, each dotting every fourth run of the key
-//     row (runs of 8 fp16 values when D is a multiple of 8, single values
-//     otherwise) with each head's query row, which sits in LDS pre-scaled by
-//     scale * log2(e) so that scores come out in log2 units; two lane
-//     exchanges add the four parts;
-//   - online softmax per head over the tile: wavefront w takes heads w and
-//     w + 4, one lane per key (tile maximum, weights, weight sum by lane
-//     exchanges), and publishes the weights and the rescale factor in LDS;
-//   - P.V: the threads form key groups of D / run threads, one run of dims
-//     each; group g accumulates keys g, g + groups, ... of every tile for
-//     every head, and the groups' partial outputs are added through LDS at
-//     the end.
-// A thread's K and V runs of a tile are requested together (V does not wait
-// for the scores), the first tile's before the query rows are staged, and
-// for D <= 256 each next tile's before the current tile is computed, so the
-// memory round trips overlap the work instead of adding to the chain.
+// rows are read once for all of them. With D a multiple of 8 each wavefront
+// walks its own 16-key tiles with its own online softmax per head (no
+// barrier in the key loop), requesting its next tile before computing the
+// current one, and the four wavefronts are merged at the end; other head
+// sizes run a scalar form in 64-key workgroup tiles. Scores are dotted with
+// query rows held in LDS, pre-scaled by scale * log2(e) so that they come out
+// in log2 units.
 //
 // Workgroups are dealt to the 8 XCDs round-robin in launch order. The launch
 // index is remapped so that each XCD takes a contiguous range of the work in
@@ -208,21 +198,42 @@ __device__ inline void finish_row(const GeneralArgs& a, int row, int split, floa
     a.part_ml[rec] = make_float2(m, l);
 }
 
+// Max / sum over the wavefront's 16 quads when the four lanes of each quad
+// hold the same value: the other quad of each 8 lanes, the other 8 of each
+// 16 (DPP), then the xor-16 and xor-32 exchanges. Each quad counts once.
+__device__ inline float max_quads(float x) {
+  x = fmaxf(x, dpp_mov<kDppHalfMirror>(x));
+  x = fmaxf(x, dpp_mov<kDppRowRor8>(x));
+  return max_xor32(max_xor16(x));
+}
+__device__ inline float sum_quads(float x) {
+  x += dpp_mov<kDppHalfMirror>(x);
+  x += dpp_mov<kDppRowRor8>(x);
+  return sum_xor32(sum_xor16(x));
+}
+
 // D a multiple of 8: runs of 8 fp16 values, up to GP query heads per
-// workgroup. KR bounds both the runs a score thread takes (ceil(D / 32)) and
-// the keys a P.V thread takes per tile (ceil(64 / groups)); kPrefetch: the
-// next tile's runs are requested while the current tile is computed (twice
-// the registers, taken for KR <= 8).
+// workgroup. Each wavefront walks its own 16-key tiles (keys t0 + 16 w,
+// then every 64th key on), with its own online softmax per head, so the key
+// loop has no workgroup barrier and no wavefront waits for another's loads;
+// the four wavefronts' (m, l, o) are merged once at the end. Per tile: four
+// lanes per key dot every fourth run with each head's query row (LDS), a
+// quad sum and the 16-key maximum and weight sum by DPP and lane-swap
+// exchanges; the weights go through the wavefront's own LDS slots to the
+// P.V lanes, which form 64 / (D / 8) key groups of D / 8 lanes, one run each.
+// KR bounds the runs a score lane takes (ceil(D / 32)) and the keys a P.V
+// lane takes per tile; kPrefetch: the wavefront's next tile is requested
+// before the current one is computed (twice the registers, taken for
+// KR <= 8).
 constexpr int kQsFloats = 1024;  // GP * D of every instantiation
+constexpr int kWaveKeys = 16;    // keys per wavefront tile
 template <int KR, int GP, bool kPrefetch, bool kQ16, bool kO16>
-__global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const GeneralArgs a) {
-  static_assert(GP <= 2 * kGenWaves && GP * KR * 32 <= kQsFloats, "heads per workgroup");
+__global__ __launch_bounds__(kGenThreads) void general_attn_wave_kernel(const GeneralArgs a) {
+  static_assert(GP * KR * 32 <= kQsFloats, "query rows of the workgroup's heads fit the LDS");
   __shared__ float qs[kQsFloats];
-  __shared__ float sc[GP][kGenKeys];
-  __shared__ float ps[GP][kGenKeys];
-  __shared__ float alpha_s[GP];
-  __shared__ float2 ml_s[GP];
-  __shared__ float opart[kGenThreads * 8];  // groups * D <= 256 * 8 floats
+  __shared__ float ps[kGenWaves][GP][kWaveKeys];
+  __shared__ float2 mls[GP][kGenWaves];
+  __shared__ float opart[kGenThreads * 8];  // 4 wavefronts x key groups x D <= 2048 floats
 
   GenWork w;
   if (!general_work(a, w)) return;
@@ -233,17 +244,17 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const Gen
   const f16* kb = a.k_cache + slab;
   const f16* vb = a.v_cache + slab;
   const int nr = D / 8;                       // runs per row, <= 64
-  const int kk = tid >> 2, qq = tid & 3;      // score role: key of the tile, quarter
-  const int groups = kGenThreads / nr;        // P.V key groups, >= 4
-  const int kg = tid / nr, u = tid - kg * nr;
-  const bool pv_on = kg < groups;
+  const int kk = lane >> 2, qq = lane & 3;    // score role: key of the tile, quarter
+  const int kgw = 64 / nr;                    // P.V key groups per wavefront, >= 1
+  const int kp = (kWaveKeys + kgw - 1) / kgw; // keys per P.V lane, <= KR
+  const int kg = lane / nr, u = lane - kg * nr;
+  const bool pv_on = kg < kgw;
 
   // Requests a tile's runs. Every load is unconditional, from an address
   // clamped into the key range and the row (keys past t1 read key t1 - 1,
-  // runs past the row its last run, idle P.V threads some row of the tile):
-  // a load whose value is selected against zero makes the compiler wait for
-  // it right away, which would serialise the prefetch. The uses below skip
-  // every such value.
+  // runs past the row its last run): a load whose value is selected against
+  // zero makes the compiler wait for it right away, which would serialise
+  // the prefetch. The uses below skip every such value.
   f16x8 kn[KR], vn[KR];
   auto request = [&](int ts) {
     const int64_t key = min(ts + kk, w.t1 - 1);
@@ -254,10 +265,13 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const Gen
     }
 #pragma unroll
     for (int i = 0; i < KR; ++i) {
-      const int64_t k = min(ts + kg + groups * i, w.t1 - 1);
-      vn[i] = *reinterpret_cast<const f16x8*>(vb + k * D + u * 8);
+      if (i < kp) {  // uniform
+        const int64_t k = min(ts + kg * kp + i, w.t1 - 1);
+        vn[i] = *reinterpret_cast<const f16x8*>(vb + k * D + u * 8);
+      }
     }
   };
+
   // The query rows (nm * D <= 1024 values, 4 per thread) are requested
   // first, then the first tile's runs, so that storing the query rows to LDS
   // waits for them alone (loads complete in order).
@@ -267,21 +281,23 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const Gen
 #pragma unroll
   for (int r = 0; r < kQsFloats / kGenThreads; ++r)
     qv[r] = load_q<kQ16>(a.q, q0 + min(tid + kGenThreads * r, nq - 1));
-  if (w.t0 < w.t1) request(w.t0);
+  const int first = w.t0 + kWaveKeys * wave;
+  if (first < w.t1) request(first);
 #pragma unroll
   for (int r = 0; r < kQsFloats / kGenThreads; ++r)
     if (tid + kGenThreads * r < nq) qs[tid + kGenThreads * r] = a.c * qv[r];
   __syncthreads();
 
-  // (m, l) of heads wave and wave + 4, held by that wavefront
-  float m_own[2] = {kNegBig, kNegBig}, l_own[2] = {0.f, 0.f};
-  float acc[GP][8];
+  float m[GP], l[GP], acc[GP][8];
 #pragma unroll
-  for (int g = 0; g < GP; ++g)
+  for (int g = 0; g < GP; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
 
-  for (int ts = w.t0; ts < w.t1; ts += kGenKeys) {
+  for (int ts = first; ts < w.t1; ts += kWaveKeys * kGenWaves) {
     f16x8 kc[KR], vc[KR];
     if constexpr (kPrefetch) {
 #pragma unroll
@@ -289,16 +305,16 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const Gen
         kc[i] = kn[i];
         vc[i] = vn[i];
       }
-      if (ts + kGenKeys < w.t1) request(ts + kGenKeys);
+      if (ts + kWaveKeys * kGenWaves < w.t1) request(ts + kWaveKeys * kGenWaves);
     } else {
-      if (ts != w.t0) request(ts);
+      if (ts != first) request(ts);
 #pragma unroll
       for (int i = 0; i < KR; ++i) {
         kc[i] = kn[i];
         vc[i] = vn[i];
       }
     }
-    // scores of this thread's key for every head
+    const bool valid = ts + kk < w.t1;
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
       if (g < nm) {
@@ -311,65 +327,62 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_vec_kernel(const Gen
             for (int e = 0; e < 8; ++e) dot = fmaf(qs[g * D + j * 8 + e], (float)kc[i][e], dot);
           }
         }
-        dot += __shfl_xor(dot, 1);
-        dot += __shfl_xor(dot, 2);
-        if (qq == 0) sc[g][kk] = dot;
-      }
-    }
-    __syncthreads();
-    // softmax: wavefront `wave` takes heads wave and wave + 4, lane = key
+        dot += dpp_mov<kDppQuadXor1>(dot);
+        dot += dpp_mov<kDppQuadXor2>(dot);
+        const float s = valid ? dot : kNegBig;
+        const float m_new = fmaxf(m[g], max_quads(s));
+        const float alpha = exp2f(m[g] - m_new);
+        const float p = valid ? exp2f(s - m_new) : 0.f;
+        l[g] = fmaf(l[g], alpha, sum_quads(p));
+        m[g] = m_new;
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + kGenWaves * r;
-      if (g < nm && g < GP) {
-        const bool kv = ts + lane < w.t1;
-        const float s = kv ? sc[g][lane] : kNegBig;
-        const float m_new = fmaxf(m_own[r], wave_max(s));
-        const float alpha = exp2f(m_own[r] - m_new);
-        const float p = kv ? exp2f(s - m_new) : 0.f;
-        ps[g][lane] = p;
-        l_own[r] = fmaf(l_own[r], alpha, wave_sum(p));
-        m_own[r] = m_new;
-        if (lane == 0) alpha_s[g] = alpha;
+        for (int e = 0; e < 8; ++e) acc[g][e] *= alpha;
+        if (qq == 0) ps[wave][g][kk] = p;
       }
     }
-    __syncthreads();
-    // P.V for every head
+    // The weights were written by this wavefront's own lanes: LDS serves a
+    // wavefront's accesses in order, so no barrier is needed.
+    __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
       if (g < nm) {
-        const float al = alpha_s[g];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[g][e] *= al;
 #pragma unroll
         for (int i = 0; i < KR; ++i) {
-          const int k = kg + groups * i;
-          if (pv_on && k < kGenKeys && ts + k < w.t1) {
-            const float p = ps[g][k];
+          const int k = kg * kp + i;
+          if (pv_on && i < kp && k < kWaveKeys && ts + k < w.t1) {
+            const float p = ps[wave][g][k];
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, (float)vc[i][e], acc[g][e]);
           }
         }
       }
     }
-    __syncthreads();  // sc, ps and alpha_s are rewritten by the next tile
+    __builtin_amdgcn_wave_barrier();  // this tile's reads before the next tile's writes
   }
+
+  // Merge the four wavefronts: per head, M = max m_w, L = sum l_w 2^(m_w - M),
+  // and each wavefront's partial outputs scaled by 2^(m_w - M).
   if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int g = wave + kGenWaves * r;
-      if (g < nm && g < GP) ml_s[g] = make_float2(m_own[r], l_own[r]);
-    }
+    for (int g = 0; g < GP; ++g)
+      if (g < nm) mls[g][wave] = make_float2(m[g], l[g]);
   }
-  __syncthreads();  // every head's (m, l) visible to all threads
+  __syncthreads();
 #pragma unroll
   for (int g = 0; g < GP; ++g) {
     if (g < nm) {
+      float M = mls[g][0].x;
+#pragma unroll
+      for (int v = 1; v < kGenWaves; ++v) M = fmaxf(M, mls[g][v].x);
+      float L = 0.f;
+#pragma unroll
+      for (int v = 0; v < kGenWaves; ++v) L = fmaf(mls[g][v].y, exp2f(mls[g][v].x - M), L);
+      const float f = exp2f(m[g] - M);
       if (pv_on) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) opart[kg * D + u * 8 + e] = acc[g][e];
+        for (int e = 0; e < 8; ++e) opart[(wave * kgw + kg) * D + u * 8 + e] = acc[g][e] * f;
       }
-      finish_row<kO16>(a, w.row0 + g, w.split, ml_s[g].x, ml_s[g].y, groups, opart);
+      finish_row<kO16>(a, w.row0 + g, w.split, M, L, kGenWaves * kgw, opart);
       __syncthreads();  // opart is rewritten for the next head
     }
   }
@@ -527,13 +540,13 @@ static hipError_t launch_attn(K kernel, const GeneralArgs& a, hipStream_t stream
 template <int KR, bool kPf, bool kQ16, bool kO16>
 static hipError_t launch_vec(const GeneralArgs& a, hipStream_t stream, void* ev_start,
                              void* ev_stop) {
-  if (a.gp <= 1) return launch_attn(general_attn_vec_kernel<KR, 1, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
-  if (a.gp <= 2) return launch_attn(general_attn_vec_kernel<KR, 2, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
+  if (a.gp <= 1) return launch_attn(general_attn_wave_kernel<KR, 1, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
+  if (a.gp <= 2) return launch_attn(general_attn_wave_kernel<KR, 2, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
   if constexpr (KR <= 8) {
-    if (a.gp <= 4) return launch_attn(general_attn_vec_kernel<KR, 4, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
+    if (a.gp <= 4) return launch_attn(general_attn_wave_kernel<KR, 4, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
   }
   if constexpr (KR <= 4) {
-    if (a.gp <= 8) return launch_attn(general_attn_vec_kernel<KR, 8, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
+    if (a.gp <= 8) return launch_attn(general_attn_wave_kernel<KR, 8, kPf, kQ16, kO16>, a, stream, ev_start, ev_stop);
   }
   return hipErrorInvalidValue;
 }
