@@ -5,10 +5,10 @@
 // LCG; inputs and attention outputs are written to <outDir> for the Python
 // parity test, which checks them against the oracle.
 //
-// usage: node check_attention.js <outDir> [heads kvHeads tokens maxSeq [chunks]]
+// usage: node check_attention.js <outDir> [heads kvHeads tokens maxSeq [chunks [headDim]]]
 // chunks (e.g. "37,64"): the first tokens go through chunked prefill in
 // chunks of these sizes, the rest one decode step each; the inputs are the
-// same either way.
+// same either way. headDim defaults to 128 (engine/config.js:12).
 const fs = require('fs');
 const path = require('path');
 const { AttentionSlice } = require('./attention_layer');
@@ -39,7 +39,7 @@ function main() {
   const kvHeads = Number(process.argv[4] || 8);
   const tokens = Number(process.argv[5] || 153);
   const maxSeq = Number(process.argv[6] || 256);
-  const headDim = 128;
+  const headDim = Number(process.argv[8] || 128);
   fs.mkdirSync(outDir, { recursive: true });
   const slice = new AttentionSlice({ heads, kvHeads, headDim, maxSeq });
   const chunks = (process.argv[7] || '').split(',').filter((x) => x).map(Number);

@@ -20,11 +20,12 @@ pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(shutil.which("node") is None, reason="node is not installed")]
 
 
-def _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks=""):
-    out = tmp_path / f"run_{heads}_{tokens}_{chunks.replace(',', '-')}"
-    print(f"node check_attention {heads}/{kv_heads} tokens={tokens} chunks={chunks}", flush=True)
+def _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks="", head_dim=128):
+    out = tmp_path / f"run_{heads}_{tokens}_{chunks.replace(',', '-')}_{head_dim}"
+    print(f"node check_attention {heads}/{kv_heads}/d{head_dim} tokens={tokens} chunks={chunks}",
+          flush=True)
     res = subprocess.run(["node", str(JS / "check_attention.js"), str(out), str(heads),
-                          str(kv_heads), str(tokens), str(max_seq), chunks],
+                          str(kv_heads), str(tokens), str(max_seq), chunks, str(head_dim)],
                          capture_output=True, text=True, timeout=180)
     assert res.returncode == 0, res.stdout + res.stderr
     man = json.loads((out / "manifest.json").read_text())
@@ -37,19 +38,24 @@ def _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks=""):
     return man, q, k, v, o
 
 
-@pytest.mark.parametrize("heads,kv_heads,tokens,max_seq,chunks", [
-    (40, 8, 153, 256, ""),
-    (32, 8, 256, 256, ""),
+@pytest.mark.parametrize("heads,kv_heads,tokens,max_seq,chunks,head_dim", [
+    (40, 8, 153, 256, "", 128),
+    (32, 8, 256, 256, "", 128),
     # a 101-token prompt as two prefill chunks, then decode steps
-    (40, 8, 153, 256, "37,64"),
+    (40, 8, 153, 256, "37,64", 128),
     # the whole capacity through prefill chunks, then both guards
-    (32, 8, 256, 256, "1,127,128"),
+    (32, 8, 256, 256, "1,127,128", 128),
+    # shapes of the general kernels: head size 96 with group 3, head size 64
+    # with group 3 through a prefill chunk first
+    (6, 2, 90, 128, "", 96),
+    (12, 4, 70, 96, "17,20", 64),
 ])
-def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, chunks):
+def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, chunks, head_dim):
     """Every token through the decode step, or the first ones through chunked
     prefill (query t of a chunk attends keys 0..t, the reference's result for
     a prompt run token by token)."""
-    man, q, k, v, o = _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks)
+    man, q, k, v, o = _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks, head_dim)
+    assert man["headDim"] == head_dim
     # the cache holds the f32 rows rounded to fp16 (kv_append's rule)
     kh = oracle.f16_to_f32(oracle.f32_to_f16(k))
     vh = oracle.f16_to_f32(oracle.f32_to_f16(v))
