@@ -138,17 +138,20 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 }
 
 // Split count of the general-shape kernels (nwd_general.hip: one workgroup
-// per split and `units` (sequence, query, KV head, head chunk)): about 1024
-// workgroups when the units alone are fewer, with at least 256 keys per split.
+// per split and `units` (sequence, query, KV head, head chunk)): about 512
+// workgroups when the units alone are fewer, with at least 128 keys per
+// split. Decode calls on MI355X, us at 1/2x, 1x, 2x this count: 28q/4kv/d128
+// at 32K keys 57.5 / 40.5 / 51.2 (128 splits), 16q/8kv/d256 at 8K 26.2 /
+// 24.4 / 26.7 (64), 32q/32kv/d96 at 4K 17.7 / 16.5 / 16.5 (16).
 int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
   const int gp = nwd::general_heads_per_workgroup(s.head_dim, s.group);
   return (int64_t)batch * n_new * s.n_kv * ((s.group + gp - 1) / gp);
 }
 
 int general_splits(int64_t units, int max_len) {
-  if (units >= 1024) return 1;
-  int n = (int)((1024 + units - 1) / units);
-  const int by_len = (max_len + 255) / 256;
+  if (units >= 512) return 1;
+  int n = (int)((512 + units - 1) / units);
+  const int by_len = (max_len + 127) / 128;
   if (n > by_len) n = by_len;
   if (n > kMaxSplits) n = kMaxSplits;
   return n < 1 ? 1 : n;

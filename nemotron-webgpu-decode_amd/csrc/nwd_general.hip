@@ -445,19 +445,21 @@ __global__ __launch_bounds__(kGenThreads) void general_attn_scalar_kernel(const 
   finish_row<kO16>(a, w.row0, w.split, m, l, groups, opart);
 }
 
-// One workgroup per row: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M),
-// M the largest m_s (split 0 always holds key 0, so M is finite; an empty
-// split's record is (kNegBig, 0, 0) and weighs nothing). The threads form
-// 256 / D split groups (one for D >= 256, where a thread takes dims d and
-// d + 256); each thread requests 16 records' values before adding them, so
-// the record reads overlap instead of costing a round trip per split, and
-// the split groups' sums are added through LDS.
+// One workgroup per row and 32 dims of it: out = sum_s o_s 2^(m_s - M) /
+// sum_s l_s 2^(m_s - M), M the largest m_s (split 0 always holds key 0, so M
+// is finite; an empty split's record is (kNegBig, 0, 0) and weighs nothing).
+// The 256 threads are 8 split groups of 32 dims; each thread requests 16
+// records' values before adding them (one batch up to 128 splits), so the
+// record reads overlap instead of costing a round trip per split, and the
+// split groups' sums are added through LDS.
 constexpr int kMergeBatch = 16;
+constexpr int kMergeDims = 32;
+constexpr int kMergeGroups = kGenThreads / kMergeDims;
 template <bool kO16>
 __global__ __launch_bounds__(kGenThreads) void general_merge_kernel(const GeneralArgs a) {
   __shared__ float wts[kGenThreads];
   __shared__ float red_max[kGenWaves], red_sum[kGenWaves];
-  __shared__ float part[kGenThreads];
+  __shared__ float part[kMergeGroups][kMergeDims];
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t r0 = (int64_t)row * a.nsplit;
   float2 ml = make_float2(kNegBig, 0.f);
@@ -478,46 +480,34 @@ __global__ __launch_bounds__(kGenThreads) void general_merge_kernel(const Genera
   for (int w = 0; w < kGenWaves; ++w) Lsum += red_sum[w];
 
   const int D = a.D;
-  const int SG = D >= kGenThreads ? 1 : kGenThreads / D;  // split groups
-  const int sg = D >= kGenThreads ? 0 : tid / D;
-  const int d = D >= kGenThreads ? tid : tid - sg * D;
-  const bool on = sg < SG && d < D;
-  const bool second = d + kGenThreads < D;
-  float o = 0.f, o2 = 0.f;
-  if (on) {
-    for (int s0 = sg; s0 < a.nsplit; s0 += SG * kMergeBatch) {
-      float v[kMergeBatch], v2[kMergeBatch];
+  const int sg = tid / kMergeDims, dl = tid - sg * kMergeDims;
+  const int d = blockIdx.y * kMergeDims + dl;
+  float o = 0.f;
+  if (d < D) {
+    for (int s0 = sg; s0 < a.nsplit; s0 += kMergeGroups * kMergeBatch) {
+      float v[kMergeBatch];
 #pragma unroll
       for (int i = 0; i < kMergeBatch; ++i) {
-        const int sp = s0 + SG * i;
+        const int sp = s0 + kMergeGroups * i;
         const int64_t at = (r0 + sp) * D + d;
         v[i] = sp < a.nsplit && in_bounds(at, 1, a.records * D, a.status) ? a.part_o[at] : 0.f;
-        v2[i] = second && sp < a.nsplit && in_bounds(at + kGenThreads, 1, a.records * D, a.status)
-                    ? a.part_o[at + kGenThreads]
-                    : 0.f;
       }
 #pragma unroll
       for (int i = 0; i < kMergeBatch; ++i) {
-        const int sp = s0 + SG * i;
-        const float w = sp < a.nsplit ? wts[sp] : 0.f;
-        o = fmaf(v[i], w, o);
-        o2 = fmaf(v2[i], w, o2);
+        const int sp = s0 + kMergeGroups * i;
+        o = fmaf(v[i], sp < a.nsplit ? wts[sp] : 0.f, o);
       }
     }
   }
-  if (SG > 1) {
-    if (on) part[sg * D + d] = o;
-    __syncthreads();
-    if (tid < D) {
-      o = 0.f;
-      for (int g = 0; g < SG; ++g) o += part[g * D + tid];
-    }
+  part[sg][dl] = o;
+  __syncthreads();
+  if (tid < kMergeDims && d < D) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < kMergeGroups; ++g) t += part[g][tid];
+    const int64_t oi = (int64_t)row * D + d;
+    if (in_bounds(oi, 1, (int64_t)gridDim.x * D, a.status)) store_o<kO16>(a.out, oi, t / Lsum);
   }
-  const int64_t base = (int64_t)row * D;
-  const int64_t size = (int64_t)gridDim.x * D;
-  if (tid < D && in_bounds(base + tid, 1, size, a.status)) store_o<kO16>(a.out, base + tid, o / Lsum);
-  if (second && in_bounds(base + tid + kGenThreads, 1, size, a.status))
-    store_o<kO16>(a.out, base + tid + kGenThreads, o2 / Lsum);
 }
 
 template <typename K>
@@ -567,7 +557,8 @@ static hipError_t launch_general_t(const GeneralArgs& a, int rows, hipStream_t s
     }
   }
   if (e != hipSuccess || a.nsplit == 1) return e;
-  general_merge_kernel<kO16><<<dim3((unsigned)rows), kGenThreads, 0, stream>>>(a);
+  general_merge_kernel<kO16><<<dim3((unsigned)rows, (unsigned)((a.D + kMergeDims - 1) / kMergeDims)),
+                                 kGenThreads, 0, stream>>>(a);
   return hipGetLastError();
 }
 
