@@ -328,9 +328,9 @@ class GeneralWorkload:
 
 
 def run_general(torch, nw, steps: int = 128, warmup: int = 8):
-    """The general-shape kernels on three head layouts the kernels built for
-    head_dim 128 with groups 1/2/4/5/8 do not cover: us per decode call
-    (graph-replayed), K/V GB/s and the fraction of the HBM peak."""
+    """Three head layouts the kernels built for head_dim 128 with groups
+    1/2/4/5/8 do not cover as they are: us per decode call (graph-replayed),
+    K/V GB/s and the fraction of the HBM peak."""
     res = {}
     for name, (heads, kv_heads, head_dim, past, desc) in GENERAL_SHAPES.items():
         log(f"[bench] {name}: {heads}q/{kv_heads}kv/d{head_dim}, {past} keys, {steps} calls")
@@ -670,11 +670,14 @@ EXTRA_WORKLOADS = {
 }
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
-# Shapes of the general-shape kernels (nwd_general.hip), decode-only, B = 1:
+# Head layouts outside the benchmark's (group 7 at head_dim 128 through the
+# padded-group decode, nwd_pad.hip; head sizes 256 and 96 on the general
+# kernels, nwd_general.hip), decode-only, B = 1:
 # name: (n_heads, n_kv_heads, head_dim, keys, description)
 GENERAL_SHAPES = {
     "general-g7-32k": (28, 4, 128, 32768, "B=1, 28q/4kv/d128 (group 7: the Qwen2.5-7B head "
-                       "layout), 32768 keys, fp16 I/O, decode call"),
+                       "layout, decoded as group 8 on padded query rows), 32768 keys, fp16 I/O, "
+                       "decode call"),
     "general-d256-8k": (16, 8, 256, 8192, "B=1, 16q/8kv/d256 (group 2, head size 256: the "
                         "Gemma-2-9B layout), 8192 keys, fp16 I/O, decode call"),
     "general-d96-4k": (32, 32, 96, 4096, "B=1, 32q/32kv/d96 (group 1, head size 96: the "

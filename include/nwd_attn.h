@@ -68,10 +68,12 @@ typedef struct nwd_desc {
                           G = H/Hkv (sparse_attn.wgsl:38-39)                */
   int32_t head_dim;    /* D, 1 .. 512 (128 in engine/config.js:12). D = 128
                           with G one of 1, 2, 4, 5, 8 runs the kernels built
-                          for those shapes; every other (D, G) the general
-                          kernels, with the same contract and cache layout
-                          (one workgroup per output row, K/V re-read per
-                          query head: a coverage path, not a fast one)       */
+                          for those shapes, and decodes with G = 3, 6, 7 run
+                          them as G = 4, 8, 8 on zero-padded query rows
+                          (buffers allocated by nwd_create); every other
+                          (D, G) runs the general kernels, with the same
+                          contract and cache layout (a coverage path, not
+                          tuned like the others)                             */
   int32_t max_seq;     /* cache capacity in tokens per sequence, at most
                           4194304 (2^22)                                    */
   int32_t max_batch;   /* sequences per call                                */

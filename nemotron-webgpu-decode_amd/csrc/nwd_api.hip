@@ -40,6 +40,8 @@ struct nwd_ctx {
   void* ev_stop;
   int* status_host;    // pinned copy target of the device status word
   int64_t o_floats;    // floats allocated for ws.part_o
+  void* q_pad;         // padded query / output rows of the padded-group decode
+  void* out_pad;       //   (groups 3, 6, 7 at D = 128), or NULL
   std::string err;
 };
 
@@ -139,10 +141,26 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 
 // Split count of the general-shape kernels (nwd_general.hip: one workgroup
 // per split and `units` (sequence, query, KV head, head chunk)): about 512
-// workgroups when the units alone are fewer, with at least 128 keys per
-// split. Decode calls on MI355X, us at 1/2x, 1x, 2x this count: 28q/4kv/d128
+// workgroups when the units alone are fewer, with at least 64 keys per split
+// (one 16-key tile per wavefront). Decode calls on MI355X, us at 1/2x, 1x, 2x this count: 28q/4kv/d128
 // at 32K keys 57.5 / 40.5 / 51.2 (128 splits), 16q/8kv/d256 at 8K 26.2 /
 // 24.4 / 26.7 (64), 32q/32kv/d96 at 4K 17.7 / 16.5 / 16.5 (16).
+// Decode calls at D = 128 with a group of 3, 6 or 7 run the kernels of
+// groups 4 / 8 on padded query rows (nwd_pad.hip), at every length: the two
+// copy launches cost less than the general kernels' longer chains. Decode
+// calls on MI355X, 28q/4kv (group 7): 9.2 against 22.3 us at 1024 keys,
+// 21.0 against 40.5 at 32768; 12q/2kv (group 6): 8.8 against 20.1 at 1024
+// keys, 17.3 at 32768; 24q/8kv (group 3): 10.0 against 14.0 at 1024 keys,
+// 28.2 at 32768. The allocation-free entry point, which has no padded
+// buffers, and the prefill use the general kernels.
+enum DecodeRoute { kRouteSpecialised = 0, kRoutePadded = 1, kRouteGeneral = 2 };
+
+DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
+  if (!s.general) return kRouteSpecialised;
+  if (have_pad && nwd::padded_group(s.group) > 0 && s.head_dim == nwd::kHeadDim) return kRoutePadded;
+  return kRouteGeneral;
+}
+
 int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
   const int gp = nwd::general_heads_per_workgroup(s.head_dim, s.group);
   return (int64_t)batch * n_new * s.n_kv * ((s.group + gp - 1) / gp);
@@ -151,7 +169,7 @@ int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
 int general_splits(int64_t units, int max_len) {
   if (units >= 512) return 1;
   int n = (int)((512 + units - 1) / units);
-  const int by_len = (max_len + 127) / 128;
+  const int by_len = (max_len + 63) / 64;
   if (n > by_len) n = by_len;
   if (n > kMaxSplits) n = kMaxSplits;
   return n < 1 ? 1 : n;
@@ -221,8 +239,8 @@ int default_layout(int batch, int max_len, int nsplit) {
   return batch >= 2 && nsplit > 1 ? 1 : 0;
 }
 
-int clamp_splits(const nwd_ctx* ctx, int batch, int n) {
-  int cap = nwd::max_decode_splits(ctx->shape, ctx->ws, batch);
+int clamp_splits(const nwd_ctx* ctx, const nwd::Shape& s, int batch, int n) {
+  int cap = nwd::max_decode_splits(s, ctx->ws, batch);
   if (cap > kMaxSplits) cap = kMaxSplits;
   if (n > cap) n = cap;
   return n < 1 ? 1 : n;
@@ -306,6 +324,8 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (prefill > ctx->ws.records) ctx->ws.records = prefill;
   ctx->ws.part_o = nullptr;
   ctx->ws.part_ml = nullptr;
+  ctx->q_pad = nullptr;
+  ctx->out_pad = nullptr;
   ctx->ws.status = nullptr;
   ctx->ws.counters = nullptr;
   ctx->status_host = nullptr;
@@ -320,6 +340,12 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
+  const int gp = nwd::padded_group(group);
+  if (e == hipSuccess && gp > 0 && d->head_dim == nwd::kHeadDim) {
+    const size_t bytes = (size_t)d->max_batch * d->n_kv_heads * gp * nwd::kHeadDim * sizeof(float);
+    e = hipMalloc(&ctx->q_pad, bytes);
+    if (e == hipSuccess) e = hipMalloc(&ctx->out_pad, bytes);
+  }
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.status, sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.status, 0, sizeof(int));
   // Pinned, so the per-step status read is one small DMA, not a staged copy.
@@ -342,6 +368,8 @@ void nwd_destroy(nwd_ctx* ctx) {
   if (ctx->ws.part_ml) (void)hipFree(ctx->ws.part_ml);
   if (ctx->ws.counters) (void)hipFree(ctx->ws.counters);
   if (ctx->ws.status) (void)hipFree(ctx->ws.status);
+  if (ctx->q_pad) (void)hipFree(ctx->q_pad);
+  if (ctx->out_pad) (void)hipFree(ctx->out_pad);
   if (ctx->status_host) (void)hipHostFree(ctx->status_host);
   if (prev >= 0) (void)hipSetDevice(prev);
   delete ctx;
@@ -392,10 +420,12 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len) {
   if (!ctx || batch < 1 || batch > ctx->desc.max_batch) return 0;
   int len = resolve_len(ctx, max_len);
   if (len > ctx->desc.max_seq) len = ctx->desc.max_seq;
+  const DecodeRoute route = decode_route(ctx->shape, ctx->q_pad != nullptr);
+  const nwd::Shape s = route == kRoutePadded ? nwd::padded_shape(ctx->shape) : ctx->shape;
   int n = ctx->forced_splits > 0 ? ctx->forced_splits
-          : ctx->shape.general     ? general_splits(general_units(ctx->shape, batch, 1), len)
-                                   : auto_splits(ctx->desc.n_heads, ctx->desc.n_kv_heads, batch, len);
-  return clamp_splits(ctx, batch, n);
+          : route == kRouteGeneral ? general_splits(general_units(s, batch, 1), len)
+                                   : auto_splits(s.n_heads, s.n_kv, batch, len);
+  return clamp_splits(ctx, s, batch, n);
 }
 
 int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits) {
@@ -418,7 +448,8 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   if (len > ctx->desc.max_seq)
     return fail(ctx, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
                 ctx->desc.max_seq);
-  if (ctx->shape.general) {
+  const DecodeRoute route = decode_route(ctx->shape, ctx->q_pad != nullptr);
+  if (route == kRouteGeneral) {
     // General shapes: the append (if any) as its own launch, then the
     // general attention kernel and its merge.
     hipError_t e = hipSuccess;
@@ -451,7 +482,10 @@ static int decode_common(nwd_ctx* ctx, const char* who, const void* q, const voi
   c.layout = ctx->decode_layout >= 0 ? ctx->decode_layout : default_layout(batch, len, c.nsplit);
   c.ev_start = ctx->ev_start;
   c.ev_stop = ctx->ev_stop;
-  hipError_t e = nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
+  hipError_t e = route == kRoutePadded
+                     ? nwd::launch_padded_decode(ctx->shape, c, ctx->ws, ctx->q_pad, ctx->out_pad,
+                                                 (hipStream_t)stream)
+                     : nwd::launch_decode(ctx->shape, c, ctx->ws, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(ctx, who, e);
   return NWD_OK;
 }

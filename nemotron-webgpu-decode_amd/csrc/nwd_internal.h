@@ -79,6 +79,15 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
 // Largest decode split count supported for `batch` sequences by `ws`.
 int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
+// Groups of 3, 6 and 7 query heads at D = 128 run the decode kernels as
+// groups of 4, 8 and 8 (padded_group, 0 for other groups), their query rows
+// copied into a padded layout (q_pad, [batch][Hkv][padded group][128], the
+// call's q dtype) and the real rows copied out of out_pad afterwards.
+int padded_group(int group);
+Shape padded_shape(const Shape& s);
+hipError_t launch_padded_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
+                                void* q_pad, void* out_pad, hipStream_t stream);
+
 // Query heads one general-shape workgroup serves (the same K/V rows read once
 // for all of them): up to 8 at D <= 128, 4 at D <= 256, 2 beyond, 1 when D
 // is not a multiple of 8; never more than the group.

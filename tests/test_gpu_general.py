@@ -248,3 +248,81 @@ def test_general_cache_rows_read_back():
         assert ctx.device_status() == nw.NWD_OK
         assert np.array_equal(from_cache(host(kc), 0, 9)[4:].view(np.uint16), k.view(np.uint16))
         assert np.array_equal(from_cache(host(vc), 0, 9)[4:].view(np.uint16), v.view(np.uint16))
+
+
+# ----------------------------------------------- groups 3, 6, 7 at D = 128 ---
+
+@pytest.mark.parametrize("H,Hkv", [(12, 4), (6, 1), (28, 4), (14, 2)])
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_padded_group_decode(H, Hkv, io):
+    """Groups 3, 6 and 7 at head_dim 128 run the decode kernels of groups 4
+    and 8 on padded query rows: against the oracle at 5000 and 1100 keys, with
+    two key bounds (different split partitions) within fp32 rounding of each
+    other, and the fused append bit-identical to append + decode in the
+    caches."""
+    D, cap = 128, 5010
+    lens = [5000, 1100]
+    say(f"padded group decode {H}q/{Hkv}kv io={io}")
+    g = rng(780 + H)
+    rows = [_rows(g, L, Hkv, D) for L in lens]
+    q = _q(g, (2, H, D), io)
+    kn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
+    vn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
+    with nw.AttnContext(H, Hkv, cap, max_batch=2, q_dtype=io, o_dtype=io) as ctx:
+        kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+        pos = pos_tensor([L - 1 for L in lens])
+        outs = {}
+        for bound in (cap, 1000):
+            out = torch.empty((2, H, D), dtype=_tdtype(io), device="cuda")
+            ctx.decode(dev(q), kc, vc, pos, out, 2, bound)
+            outs[bound] = host(out).astype(np.float32)
+        assert ctx.device_status() == nw.NWD_OK
+        for b, (k, v) in enumerate(rows):
+            want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k), f32(v))
+            assert max_abs(outs[cap][b], want) < TOL, b
+        assert max_abs(outs[cap], outs[1000]) < (2e-3 if io == "f16" else 2e-5)  # other splits
+        # fused append + attend at the bound that takes the padded kernels
+        res = []
+        for fused in (True, False):
+            kc2, vc2 = kc.clone(), vc.clone()
+            out = torch.empty((2, H, D), dtype=_tdtype(io), device="cuda")
+            p2 = pos_tensor(lens)  # the new rows go at L, attended over L + 1 keys
+            if fused:
+                ctx.append_decode(dev(q), dev(kn), dev(vn), kc2, vc2, p2, out, 2, cap)
+            else:
+                ctx.kv_append(dev(kn[:, None]), dev(vn[:, None]), kc2, vc2, p2, 2, 1)
+                ctx.decode(dev(q), kc2, vc2, p2, out, 2, cap)
+            assert ctx.device_status() == nw.NWD_OK
+            res.append((host(out), host(kc2).view(np.uint16), host(vc2).view(np.uint16)))
+        assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+        assert max_abs(res[0][0].astype(np.float32), res[1][0].astype(np.float32)) < (
+            1e-3 if io == "f16" else 1e-5)
+        for b, L in enumerate(lens):
+            k_all = np.concatenate([rows[b][0], kn[b][None]], axis=0)
+            v_all = np.concatenate([rows[b][1], vn[b][None]], axis=0)
+            want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k_all), f32(v_all))
+            assert max_abs(res[0][0][b].astype(np.float32), want) < TOL, b
+
+
+def test_padded_group_knobs():
+    """The decode knobs apply on the padded path: forced split counts and both
+    split kernels give the same results within fp32 rounding."""
+    H, Hkv, D, L = 14, 2, 128, 3000
+    g = rng(790)
+    k, v = _rows(g, L, Hkv, D)
+    q = _q(g, (1, H, D), "f32")
+    outs = []
+    with nw.AttnContext(H, Hkv, L, q_dtype="f32", o_dtype="f32") as ctx:
+        kc, vc = dev(to_cache([k], Hkv, L)), dev(to_cache([v], Hkv, L))
+        for n, kern in ((0, None), (3, None), (40, None), (0, 0), (0, 1)):
+            ctx.set_decode_splits(n)
+            ctx.set_decode_kernel(kern)
+            out = torch.empty((1, H, D), device="cuda")
+            ctx.decode(dev(q), kc, vc, pos_tensor([L - 1]), out, 1, L)
+            outs.append(host(out)[0])
+        assert ctx.device_status() == nw.NWD_OK
+    want = oracle.sparse_attn_f32(q[0], f32(k), f32(v))
+    for o in outs:
+        assert max_abs(o, want) < TOL
+        assert max_abs(o, outs[0]) < 1e-5
