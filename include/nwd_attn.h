@@ -188,8 +188,9 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * accumulation: an fp16 q enters exact and its scores are scaled in fp32;
  * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
  * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
- * makes nwd_device_status report NWD_ERR_DEVICE. The general shapes (see
- * nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
+ * makes nwd_device_status report NWD_ERR_DEVICE (groups 3, 6, 7 at D = 128
+ * run these kernels on padded query rows, in sub-chunks). The general shapes
+ * (see nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
  * outside the cache (pos0[b] < 0 or pos0[b] + n_new > max_seq) is flagged in
  * the device status and run at the nearest valid pos0. max_len bounds
  * pos0[b] + n_new (0 means max_seq). */

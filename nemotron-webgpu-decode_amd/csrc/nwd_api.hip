@@ -41,7 +41,9 @@ struct nwd_ctx {
   int* status_host;    // pinned copy target of the device status word
   int64_t o_floats;    // floats allocated for ws.part_o
   void* q_pad;         // padded query / output rows of the padded-group decode
-  void* out_pad;       //   (groups 3, 6, 7 at D = 128), or NULL
+  void* out_pad;       //   and prefill (groups 3, 6, 7 at D = 128), or NULL
+  int32_t* pos_sub;    // first positions of a padded prefill sub-chunk
+  int pad_tokens;      // tokens of a padded prefill sub-chunk
   std::string err;
 };
 
@@ -151,8 +153,9 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 // calls on MI355X, 28q/4kv (group 7): 9.2 against 22.3 us at 1024 keys,
 // 21.0 against 40.5 at 32768; 12q/2kv (group 6): 8.8 against 20.1 at 1024
 // keys, 17.3 at 32768; 24q/8kv (group 3): 10.0 against 14.0 at 1024 keys,
-// 28.2 at 32768. The allocation-free entry point, which has no padded
-// buffers, and the prefill use the general kernels.
+// 28.2 at 32768. The prefill of these groups runs the prefill kernels the
+// same way. The allocation-free entry point, which has no padded buffers,
+// uses the general kernels.
 enum DecodeRoute { kRouteSpecialised = 0, kRoutePadded = 1, kRouteGeneral = 2 };
 
 DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
@@ -326,6 +329,8 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->ws.part_ml = nullptr;
   ctx->q_pad = nullptr;
   ctx->out_pad = nullptr;
+  ctx->pos_sub = nullptr;
+  ctx->pad_tokens = 0;
   ctx->ws.status = nullptr;
   ctx->ws.counters = nullptr;
   ctx->status_host = nullptr;
@@ -342,9 +347,17 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
   const int gp = nwd::padded_group(group);
   if (e == hipSuccess && gp > 0 && d->head_dim == nwd::kHeadDim) {
-    const size_t bytes = (size_t)d->max_batch * d->n_kv_heads * gp * nwd::kHeadDim * sizeof(float);
-    e = hipMalloc(&ctx->q_pad, bytes);
-    if (e == hipSuccess) e = hipMalloc(&ctx->out_pad, bytes);
+    // Padded rows of up to 512 prefill tokens per sub-chunk, within 32 MiB
+    // per buffer (at least one token: the decode's rows).
+    const size_t per_token = (size_t)d->max_batch * d->n_kv_heads * gp * nwd::kHeadDim * sizeof(float);
+    size_t tokens = ((size_t)32 << 20) / per_token;
+    if (tokens > 512) tokens = 512;
+    if (tokens > (size_t)d->max_seq) tokens = (size_t)d->max_seq;
+    if (tokens < 1) tokens = 1;
+    ctx->pad_tokens = (int)tokens;
+    e = hipMalloc(&ctx->q_pad, per_token * tokens);
+    if (e == hipSuccess) e = hipMalloc(&ctx->out_pad, per_token * tokens);
+    if (e == hipSuccess) e = hipMalloc(&ctx->pos_sub, (size_t)d->max_batch * sizeof(int32_t));
   }
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.status, sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.status, 0, sizeof(int));
@@ -370,6 +383,7 @@ void nwd_destroy(nwd_ctx* ctx) {
   if (ctx->ws.status) (void)hipFree(ctx->ws.status);
   if (ctx->q_pad) (void)hipFree(ctx->q_pad);
   if (ctx->out_pad) (void)hipFree(ctx->out_pad);
+  if (ctx->pos_sub) (void)hipFree(ctx->pos_sub);
   if (ctx->status_host) (void)hipHostFree(ctx->status_host);
   if (prev >= 0) (void)hipSetDevice(prev);
   delete ctx;
@@ -619,7 +633,11 @@ int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const voi
     return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: max_len %d outside [n_new, max_seq=%d]",
                 len, ctx->desc.max_seq);
   hipError_t e;
-  if (ctx->shape.general) {
+  if (decode_route(ctx->shape, ctx->q_pad != nullptr) == kRoutePadded) {
+    nwd::PadBuffers pb{ctx->q_pad, ctx->out_pad, ctx->pos_sub, ctx->pad_tokens};
+    e = nwd::launch_padded_prefill(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new, len,
+                                   ctx->ws, pb, (hipStream_t)stream);
+  } else if (ctx->shape.general) {
     const int64_t rows = (int64_t)batch * n_new * ctx->desc.n_heads;
     if (rows > 0x7FFFFFFF)
       return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: %lld output rows exceed 2^31 - 1",

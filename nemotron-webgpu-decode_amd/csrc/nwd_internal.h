@@ -88,6 +88,21 @@ Shape padded_shape(const Shape& s);
 hipError_t launch_padded_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                                 void* q_pad, void* out_pad, hipStream_t stream);
 
+// The prefill of those groups on the prefill kernels of groups 4 / 8: the
+// chunk goes through in sub-chunks of chunk_tokens tokens, each padded into
+// q_pad ([batch][chunk_tokens][Hkv][padded group][128]), its first positions
+// in pos_sub ([batch]), its output unpadded from out_pad.
+struct PadBuffers {
+  void* q_pad;
+  void* out_pad;
+  int32_t* pos_sub;
+  int chunk_tokens;
+};
+hipError_t launch_padded_prefill(const Shape& s, const void* q, const void* k_cache,
+                                 const void* v_cache, const int32_t* pos0, void* out, int batch,
+                                 int n_new, int max_len, const Workspace& ws, const PadBuffers& pb,
+                                 hipStream_t stream);
+
 // Query heads one general-shape workgroup serves (the same K/V rows read once
 // for all of them): up to 8 at D <= 128, 4 at D <= 256, 2 beyond, 1 when D
 // is not a multiple of 8; never more than the group.

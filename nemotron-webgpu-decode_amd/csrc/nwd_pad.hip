@@ -1,15 +1,17 @@
-// nwd_pad.hip — decode at head_dim 128 with groups of 3, 6 or 7 query heads
-// on the kernels built for groups of 4 and 8 (nwd_decode.hip).
+// nwd_pad.hip — decode and prefill at head_dim 128 with groups of 3, 6 or 7
+// query heads on the kernels built for groups of 4 and 8 (nwd_decode.hip,
+// nwd_prefill.hip).
 //
 // The reference kernel maps query head h to KV head h / (H / Hkv) for any
-// group (kernels/sparse_attn.wgsl:38-39). nwd_decode.hip serves a whole group
-// per workgroup, reading each K/V row once, for groups 1, 2, 4, 5 and 8. A
-// group of 3 (6, 7) is run as a group of 4 (8): the query rows are copied
-// into a padded layout with zero rows after each group's real heads, the
-// decode runs on it, and the real heads' rows are copied out. Decode is bound
-// by the K/V stream, which the padding leaves unchanged; the zero rows'
-// outputs are discarded. The copies are two small launches (B x Hkv x 8 x 128
-// values each), so the host takes this path from a key bound up.
+// group (kernels/sparse_attn.wgsl:38-39). The decode and prefill kernels
+// serve a whole group per workgroup, reading each K/V row once, for groups
+// 1, 2, 4, 5 and 8. A group of 3 (6, 7) is run as a group of 4 (8): the
+// query rows are copied into a padded layout with zero rows after each
+// group's real heads, the kernels run on it, and the real heads' rows are
+// copied out. Decode is bound by the K/V stream, which the padding leaves
+// unchanged; the zero rows' outputs are discarded. A prefill chunk goes
+// through in sub-chunks sized to the context's padded buffers, each with its
+// first positions offset.
 #include "nwd_common.h"
 #include "nwd_internal.h"
 
@@ -43,6 +45,56 @@ __global__ __launch_bounds__(kPadThreads) void unpad_rows_kernel(const T* __rest
   const int g = (int)(r % G);
   const int64_t bh = r / G;
   out[i] = op[(bh * Gf + g) * kHeadDim + d];
+}
+
+// Prefill: rows qp[b][i][hk][g][d] = g < G ? q[b][c0 + i][hk * G + g][d] : 0
+// for the nc tokens c0 .. c0 + nc - 1 of the chunk; thread i < batch also
+// writes the sub-chunk's first position, pos0[b] clamped into the cache as
+// the prefill kernels clamp it, plus c0 (an out-of-range chunk is flagged
+// once, on its first sub-chunk).
+template <typename T>
+__global__ __launch_bounds__(kPadThreads) void pad_chunk_kernel(
+    const T* __restrict__ q, T* __restrict__ qp, const int32_t* __restrict__ pos0,
+    int32_t* __restrict__ pos_sub, int64_t n, int batch, int n_new, int c0, int nc, int n_kv,
+    int G, int Gf, int cap, int* __restrict__ status) {
+  const int64_t i = (int64_t)blockIdx.x * kPadThreads + threadIdx.x;
+  if (i < batch) {
+    int P0 = pos0[i];
+    if (P0 < 0 || P0 > cap - n_new) {
+      if (c0 == 0) atomicOr(status, kStatusBadPos);
+      P0 = P0 < 0 ? 0 : cap - n_new;
+    }
+    pos_sub[i] = P0 + c0;
+  }
+  if (i >= n) return;
+  const int d = (int)(i % kHeadDim);
+  int64_t r = i / kHeadDim;
+  const int g = (int)(r % Gf);
+  r /= Gf;
+  const int hk = (int)(r % n_kv);
+  r /= n_kv;
+  const int t = (int)(r % nc);
+  const int64_t b = r / nc;
+  qp[i] = g < G ? q[(((b * n_new + c0 + t) * n_kv + hk) * G + g) * kHeadDim + d] : T(0);
+}
+
+// out[b][c0 + i][hk * G + g][d] = op[b][i][hk][g][d] for g < G.
+template <typename T>
+__global__ __launch_bounds__(kPadThreads) void unpad_chunk_kernel(
+    const T* __restrict__ op, T* __restrict__ out, int64_t n, int n_new, int c0, int nc, int n_kv,
+    int G, int Gf) {
+  const int64_t i = (int64_t)blockIdx.x * kPadThreads + threadIdx.x;
+  if (i >= n) return;
+  const int d = (int)(i % kHeadDim);
+  int64_t r = i / kHeadDim;  // (b, t, hk, g) of the sub-chunk's real rows
+  const int g = (int)(r % G);
+  r /= G;
+  const int hk = (int)(r % n_kv);
+  r /= n_kv;
+  const int t = (int)(r % nc);
+  const int64_t b = r / nc;
+  out[(((b * n_new + c0 + t) * n_kv + hk) * G + g) * kHeadDim + d] =
+      op[(((b * nc + t) * n_kv + hk) * Gf + g) * kHeadDim + d];
 }
 
 int padded_group(int group) {
@@ -88,6 +140,48 @@ hipError_t launch_padded_decode(const Shape& s, const DecodeCall& c, const Works
                  : run_padded<f16, float>(s, c, ws, q_pad, out_pad, stream);
   return s.o16 ? run_padded<float, f16>(s, c, ws, q_pad, out_pad, stream)
                : run_padded<float, float>(s, c, ws, q_pad, out_pad, stream);
+}
+
+
+template <typename TQ, typename TO>
+static hipError_t run_padded_prefill(const Shape& s, const void* q, const void* kc, const void* vc,
+                                     const int32_t* pos0, void* out, int batch, int n_new,
+                                     int max_len, const Workspace& ws, const PadBuffers& pb,
+                                     hipStream_t stream) {
+  const Shape p = padded_shape(s);
+  for (int c0 = 0; c0 < n_new; c0 += pb.chunk_tokens) {
+    const int nc = min(pb.chunk_tokens, n_new - c0);
+    const int64_t n_pad = (int64_t)batch * nc * p.n_heads * kHeadDim;
+    const int64_t n_real = (int64_t)batch * nc * s.n_heads * kHeadDim;
+    const int64_t n_launch = n_pad > batch ? n_pad : batch;
+    pad_chunk_kernel<TQ><<<(unsigned)((n_launch + kPadThreads - 1) / kPadThreads), kPadThreads, 0, stream>>>(
+        static_cast<const TQ*>(q), static_cast<TQ*>(pb.q_pad), pos0, pb.pos_sub, n_pad, batch, n_new,
+        c0, nc, s.n_kv, s.group, p.group, s.cap, ws.status);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    e = launch_prefill(p, pb.q_pad, kc, vc, pb.pos_sub, pb.out_pad, batch, nc, max_len, ws, stream);
+    if (e != hipSuccess) return e;
+    unpad_chunk_kernel<TO><<<(unsigned)((n_real + kPadThreads - 1) / kPadThreads), kPadThreads, 0, stream>>>(
+        static_cast<const TO*>(pb.out_pad), static_cast<TO*>(out), n_real, n_new, c0, nc, s.n_kv, s.group,
+        p.group);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_padded_prefill(const Shape& s, const void* q, const void* k_cache,
+                                 const void* v_cache, const int32_t* pos0, void* out, int batch,
+                                 int n_new, int max_len, const Workspace& ws, const PadBuffers& pb,
+                                 hipStream_t stream) {
+  if (padded_group(s.group) == 0 || s.head_dim != kHeadDim || !pb.q_pad || !pb.out_pad ||
+      !pb.pos_sub || pb.chunk_tokens < 1)
+    return hipErrorInvalidValue;
+  if (s.q16)
+    return s.o16 ? run_padded_prefill<f16, f16>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, pb, stream)
+                 : run_padded_prefill<f16, float>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, pb, stream);
+  return s.o16 ? run_padded_prefill<float, f16>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, pb, stream)
+               : run_padded_prefill<float, float>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, pb, stream);
 }
 
 }  // namespace nwd

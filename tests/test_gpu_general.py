@@ -326,3 +326,38 @@ def test_padded_group_knobs():
     for o in outs:
         assert max_abs(o, want) < TOL
         assert max_abs(o, outs[0]) < 1e-5
+
+
+@pytest.mark.parametrize("H,Hkv", [(12, 4), (7, 1)])
+@pytest.mark.parametrize("max_batch", [2, 2048])
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_padded_group_prefill(H, Hkv, max_batch, io):
+    """Groups 3 and 7 at head_dim 128 prefill on the fp16 MFMA prefill kernels
+    of groups 4 and 8 through padded query rows: 37 queries onto pos0 90 and
+    0, row by row against the oracle's decode over keys 0..pos0+i. With
+    max_batch 2048 the context's padded buffers hold a few tokens, so the
+    chunk runs in several sub-chunks."""
+    D, n_new, pos0, cap = 128, 37, [90, 0], 140
+    say(f"padded group prefill {H}q/{Hkv}kv max_batch={max_batch} io={io}")
+    g = rng(800 + H)
+    rows = [_rows(g, p + n_new, Hkv, D, scale=0.5) for p in pos0]
+    q = _q(g, (2, n_new, H, D), io)
+    with nw.AttnContext(H, Hkv, cap, max_batch=max_batch, q_dtype=io, o_dtype="f32") as ctx:
+        kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+        out = torch.empty((2, n_new, H, D), device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor(pos0), out, 2, n_new, max(pos0) + n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        got = host(out)
+        # a chunk past the capacity is flagged once and run at the last fitting pos0
+        ctx.prefill(dev(q), kc, vc, pos_tensor([cap - 10, 0]), out, 2, n_new, cap)
+        assert ctx.device_status() == nw.NWD_ERR_DEVICE
+        assert ctx.device_status() == nw.NWD_OK
+    worst = 0.0
+    for b, (k, v) in enumerate(rows):
+        for i in range(n_new):
+            L = pos0[b] + i + 1
+            want = oracle.sparse_attn_f32(q[b, i].astype(np.float32), f32(k[:L]), f32(v[:L]))
+            worst = max(worst, max_abs(got[b, i], want))
+    say(f"  max-abs {worst:.2e}")
+    assert worst < TOL
