@@ -339,8 +339,17 @@ def run_general(torch, nw, steps: int = 128, warmup: int = 8):
         _, ms = time_graph(torch, wl, steps, warmup, append=False, reps=3)
         us = ms * 1e3 / steps
         gbs = wl.kv_bytes() / (us * 1e-6) / 1e9
+        splits = wl.ctx.decode_splits(1, past)
+        # the library's split count against half and twice as many
+        by_splits = {}
+        for n in sorted({max(1, splits // 2), min(256, splits * 2)} - {splits}):
+            wl.ctx.set_decode_splits(n)
+            _, ms_n = time_graph(torch, wl, steps, warmup, append=False, reps=3)
+            by_splits[str(n)] = ms_n * 1e3 / steps
+        wl.ctx.set_decode_splits(0)
         res[name] = {"desc": desc, "us_per_call": us, "kv_bytes": wl.kv_bytes(), "gbs": gbs,
-                     "hbm_frac": gbs / HBM_PEAK_GBS, "splits": wl.ctx.decode_splits(1, past)}
+                     "hbm_frac": gbs / HBM_PEAK_GBS, "splits": splits,
+                     "us_by_forced_splits": by_splits}
         log(f"[bench] {name}: {res[name]}")
         wl.ctx.close()
         del wl

@@ -141,12 +141,6 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   return n < 1 ? 1 : n;
 }
 
-// Split count of the general-shape kernels (nwd_general.hip: one workgroup
-// per split and `units` (sequence, query, KV head, head chunk)): about 512
-// workgroups when the units alone are fewer, with at least 64 keys per split
-// (one 16-key tile per wavefront). Decode calls on MI355X, us at 1/2x, 1x, 2x this count: 28q/4kv/d128
-// at 32K keys 57.5 / 40.5 / 51.2 (128 splits), 16q/8kv/d256 at 8K 26.2 /
-// 24.4 / 26.7 (64), 32q/32kv/d96 at 4K 17.7 / 16.5 / 16.5 (16).
 // Decode calls at D = 128 with a group of 3, 6 or 7 run the kernels of
 // groups 4 / 8 on padded query rows (nwd_pad.hip), at every length: the two
 // copy launches cost less than the general kernels' longer chains. Decode
@@ -169,6 +163,13 @@ int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
   return (int64_t)batch * n_new * s.n_kv * ((s.group + gp - 1) / gp);
 }
 
+// Split count of the general-shape kernels (nwd_general.hip: one workgroup
+// per split and `units` (sequence, query, KV head, head chunk)): about 512
+// workgroups when the units alone are fewer, with at least 64 keys per split
+// (one 16-key tile per wavefront). Decode calls on MI355X, us at 1/2x, 1x and
+// 2x this count (bench.py --workload general, us_by_forced_splits):
+// 16q/8kv/d256 at 8K keys 26.0 / 24.2 / 26.5 (64 splits), 32q/32kv/d96 at 4K
+// 17.6 / 16.3 / 16.5 (16).
 int general_splits(int64_t units, int max_len) {
   if (units >= 512) return 1;
   int n = (int)((512 + units - 1) / units);
