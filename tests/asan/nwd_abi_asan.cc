@@ -156,7 +156,8 @@ struct Q4 {
 
 // One context of group g and head size d through every entry point: batch
 // 2, 512 positions (d = 128 with groups 1, 2, 4, 5, 8 runs the specialised
-// kernels, the other shapes the general ones).
+// kernels, group 7 at d = 128 the padded-group route, the other shapes the
+// general kernels).
 static void gpu_cycle(int group, int d) {
   const int hkv = 8, h = hkv * group, batch = 2, max_seq = 512;
   nwd_desc desc = make_desc(h, hkv, max_seq, batch);
@@ -257,7 +258,8 @@ int main(int argc, char** argv) {
   std::printf("nwd_abi_asan: cpu checks: %d calls, %d failed\n", g_calls, g_failed);
   std::fflush(stdout);
   if (gpu) {
-    const int shapes[][2] = {{1, 128}, {2, 128}, {4, 128}, {5, 128}, {8, 128}, {3, 96}, {2, 100}};
+    const int shapes[][2] = {{1, 128}, {2, 128}, {4, 128}, {5, 128}, {8, 128}, {3, 96}, {2, 100},
+                             {7, 128}};
     for (const auto& gd : shapes) {
       const int before = g_calls;
       gpu_cycle(gd[0], gd[1]);
