@@ -297,7 +297,7 @@ class Q4LayerWorkload:
 
 
 class GeneralWorkload:
-    """Decode-only calls on a shape of the general kernels (nwd_general.hip):
+    """Decode-only calls on a head layout other than the benchmark's:
     `layers` caches of `past` random fp16 tokens (rotated so the K/V reads
     come from HBM), one fp16 query per call attending all `past` keys."""
 
@@ -328,9 +328,10 @@ class GeneralWorkload:
 
 
 def run_general(torch, nw, steps: int = 128, warmup: int = 8):
-    """Three head layouts the kernels built for head_dim 128 with groups
-    1/2/4/5/8 do not cover as they are: us per decode call (graph-replayed),
-    K/V GB/s and the fraction of the HBM peak."""
+    """Head layouts other than the benchmark's (head_dim 128 with groups
+    1/2/4/5/8): us per decode call (graph-replayed), K/V GB/s and the
+    fraction of the HBM peak, and the time at half and twice the split
+    count."""
     res = {}
     for name, (heads, kv_heads, head_dim, past, desc) in GENERAL_SHAPES.items():
         log(f"[bench] {name}: {heads}q/{kv_heads}kv/d{head_dim}, {past} keys, {steps} calls")
@@ -691,6 +692,8 @@ GENERAL_SHAPES = {
                         "Gemma-2-9B layout), 8192 keys, fp16 I/O, decode call"),
     "general-d96-4k": (32, 32, 96, 4096, "B=1, 32q/32kv/d96 (group 1, head size 96: the "
                        "Phi-3-mini layout), 4096 keys, fp16 I/O, decode call"),
+    "general-d64-16k": (32, 8, 64, 16384, "B=1, 32q/8kv/d64 (group 4, head size 64: the "
+                        "Llama-3.2-1B layout), 16384 keys, fp16 I/O, decode call"),
 }
 
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,

@@ -70,8 +70,11 @@ typedef struct nwd_desc {
                           with G one of 1, 2, 4, 5, 8 runs the kernels built
                           for those shapes, and decodes with G = 3, 6, 7 run
                           them as G = 4, 8, 8 on zero-padded query rows
-                          (buffers allocated by nwd_create); every other
-                          (D, G) runs the general kernels, with the same
+                          (buffers allocated by nwd_create); decodes at
+                          D = 64 (G 1, 2, 4, 5, 8) and D = 256 (G 1, 2, 4, 5)
+                          run the dot-product split kernel built for those
+                          sizes; every other (D, G), and prefill at D other
+                          than 128, runs the general kernels, with the same
                           contract and cache layout (a coverage path, not
                           tuned like the others)                             */
   int32_t max_seq;     /* cache capacity in tokens per sequence, at most
@@ -211,8 +214,8 @@ int nwd_device_status(nwd_ctx* ctx, void* stream);
 int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len);
 
 /* Overrides the split count chosen by nwd_decode_attn (0 restores the
- * automatic choice); on the general shapes (see nwd_desc.head_dim) it also
- * sets nwd_prefill_attn's. Values are clamped to [1, 256]. Results do not
+ * automatic choice); on shapes whose prefill runs the general kernels (see
+ * nwd_desc.head_dim) it also sets nwd_prefill_attn's. Values are clamped to [1, 256]. Results do not
  * depend on it beyond fp32 reordering. */
 int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
 
@@ -222,8 +225,10 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * last workgroup of each (sequence, kv head) to finish (of each (sequence,
  * query head) when the call runs one workgroup per query head); negative restores the
  * default, the separate kernel (measured faster on MI355X at 4K and 32K
- * keys). Same results, bit for bit. The general shapes always use the
- * separate merge; this and the two knobs below do not apply to them. */
+ * keys). Same results, bit for bit. The general kernels always use the
+ * separate merge; this and the two knobs below do not apply to them (at
+ * D = 64 and 256 this and the layout knob apply, the kernel knob does not:
+ * only the dot-product kernel is built for those sizes). */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
 /* Chooses the split kernel of later decode calls (the workgroup form of

@@ -149,11 +149,13 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 // keys, 17.3 at 32768; 24q/8kv (group 3): 10.0 against 14.0 at 1024 keys,
 // 28.2 at 32768. The prefill of these groups runs the prefill kernels the
 // same way. The allocation-free entry point, which has no padded buffers,
-// uses the general kernels.
+// uses the general kernels. Decode at head size 64 (groups 1, 2, 4, 5, 8)
+// and 256 (groups 1, 2, 4, 5) runs the dot-product split kernel built for
+// those sizes; their prefill runs the general kernels.
 enum DecodeRoute { kRouteSpecialised = 0, kRoutePadded = 1, kRouteGeneral = 2 };
 
 DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
-  if (!s.general) return kRouteSpecialised;
+  if (nwd::split_decode_shape(s.head_dim, s.group)) return kRouteSpecialised;
   if (have_pad && nwd::padded_group(s.group) > 0 && s.head_dim == nwd::kHeadDim) return kRoutePadded;
   return kRouteGeneral;
 }
@@ -537,8 +539,9 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
     return fail(nullptr, NWD_ERR_CAPACITY, "%s: max_len %d exceeds max_seq %d", who, len,
                 desc->max_seq);
   const nwd::Shape sh = shape_of(desc);
-  int n = sh.general ? general_splits(general_units(sh, batch, 1), len)
-                     : auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
+  const bool general = decode_route(sh, false) == kRouteGeneral;
+  int n = general ? general_splits(general_units(sh, batch, 1), len)
+                  : auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
   if (n > kMaxSplits) n = kMaxSplits;
   const int64_t records = n > 1 ? (int64_t)batch * desc->n_heads * n : 0;
   const int64_t have = scratch_records(desc->head_dim);
@@ -573,7 +576,7 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   c.ev_start = nullptr;
   c.ev_stop = nullptr;
   hipError_t e = hipSuccess;
-  if (sh.general) {
+  if (general) {
     e = nwd::launch_kv_append(sh, k_new, v_new, k_cache, v_cache, pos, batch, 1, ws.status,
                               (hipStream_t)stream);
     if (e == hipSuccess)

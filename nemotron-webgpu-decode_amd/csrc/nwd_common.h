@@ -15,7 +15,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kHeadDim = 128;            // D, the only head size built
+constexpr int kHeadDim = 128;  // D of the benchmark shapes, the matrix-core and prefill kernels
 // Largest cache capacity in tokens: a (sequence, kv head) slab is then at most
 // 1 GiB, so 32-bit byte offsets into it, including those of the few tiles
 // requested past a range's end, stay below 2^31.

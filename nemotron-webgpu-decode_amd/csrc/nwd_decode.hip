@@ -51,6 +51,7 @@
 #include <hip/hip_ext.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "nwd_common.h"
 #include "nwd_internal.h"
@@ -58,21 +59,27 @@
 namespace nwd {
 
 // Shape of one split workgroup: kW wavefronts, rows of kL lanes per key,
-// kKpr keys per row per iteration, kT iterations' tiles in flight.
-template <int kW, int kL, int kKpr_, int kT>
-struct DecodeCfg {
+// kKpr keys per row per iteration, kT iterations' tiles in flight, head size
+// kD (64, 128 or 256).
+template <int kW, int kL, int kKpr_, int kT, int kD_>
+struct DecodeShape {
+  static constexpr int kD = kD_;
   static constexpr int kTiles = kT;
   static constexpr int kWaves = kW;
   static constexpr int kThreads = kW * 64;
   static constexpr int kLanes = kL;               // lanes per key row
   static constexpr int kRows = 64 / kL;           // key rows per wavefront
-  static constexpr int kRuns = 16 / kL;           // 16-byte runs per lane per key
+  static constexpr int kRuns = kD / 8 / kL;       // 16-byte runs per lane per key
   static constexpr int kDims = 8 * kRuns;         // dims per lane
   static constexpr int kKpr = kKpr_;              // keys per row per iteration
   static constexpr int kWaveKeys = kRows * kKpr;  // keys per wavefront per iteration
   static constexpr int kBlockKeys = kW * kWaveKeys;
   static_assert(kL == 8 || kL == 16, "rows of 8 or 16 lanes");
+  static_assert(kD % (8 * kL) == 0, "whole 16-byte runs per lane");
 };
+// The head-128 form.
+template <int kW, int kL, int kKpr_, int kT>
+struct DecodeCfg : DecodeShape<kW, kL, kKpr_, kT, kHeadDim> {};
 
 // Units the key range is split in (16 keys, one matrix-core wavefront
 // block, two dot-product wavefront tiles). Each split's time is that of its
@@ -173,11 +180,75 @@ constexpr int kMergePass = 32;
 // the earlier 256-thread merge, which combined eight thread groups' partial
 // sums through LDS, per call: 32K keys 24.5 against 24.9-25.0 us, 4K 8.6
 // against 9.0, 40q/8kv at 32K 24.7 against 25.1.)
-template <bool kO16, int kPolicy>
+// The same for head sizes other than 128 (kD / 64 dims per lane, one
+// 4-, 8- or 16-byte load per split and lane).
+template <bool kO16, int kPolicy, int kD>
+__device__ inline void merge_row_wave_d(const float* __restrict__ part_o,
+                                        const float2* __restrict__ part_ml, void* __restrict__ out,
+                                        int64_t row, int nsplit, int64_t out_rows, int64_t records,
+                                        int* status) {
+  constexpr int kDL = kD / 64;  // dims per lane
+  static_assert(kDL == 1 || kDL == 4, "head size 64 or 256");
+  const int lane = threadIdx.x & 63;
+  const int64_t rec0 = row * nsplit;
+  if (!in_bounds(rec0, nsplit, records, status)) return;
+  const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(const_cast<float2*>(part_ml + rec0), 0,
+                                                      nsplit * 8, kBufferWord3);
+  const auto r_o = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(part_o + rec0 * kD), 0,
+                                                     nsplit * kD * 4, kBufferWord3);
+  float M = kNegBig, L = 0.f, acc[kDL];
+#pragma unroll
+  for (int i = 0; i < kDL; ++i) acc[i] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += kMergePass) {
+    const int ns = min(kMergePass, nsplit - s0);
+    const float2 ml = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+        r_ml, (s0 + min(lane, ns - 1)) * 8, 0, kPolicy));
+    float ov[kMergePass][kDL];
+#pragma unroll
+    for (int s = 0; s < kMergePass; ++s) {
+      const uint32_t off = ((s0 + min(s, ns - 1)) * kD + kDL * lane) * 4;
+      if constexpr (kDL == 1) {
+        ov[s][0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r_o, off, 0, kPolicy));
+      } else {
+        const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r_o, off, 0, kPolicy));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[s][i] = v[i];
+      }
+    }
+    const float m = lane < ns ? ml.x : kNegBig;
+    const float mn = fmaxf(M, max_xor32(max32(m)));
+    const float w = lane < ns ? fast_exp2(m - mn) : 0.f;
+    const float alpha = fast_exp2(M - mn);
+    L = fmaf(L, alpha, sum64(ml.y * w));
+#pragma unroll
+    for (int i = 0; i < kDL; ++i) acc[i] *= alpha;
+#pragma unroll
+    for (int s = 0; s < kMergePass; ++s) {
+      const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+#pragma unroll
+      for (int i = 0; i < kDL; ++i) acc[i] = fmaf(ov[s][i], ws, acc[i]);
+    }
+    M = mn;
+  }
+  const float inv = 1.f / L;
+  const int64_t at = row * kD + kDL * lane;
+  if (!in_bounds(at, kDL, out_rows * kD, status)) return;
+#pragma unroll
+  for (int i = 0; i < kDL; ++i) {
+    if constexpr (kO16) static_cast<f16*>(out)[at + i] = (f16)(acc[i] * inv);
+    else static_cast<float*>(out)[at + i] = acc[i] * inv;
+  }
+}
+
+template <bool kO16, int kPolicy, int kD = kHeadDim>
 __device__ inline void merge_row_wave(const float* __restrict__ part_o,
                                       const float2* __restrict__ part_ml, void* __restrict__ out,
                                       int64_t row, int nsplit, int64_t out_rows, int64_t records,
                                       int* status) {
+  if constexpr (kD != kHeadDim) {
+    merge_row_wave_d<kO16, kPolicy, kD>(part_o, part_ml, out, row, nsplit, out_rows, records, status);
+    return;
+  }
   const int lane = threadIdx.x & 63;
   const int64_t rec0 = row * nsplit;
   // uniform over the wavefront
@@ -255,11 +326,18 @@ constexpr int kRecPolicy = 16;
 // kStates partial states its wavefronts left in LDS (lds_o [kStates][G][D]
 // and lds_ml [kStates][G][2], (m, l) in log2 units) into one record per
 // query head, or, with one split, the normalised output. Called by every
-// thread after a barrier; thread t < 32 G owns the 4-dim run t % 32 of
-// head t / 32. hrow0 = b * n_heads + first head.
-template <int G, bool kO16, int kStates>
+// thread after a barrier; thread t < 32 G owns the kD / 32-dim run t % 32
+// of head t / 32. hrow0 = b * n_heads + first head.
+template <int kN>
+using f32xn = float __attribute__((ext_vector_type(kN)));
+template <int kN>
+using f16xn = f16 __attribute__((ext_vector_type(kN)));
+template <int G, bool kO16, int kStates, int kD = kHeadDim>
 __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_o,
                                           const float* lds_ml, int64_t hrow0, int split) {
+  constexpr int kR = kD / 32;  // dims per thread: 2, 4 or 8
+  static_assert(kR == 2 || kR == 4 || kR == 8, "head size 64, 128 or 256");
+  using vec = f32xn<kR>;
   const int tid = threadIdx.x;
   const int nsplit = a.nsplit;
   if (tid < G * 32) {
@@ -267,27 +345,27 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
     float M = kNegBig;
 #pragma unroll
     for (int w = 0; w < kStates; ++w) M = fmaxf(M, lds_ml[(w * G + g) * 2]);
-    f32x4 o = f32x4{0.f, 0.f, 0.f, 0.f};
+    vec o = vec(0.f);
     float lt = 0.f;
 #pragma unroll
     for (int w = 0; w < kStates; ++w) {
       const float sc = fast_exp2(lds_ml[(w * G + g) * 2] - M);
-      o += *reinterpret_cast<const f32x4*>(&lds_o[(w * G + g) * kHeadDim + d4 * 4]) * sc;
+      o += *reinterpret_cast<const vec*>(&lds_o[(w * G + g) * kD + d4 * kR]) * sc;
       lt = fmaf(lds_ml[(w * G + g) * 2 + 1], sc, lt);
     }
     const int64_t out_rows = (int64_t)a.batch * a.n_heads;
     if (nsplit == 1) {
       const float inv = 1.f / lt;
-      const int64_t at = (hrow0 + g) * kHeadDim + d4 * 4;
-      if (!in_bounds(at, 4, out_rows * kHeadDim, a.status)) {
+      const int64_t at = (hrow0 + g) * kD + d4 * kR;
+      if (!in_bounds(at, kR, out_rows * kD, a.status)) {
         // (bounds-checked builds only) the store is dropped
       } else if constexpr (kO16) {
-        f16x4 v;
+        f16xn<kR> v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = (f16)(o[i] * inv);
-        *reinterpret_cast<f16x4*>(static_cast<f16*>(a.out) + at) = v;
+        for (int i = 0; i < kR; ++i) v[i] = (f16)(o[i] * inv);
+        *reinterpret_cast<f16xn<kR>*>(static_cast<f16*>(a.out) + at) = v;
       } else {
-        *reinterpret_cast<f32x4*>(static_cast<float*>(a.out) + at) = o * inv;
+        *reinterpret_cast<vec*>(static_cast<float*>(a.out) + at) = o * inv;
       }
     } else {
       // records of this split: (g, split) at hrow0 * nsplit + g * nsplit + split
@@ -295,20 +373,38 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
       // the descriptors below stop stores past this head group's records;
       // head g's nsplit records must lie inside the workspace
       const bool rec_ok = in_bounds((hrow0 + g) * nsplit, nsplit, a.records, a.status);
-      const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kHeadDim, 0,
-                                                         G * nsplit * kHeadDim * 4, kBufferWord3);
+      const auto r_o = __builtin_amdgcn_make_buffer_rsrc(a.part_o + rec0 * kD, 0,
+                                                         G * nsplit * kD * 4, kBufferWord3);
       const auto r_ml = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + rec0, 0, G * nsplit * 8,
                                                           kBufferWord3);
-      const uint32_t off = (g * nsplit * kHeadDim + d4 * 4) * 4;
+      const uint32_t off = (g * nsplit * kD + d4 * kR) * 4;
+      // the o run as 8- or 16-byte stores with the given cache policy
+      auto store_o = [&](auto policy) {
+        if constexpr (kR == 2) {
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, o), r_o, off, 0,
+                                                decltype(policy)::value);
+        } else if constexpr (kR == 4) {
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0,
+                                                 decltype(policy)::value);
+        } else {
+          // (the halves copied element by element: a bit cast of o.hi compiled to
+          // o.lo's registers)
+          const f32x4 lo = {o[0], o[1], o[2], o[3]}, hi = {o[4], o[5], o[6], o[7]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, lo), r_o, off, 0,
+                                                 decltype(policy)::value);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, hi), r_o, off + 16,
+                                                 0, decltype(policy)::value);
+        }
+      };
       if (!rec_ok) {
         // (bounds-checked builds only) the stores are dropped
       } else if (a.fused_merge) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, kRecPolicy);
+        store_o(std::integral_constant<int, kRecPolicy>{});
         if (d4 == 0)
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
                                                 g * nsplit * 8, 0, kRecPolicy);
       } else {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), r_o, off, 0, 0);
+        store_o(std::integral_constant<int, 0>{});
         if (d4 == 0)
           __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(M, lt)), r_ml,
                                                 g * nsplit * 8, 0, 0);
@@ -333,7 +429,7 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
 // barrier that precedes the ticket, and the acquire to the sc1 loads in
 // merge_row_wave, which are issued only after the ticket has returned (they
 // depend on it through lds_last). Wavefront w merges heads w, w + waves, ...
-template <int G, bool kO16>
+template <int G, bool kO16, int kD = kHeadDim>
 __device__ inline void merge_on_last_arrival(const DecodeArgs& a, int* counter, int64_t hrow0) {
   __shared__ int lds_last;
   wait_vm();
@@ -345,10 +441,19 @@ __device__ inline void merge_on_last_arrival(const DecodeArgs& a, int* counter, 
   __syncthreads();
   if (!lds_last) return;
   for (int g = (int)threadIdx.x >> 6; g < G; g += (int)blockDim.x >> 6)
-    merge_row_wave<kO16, kRecPolicy>(a.part_o, a.part_ml, a.out, hrow0 + g, a.nsplit,
-                                     (int64_t)a.batch * a.n_heads, a.records, a.status);
+    merge_row_wave<kO16, kRecPolicy, kD>(a.part_o, a.part_ml, a.out, hrow0 + g, a.nsplit,
+                                         (int64_t)a.batch * a.n_heads, a.records, a.status);
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Lane-exchange steps that merge a wavefront's row states in registers
+// before they go to LDS: the fewest (up to log2 rows) that bring `bytes`,
+// the LDS the unmerged states would take, under 48 KB.
+constexpr int row_steps(int bytes, int rows) {
+  int st = 0;
+  while ((1 << st) < rows && (bytes >> st) > 48 * 1024) ++st;
+  return st;
 }
 
 // kQsub workgroups per KV head, each serving G of its query heads (kQsub = 1:
@@ -359,20 +464,21 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kLanes = C::kLanes, kRows = C::kRows, kRuns = C::kRuns, kDims = C::kDims;
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
   constexpr int kTiles = C::kTiles;
-  static_assert(G * 32 <= kThreads, "one 4-dim run of each head per thread");
+  constexpr int kD = C::kD;
+  static_assert(G * 32 <= kThreads, "one run of each head per thread");
   // Row states written to LDS per wavefront (see the end of the kernel). The
   // rule depends on the shape's group size, not on the heads this
   // workgroup serves, so both forms of a shape merge in the same order (same
   // bits).
-  constexpr int kRowSteps = G * kQsub * kWaves * kRows * (kHeadDim + 2) * 4 <= 48 * 1024 ? 0 : 1;
+  constexpr int kRowSteps = row_steps(G * kQsub * kWaves * kRows * (kD + 2) * 4, kRows);
   constexpr int kRowStates = kRows >> kRowSteps;
   constexpr int kStates = kWaves * kRowStates;
-  constexpr int kLdsFloats = kStates * G * (kHeadDim + 2);
+  constexpr int kLdsFloats = kStates * G * (kD + 2);
   static_assert(kLdsFloats * 4 <= 64 * 1024, "static LDS of one workgroup");
 
   __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
   float* lds_o = lds;                                 // [kStates][G][D]
-  float* lds_ml = lds + kStates * G * kHeadDim;        // [kStates][G][2]
+  float* lds_ml = lds + kStates * G * kD;        // [kStates][G][2]
 
   // Workgroups are dealt to the 8 XCDs round-robin in launch order, so the
   // XCD of a workgroup follows blockIdx.x. Rotating each sequence's splits
@@ -410,14 +516,14 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int it_keys = a.strided ? nsplit * kBlockKeys : kBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
 
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kD;
   // K/V are read through buffer descriptors over the slab that end at the
   // last key a load may need: a load at or past the end fails the hardware
   // range check and returns zeros without a memory access. So the prefetch
   // past the last tile (unconditional, to keep the compiler's wait counts
   // exact) costs no memory round trip for the waits that follow the loop.
   auto slab_rsrc = [&](f16* cache, int end_key) {
-    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kHeadDim * 2),
+    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kD * 2),
                                              kBufferWord3);
   };
 
@@ -432,7 +538,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     const int base = t0 + it * it_keys + wave * kWaveKeys + row;
 #pragma unroll
     for (int j = 0; j < kKpr; ++j) {
-      const uint32_t off = (uint32_t)(base + j * kRows) * (kHeadDim * 2) + col * 16;
+      const uint32_t off = (uint32_t)(base + j * kRows) * (kD * 2) + col * 16;
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
         tl.k[j][i] = __builtin_bit_cast(
@@ -451,7 +557,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   if (has_new) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim + (col + i * kLanes) * 8;
+      const int64_t src = (int64_t)(b * a.n_kv + hkv) * kD + (col + i * kLanes) * 8;
       nk_raw[i] = load_src_run_raw(a.k_new, src, a.new16);
       nv_raw[i] = load_src_run_raw(a.v_new, src, a.new16);
     }
@@ -473,14 +579,14 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 
   // Query registers: this lane's dims of each of the G heads.
   const int h0 = hgrp * G;
-  const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kHeadDim + col * 8;
+  const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kD + col * 8;
   f16x8 q16[kQ16 ? G : 1][kRuns];
   float q32[kQ16 ? 1 : G][kDims];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      const int64_t e = qoff + g * kHeadDim + i * kLanes * 8;
+      const int64_t e = qoff + g * kD + i * kLanes * 8;
       if constexpr (kQ16) {
         q16[g][i] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + e);
       } else {
@@ -531,8 +637,8 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     if (wave == 0 && row < 2 && sub == 0) {
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
-        const int64_t at = slab + (int64_t)pnew * kHeadDim + (col + i * kLanes) * 8;
-        if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kHeadDim, a.status)) {
+        const int64_t at = slab + (int64_t)pnew * kD + (col + i * kLanes) * 8;
+        if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kD, a.status)) {
           f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
           *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
         }
@@ -679,7 +785,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     for (int g = 0; g < G; ++g) {
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
-        f32x4* dst = reinterpret_cast<f32x4*>(&lds_o[(sidx * G + g) * kHeadDim + (col + i * kLanes) * 8]);
+        f32x4* dst = reinterpret_cast<f32x4*>(&lds_o[(sidx * G + g) * kD + (col + i * kLanes) * 8]);
         dst[0] = f32x4{acc[g][i * 8], acc[g][i * 8 + 1], acc[g][i * 8 + 2], acc[g][i * 8 + 3]};
         dst[1] = f32x4{acc[g][i * 8 + 4], acc[g][i * 8 + 5], acc[g][i * 8 + 6], acc[g][i * 8 + 7]};
       }
@@ -691,10 +797,10 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
 
-  store_split_states<G, kO16, kStates>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0, split);
+  store_split_states<G, kO16, kStates, kD>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0, split);
   if (nsplit == 1 || !a.fused_merge) return;
-  merge_on_last_arrival<G, kO16>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
-                                 (int64_t)b * a.n_heads + h0);
+  merge_on_last_arrival<G, kO16, kD>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
+                                     (int64_t)b * a.n_heads + h0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1083,6 +1189,14 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
   merge_row_wave<kO16, 0>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit,
                           (int64_t)gridDim.y * n_heads, records, status);
 }
+template <bool kO16, int kD>
+__global__ __launch_bounds__(64) void decode_merge_hd_kernel(
+    const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+    void* __restrict__ out, int n_heads, int nsplit, int64_t records, int* __restrict__ status) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  merge_row_wave<kO16, 0, kD>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit,
+                              (int64_t)gridDim.y * n_heads, records, status);
+}
 
 // The split workgroup's shape, from sweeps on MI355X (decode-only, per call,
 // 32K / 4K / 153 keys): 4 wavefronts, 16-lane rows, 2 keys per row, 2 tiles
@@ -1093,12 +1207,17 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(
 // (the K/V stream alone, with the compute removed, runs at the rate of a
 // plain read of the same pattern, ~6.2 TB/s), so more work in flight only
 // lengthens the latency of each load.
+// Head size 64 takes 8-lane rows (one 16-byte run per lane), 256 two runs
+// per lane of 16-lane rows.
 using SplitCfg = DecodeCfg<4, 16, 2, 2>;
+template <int kD>
+using SplitCfgD = std::conditional_t<kD == kHeadDim, SplitCfg,
+                                     DecodeShape<4, kD == 64 ? 8 : 16, 2, 2, kD>>;
 
-template <int G, bool kQ16, bool kO16, int kQsub>
+template <int G, bool kQ16, bool kO16, int kQsub, int kD = kHeadDim>
 static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, void* ev_start,
                            void* ev_stop) {
-  using C = SplitCfg;
+  using C = SplitCfgD<kD>;
   dim3 grid((unsigned)a.nsplit, (unsigned)(a.n_kv * kQsub), (unsigned)batch);
   hipError_t e;
   if (ev_start || ev_stop) {
@@ -1114,20 +1233,26 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, v
     e = hipGetLastError();
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
-  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
-      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
+  const dim3 mgrid((unsigned)a.n_heads, (unsigned)batch);
+  if constexpr (kD == kHeadDim)
+    decode_merge_kernel<kO16><<<mgrid, 64, 0, stream>>>(a.part_o, a.part_ml, a.out, a.n_heads,
+                                                        a.nsplit, a.records, a.status);
+  else
+    decode_merge_hd_kernel<kO16, kD><<<mgrid, 64, 0, stream>>>(a.part_o, a.part_ml, a.out,
+                                                               a.n_heads, a.nsplit, a.records,
+                                                               a.status);
   return hipGetLastError();
 }
 
-template <int G, int kQsub = 1>
+template <int G, int kQsub = 1, int kD = kHeadDim>
 static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                             hipStream_t st) {
   const int B = c.batch;
   if (s.q16)
-    return s.o16 ? launch_g<G, true, true, kQsub>(a, B, st, c.ev_start, c.ev_stop)
-                 : launch_g<G, true, false, kQsub>(a, B, st, c.ev_start, c.ev_stop);
-  return s.o16 ? launch_g<G, false, true, kQsub>(a, B, st, c.ev_start, c.ev_stop)
-               : launch_g<G, false, false, kQsub>(a, B, st, c.ev_start, c.ev_stop);
+    return s.o16 ? launch_g<G, true, true, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop)
+                 : launch_g<G, true, false, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop);
+  return s.o16 ? launch_g<G, false, true, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop)
+               : launch_g<G, false, false, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop);
 }
 
 
@@ -1175,8 +1300,46 @@ static hipError_t launch_mfma(const Shape& s, const DecodeArgs& a, const DecodeC
                : launch_mfma_t<G, false, false>(a, B, st, c.ev_start, c.ev_stop);
 }
 
+// Head sizes 64 and 256 (decode_split_kernel only; the matrix-core kernel is
+// built for 128): the same per-query-head rule, then one workgroup per KV
+// head. Group 8 at 256 is not built (its accumulators and query registers
+// would not fit one lane's registers) and takes the general-shape kernels.
+template <int kD>
+static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
+                                   hipStream_t stream) {
+  if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
+    switch (s.group) {
+      case 2: return launch_qo<1, 2, kD>(s, a, c, stream);
+      case 4: return launch_qo<1, 4, kD>(s, a, c, stream);
+      case 5: return launch_qo<1, 5, kD>(s, a, c, stream);
+      case 8:
+        if constexpr (kD == 64) return launch_qo<1, 8, kD>(s, a, c, stream);
+        break;
+      default: break;
+    }
+  }
+  switch (s.group) {
+    case 1: return launch_qo<1, 1, kD>(s, a, c, stream);
+    case 2: return launch_qo<2, 1, kD>(s, a, c, stream);
+    case 4: return launch_qo<4, 1, kD>(s, a, c, stream);
+    case 5: return launch_qo<5, 1, kD>(s, a, c, stream);
+    case 8:
+      if constexpr (kD == 64) return launch_qo<8, 1, kD>(s, a, c, stream);
+      return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool split_decode_shape(int head_dim, int group) {
+  if (head_dim == kHeadDim) return specialised_group(group);
+  if (head_dim == 64) return specialised_group(group);
+  if (head_dim == 256) return specialised_group(group) && group != 8;
+  return false;
+}
+
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                          hipStream_t stream) {
+  if (!split_decode_shape(s.head_dim, s.group)) return hipErrorInvalidValue;
   DecodeArgs a;
   a.q = c.q;
   a.k_cache = static_cast<f16*>(c.k_cache);
@@ -1200,6 +1363,8 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.strided = c.layout == 1;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
+  if (s.head_dim == 64) return launch_decode_hd<64>(s, a, c, stream);
+  if (s.head_dim == 256) return launch_decode_hd<256>(s, a, c, stream);
   // When one workgroup per (sequence, query head, split) fits the chip, each
   // query head gets its own workgroups: a workgroup's time is its serial
   // chain of key iterations, whose compute grows with the heads it serves,

@@ -60,6 +60,10 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
                             int batch, int n_tokens, int* status,
                             hipStream_t stream);
 
+// Shapes launch_decode takes: head size 128, 64 or 256 with a group of 1, 2,
+// 4, 5 or 8 (not 8 at 256).
+bool split_decode_shape(int head_dim, int group);
+
 // nsplit == 1 writes `out` directly; otherwise partial records then a merge.
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                          hipStream_t stream);

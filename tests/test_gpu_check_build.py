@@ -191,14 +191,16 @@ def test_q4_checked_build_matches():
 
 
 
-@pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1), (128, 7, 1), (128, 12, 4)])
+@pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1), (128, 7, 1), (128, 12, 4),
+                                      (64, 8, 2), (256, 10, 2)])
 def test_general_checked_build_matches(Dh, H, Hkv):
     """The general-shape kernels in the checked build: append, decode with
     the workspace filled exactly (max_seq 64 gives H * 256 records, and 256
     forced splits use them all, most with no key), append + decode, and a
     split prefill; nothing flagged, the product build's bits. Groups 7 and 3
     at head_dim 128 take the padded-group route (the group-8 / group-4
-    kernels on padded rows, decode and prefill)."""
+    kernels on padded rows, decode and prefill); head sizes 64 and 256 the
+    split kernel built for them (decode) and the general kernels (prefill)."""
     say("check build general", Dh, H, Hkv)
     cap, B = 64, 1
     prod, chk = _pair(H, Hkv, cap, head_dim=Dh, o_dtype="f32")
@@ -246,4 +248,6 @@ def test_asan_host_driver_on_gpu():
     assert "gpu cycle group 3 head_dim 96" in res.stdout  # the general kernels' host paths
     assert "gpu cycle group 2 head_dim 100" in res.stdout
     assert "gpu cycle group 7 head_dim 128" in res.stdout  # the padded-group route
+    assert "gpu cycle group 4 head_dim 64" in res.stdout  # the split kernel at other head sizes
+    assert "gpu cycle group 5 head_dim 256" in res.stdout
     assert "0 failed so far" in res.stdout.splitlines()[-1]

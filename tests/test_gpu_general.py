@@ -7,6 +7,9 @@ The reference's attention takes head_dim and both head counts as parameters
 kernels' set (head_dim 128 with a group of 1, 2, 4, 5 or 8) run the general
 kernels; these tests cover head sizes that are and are not multiples of 8,
 above 256 (two runs per thread), down to 1, and groups 3, 6, 7 and 12.
+Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
+runs the dot-product split kernel built for those sizes (csrc/nwd_decode.hip);
+test_head_size_split_decode covers its launch forms and knobs.
 
 Bars, as for the specialised path: the append bit-exact (fp16 rows copied,
 fp32 rows rounded to nearest even); attention max-abs <= 2e-3 against the
@@ -35,6 +38,7 @@ SHAPES = [
     (80, 12, 1),    # G 12
     (100, 3, 3),    # single-value runs (100 % 8 != 0)
     (256, 4, 1),    # G 4, 32 runs per row
+    (256, 8, 1),    # G 8 at 256: the general kernels (the split kernel is not built for it)
     (320, 2, 2),    # 40 runs: 6 key groups, 16 threads idle in P.V
     (300, 2, 1),    # single values, 300 > 256 threads: two runs per thread
     (512, 2, 1),    # the largest head size
@@ -90,6 +94,74 @@ def test_general_decode_matches_oracle(D, H, Hkv):
             want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k), f32(v))
             err = max_abs(got[b], want)
             assert err < TOL, (b, err)
+
+
+@pytest.mark.parametrize("D,H,Hkv", [(64, 8, 8), (64, 16, 8), (64, 32, 8), (64, 40, 8),
+                                     (64, 64, 8), (256, 8, 8), (256, 16, 8), (256, 32, 8),
+                                     (256, 20, 4)])
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_head_size_split_decode(D, H, Hkv, io):
+    """Head sizes 64 and 256 on the dot-product split kernel: a batch of one
+    at 3000 keys (one workgroup per query head when batch x heads x splits
+    fits 256 workgroups, else one per KV head) and a ragged batch of three,
+    against the oracle; forced split counts 1, 7 and 64, the in-kernel merge
+    and both key layouts within fp32 rounding of the default; the fused append
+    bit-identical to append + decode in the caches."""
+    g = rng(820 + D + H)
+    lens = [3000, 40, 1333]
+    cap = max(lens) + 2
+    rows = [_rows(g, L, Hkv, D) for L in lens]
+    q = _q(g, (3, H, D), io)
+    kn = g.standard_normal((3, Hkv, D), dtype=np.float32).astype(np.float16)
+    vn = g.standard_normal((3, Hkv, D), dtype=np.float32).astype(np.float16)
+    rt = 2e-3 if io == "f16" else 2e-5
+    with nw.AttnContext(H, Hkv, cap, head_dim=D, max_batch=3, q_dtype=io, o_dtype=io) as ctx:
+        kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+        for batch in (1, 3):
+            say(f"head size {D} {H}q/{Hkv}kv io={io} batch={batch} "
+                f"splits {ctx.decode_splits(batch, max(lens[:batch]))}")
+            pos = pos_tensor([L - 1 for L in lens[:batch]])
+            outs = []
+            for n, merge, layout in ((0, None, None), (1, None, None), (7, None, None),
+                                     (64, None, None), (0, 0, None), (7, 0, None), (7, None, 1),
+                                     (7, None, 0)):
+                ctx.set_decode_splits(n)
+                ctx.set_decode_merge(merge)
+                ctx.set_decode_layout(layout)
+                out = torch.empty((batch, H, D), dtype=_tdtype(io), device="cuda")
+                ctx.decode(dev(q[:batch]), kc, vc, pos, out, batch, max(lens[:batch]))
+                outs.append(host(out).astype(np.float32))
+            assert ctx.device_status() == nw.NWD_OK
+            for b in range(batch):
+                k, v = rows[b]
+                want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k), f32(v))
+                assert max_abs(outs[0][b], want) < TOL, (batch, b)
+            for i, o in enumerate(outs[1:]):
+                assert max_abs(o, outs[0]) < rt, (batch, i)
+        ctx.set_decode_splits(0)
+        ctx.set_decode_merge(None)
+        ctx.set_decode_layout(None)
+        res = []
+        for fused in (True, False):
+            kc2, vc2 = kc.clone(), vc.clone()
+            out = torch.empty((3, H, D), dtype=_tdtype(io), device="cuda")
+            p2 = pos_tensor(lens)
+            if fused:
+                ctx.append_decode(dev(q), dev(kn), dev(vn), kc2, vc2, p2, out, 3, cap)
+            else:
+                ctx.kv_append(dev(kn[:, None]), dev(vn[:, None]), kc2, vc2, p2, 3, 1)
+                ctx.decode(dev(q), kc2, vc2, p2, out, 3, cap)
+            assert ctx.device_status() == nw.NWD_OK
+            res.append((host(out).astype(np.float32), host(kc2).view(np.uint16),
+                        host(vc2).view(np.uint16)))
+        assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+        assert max_abs(res[0][0], res[1][0]) < rt
+        for b, L in enumerate(lens):
+            k_all = np.concatenate([rows[b][0], kn[b][None]], axis=0)
+            v_all = np.concatenate([rows[b][1], vn[b][None]], axis=0)
+            want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k_all), f32(v_all))
+            assert max_abs(res[0][0][b], want) < TOL, b
 
 
 @pytest.mark.parametrize("D,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1)])

@@ -73,12 +73,14 @@ def test_noalloc_matches_context_entry_point():
 
 
 
-def test_noalloc_general_shape_matches_context_entry_point():
-    """The same on a shape of the general kernels (head_dim 96, group 3):
-    its records of 96 floats in the scratch, two calls in a row (the second
-    smaller), bit-identical to nwd_append_decode."""
-    H, Hkv, Dg, cap = 6, 2, 96, 4096
-    g = rng(910)
+@pytest.mark.parametrize("H,Hkv,Dg", [(6, 2, 96), (16, 4, 64), (10, 2, 256)])
+def test_noalloc_general_shape_matches_context_entry_point(H, Hkv, Dg):
+    """The same at other head sizes: the general kernels (head_dim 96, group
+    3) and the split kernel built for head sizes 64 and 256, their records of
+    D floats in the scratch, two calls in a row (the second smaller),
+    bit-identical to nwd_append_decode."""
+    cap = 4096
+    g = rng(910 + Dg)
     cases = [(2, [4000, 1500], 0), (1, [200], 256)]
     with nw.AttnContext(H, Hkv, cap, head_dim=Dg, max_batch=2) as ctx:
         desc = ctx.desc
