@@ -327,6 +327,37 @@ class GeneralWorkload:
         return self.past * self.kv_heads * self.head_dim * 2 * 2
 
 
+class GeneralPrefillWorkload:
+    """Prefill-only calls on a head layout other than the benchmark's: n_new
+    fp16 queries onto `past` cached tokens (the cache already holds the new
+    rows)."""
+
+    def __init__(self, torch, nw, heads: int, kv_heads: int, head_dim: int, past: int,
+                 n_new: int, seed: int = 9):
+        self.heads, self.head_dim, self.past, self.n_new = heads, head_dim, past, n_new
+        cap = past + n_new
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+
+        def rnd(*shape):
+            return torch.randn(*shape, generator=g, device="cuda", dtype=torch.float32).to(torch.float16)
+
+        self.kc, self.vc = rnd(1, kv_heads, cap, head_dim), rnd(1, kv_heads, cap, head_dim)
+        self.q = rnd(1, n_new, heads, head_dim)
+        self.out = torch.empty_like(self.q)
+        self.pos0 = torch.tensor([past], dtype=torch.int32, device="cuda")
+        self.cap = cap
+        self.ctx = nw.AttnContext(heads, kv_heads, cap, head_dim=head_dim)
+
+    def step(self, s: int, stream, append=False):
+        self.ctx.prefill(self.q, self.kc, self.vc, self.pos0, self.out, 1, self.n_new, self.cap,
+                         stream)
+
+    def flops(self) -> float:
+        """QK^T and PV over the real head dims, 2 flops per multiply-add."""
+        return 4.0 * self.heads * self.head_dim * sum(self.past + i + 1 for i in range(self.n_new))
+
+
 def run_general(torch, nw, steps: int = 128, warmup: int = 8):
     """Head layouts other than the benchmark's (head_dim 128 with groups
     1/2/4/5/8): us per decode call (graph-replayed), K/V GB/s and the
@@ -351,6 +382,19 @@ def run_general(torch, nw, steps: int = 128, warmup: int = 8):
         res[name] = {"desc": desc, "us_per_call": us, "kv_bytes": wl.kv_bytes(), "gbs": gbs,
                      "hbm_frac": gbs / HBM_PEAK_GBS, "splits": splits,
                      "us_by_forced_splits": by_splits}
+        log(f"[bench] {name}: {res[name]}")
+        wl.ctx.close()
+        del wl
+        torch.cuda.empty_cache()
+    for name, (heads, kv_heads, head_dim, past, n_new, desc) in GENERAL_PREFILL_SHAPES.items():
+        log(f"[bench] {name}: {heads}q/{kv_heads}kv/d{head_dim}, {n_new} onto {past}")
+        wl = GeneralPrefillWorkload(torch, nw, heads, kv_heads, head_dim, past, n_new)
+        warm_up(torch, wl, 0.1, append=False)
+        _, ms = time_graph(torch, wl, 16, 2, append=False, reps=3)
+        us = ms * 1e3 / 16
+        tflops = wl.flops() / (us * 1e-6) / 1e12
+        res[name] = {"desc": desc, "us_per_call": us, "tflops": tflops,
+                     "mfma_frac": tflops / MFMA_F16_PEAK_TFLOPS}
         log(f"[bench] {name}: {res[name]}")
         wl.ctx.close()
         del wl
@@ -694,6 +738,15 @@ GENERAL_SHAPES = {
                        "Phi-3-mini layout), 4096 keys, fp16 I/O, decode call"),
     "general-d64-16k": (32, 8, 64, 16384, "B=1, 32q/8kv/d64 (group 4, head size 64: the "
                         "Llama-3.2-1B layout), 16384 keys, fp16 I/O, decode call"),
+}
+# Prefill on other head layouts: (heads, kv heads, head_dim, past, new tokens, description).
+GENERAL_PREFILL_SHAPES = {
+    "general-prefill-d64": (32, 8, 64, 8192, 512, "B=1, 32q/8kv/d64 (Llama-3.2-1B layout), 512 "
+                            "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
+                            "padded to 128 dims)"),
+    "general-prefill-d96": (32, 32, 96, 8192, 512, "B=1, 32q/32kv/d96 (Phi-3-mini layout), 512 "
+                            "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
+                            "padded to 128 dims)"),
 }
 
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,

@@ -73,10 +73,13 @@ typedef struct nwd_desc {
                           (buffers allocated by nwd_create); decodes at
                           D = 64 (G 1, 2, 4, 5, 8) and D = 256 (G 1, 2, 4, 5)
                           run the dot-product split kernel built for those
-                          sizes; every other (D, G), and prefill at D other
-                          than 128, runs the general kernels, with the same
-                          contract and cache layout (a coverage path, not
-                          tuned like the others)                             */
+                          sizes (G 3, 6, 7 padded where the padded group is
+                          built); prefills at D below 128 and a multiple of
+                          8 run the MFMA prefill kernel on rows padded to
+                          128 dims (G 3, 6, 7 through padded query rows);
+                          every other (D, G) runs the general kernels, with
+                          the same contract and cache layout (a coverage
+                          path, not tuned like the others)                   */
   int32_t max_seq;     /* cache capacity in tokens per sequence, at most
                           4194304 (2^22)                                    */
   int32_t max_batch;   /* sequences per call                                */
@@ -191,8 +194,9 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * accumulation: an fp16 q enters exact and its scores are scaled in fp32;
  * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
  * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
- * makes nwd_device_status report NWD_ERR_DEVICE (groups 3, 6, 7 at D = 128
- * run these kernels on padded query rows, in sub-chunks). The general shapes
+ * makes nwd_device_status report NWD_ERR_DEVICE (head sizes below 128 run
+ * these kernels on rows padded with zeros to 128 dims, and groups 3, 6, 7
+ * on padded query rows, in sub-chunks). The shapes of the general kernels
  * (see nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
  * outside the cache (pos0[b] < 0 or pos0[b] + n_new > max_seq) is flagged in
  * the device status and run at the nearest valid pos0. max_len bounds

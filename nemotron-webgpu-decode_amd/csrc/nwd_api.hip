@@ -156,8 +156,26 @@ enum DecodeRoute { kRouteSpecialised = 0, kRoutePadded = 1, kRouteGeneral = 2 };
 
 DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
   if (nwd::split_decode_shape(s.head_dim, s.group)) return kRouteSpecialised;
-  if (have_pad && nwd::padded_group(s.group) > 0 && s.head_dim == nwd::kHeadDim) return kRoutePadded;
+  if (have_pad && nwd::padded_decode_shape(s.head_dim, s.group)) return kRoutePadded;
   return kRouteGeneral;
+}
+
+// Prefill: the MFMA prefill kernel at head size 128 and the multiples of 8
+// below it (rows padded with zeros to 128 dims) with groups 1, 2, 4, 5, 8,
+// and groups 3, 6, 7 there through padded query rows; the general kernels
+// otherwise. 512 tokens onto 8192 on MI355X, per call, against the general
+// kernels: 32q/8kv/d64 77.6 against 1640 us, 32q/32kv/d96 79.1 against 7738.
+DecodeRoute prefill_route(const nwd::Shape& s, bool have_pad) {
+  if (!nwd::prefill_head_dim(s.head_dim)) return kRouteGeneral;
+  if (nwd::specialised_group(s.group)) return kRouteSpecialised;
+  if (have_pad && nwd::padded_group(s.group) > 0) return kRoutePadded;
+  return kRouteGeneral;
+}
+
+// Whether a context of this shape gets the padded-row buffers.
+bool wants_pad_buffers(int head_dim, int group) {
+  return nwd::padded_group(group) > 0 &&
+         (nwd::padded_decode_shape(head_dim, group) || nwd::prefill_head_dim(head_dim));
 }
 
 int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
@@ -225,9 +243,6 @@ nwd::Shape shape_of(const nwd_desc* d) {
   sh.kv16 = d->kv_dtype == NWD_F16;
   sh.qk_scale = d->scale > 0.f ? d->scale : 1.0f / std::sqrt((float)d->head_dim);
   sh.head_dim = d->head_dim;
-  // D = 128 with a group of 1, 2, 4, 5 or 8 runs the specialised kernels
-  // (nwd_decode.hip, nwd_prefill.hip); every other shape the general ones.
-  sh.general = d->head_dim != nwd::kHeadDim || !nwd::specialised_group(sh.group);
   return sh;
 }
 
@@ -349,10 +364,10 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
   const int gp = nwd::padded_group(group);
-  if (e == hipSuccess && gp > 0 && d->head_dim == nwd::kHeadDim) {
+  if (e == hipSuccess && wants_pad_buffers(d->head_dim, group)) {
     // Padded rows of up to 512 prefill tokens per sub-chunk, within 32 MiB
     // per buffer (at least one token: the decode's rows).
-    const size_t per_token = (size_t)d->max_batch * d->n_kv_heads * gp * nwd::kHeadDim * sizeof(float);
+    const size_t per_token = (size_t)d->max_batch * d->n_kv_heads * gp * d->head_dim * sizeof(float);
     size_t tokens = ((size_t)32 << 20) / per_token;
     if (tokens > 512) tokens = 512;
     if (tokens > (size_t)d->max_seq) tokens = (size_t)d->max_seq;
@@ -637,11 +652,12 @@ int nwd_prefill_attn(nwd_ctx* ctx, const void* q, const void* k_cache, const voi
     return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: max_len %d outside [n_new, max_seq=%d]",
                 len, ctx->desc.max_seq);
   hipError_t e;
-  if (decode_route(ctx->shape, ctx->q_pad != nullptr) == kRoutePadded) {
+  const DecodeRoute route = prefill_route(ctx->shape, ctx->q_pad != nullptr);
+  if (route == kRoutePadded) {
     nwd::PadBuffers pb{ctx->q_pad, ctx->out_pad, ctx->pos_sub, ctx->pad_tokens};
     e = nwd::launch_padded_prefill(ctx->shape, q, k_cache, v_cache, pos0, out, batch, n_new, len,
                                    ctx->ws, pb, (hipStream_t)stream);
-  } else if (ctx->shape.general) {
+  } else if (route == kRouteGeneral) {
     const int64_t rows = (int64_t)batch * n_new * ctx->desc.n_heads;
     if (rows > 0x7FFFFFFF)
       return fail(ctx, NWD_ERR_CAPACITY, "nwd_prefill_attn: %lld output rows exceed 2^31 - 1",

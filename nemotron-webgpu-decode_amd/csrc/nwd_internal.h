@@ -17,7 +17,6 @@ struct Shape {
   int kv16;        // new K/V rows are fp16 (else fp32)
   float qk_scale;  // softmax scale (1/sqrt(D) by default)
   int head_dim;    // D
-  int general;     // D or the group is outside the specialised kernels' set
 };
 
 // Head sizes the general-shape kernels take (sparse_attn.wgsl:12-17 takes
@@ -75,6 +74,10 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
 // B = 32: 13.4 against 7.2 (B = 1-8 gain or tie).
 constexpr int kSubSplitMaxWorkgroups = 256;
 
+// Head sizes launch_prefill takes: 128, and the multiples of 8 below it
+// (rows padded with zeros to 128 dims).
+bool prefill_head_dim(int head_dim);
+
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,
                           int batch, int n_new, int max_len, const Workspace& ws,
@@ -83,19 +86,22 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
 // Largest decode split count supported for `batch` sequences by `ws`.
 int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
-// Groups of 3, 6 and 7 query heads at D = 128 run the decode kernels as
-// groups of 4, 8 and 8 (padded_group, 0 for other groups), their query rows
-// copied into a padded layout (q_pad, [batch][Hkv][padded group][128], the
+// Groups of 3, 6 and 7 query heads run the decode kernels as groups of 4, 8
+// and 8 (padded_group, 0 for other groups) where launch_decode takes the
+// padded group at the head size (padded_decode_shape), their query rows
+// copied into a padded layout (q_pad, [batch][Hkv][padded group][D], the
 // call's q dtype) and the real rows copied out of out_pad afterwards.
 int padded_group(int group);
+bool padded_decode_shape(int head_dim, int group);
 Shape padded_shape(const Shape& s);
 hipError_t launch_padded_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
                                 void* q_pad, void* out_pad, hipStream_t stream);
 
-// The prefill of those groups on the prefill kernels of groups 4 / 8: the
-// chunk goes through in sub-chunks of chunk_tokens tokens, each padded into
-// q_pad ([batch][chunk_tokens][Hkv][padded group][128]), its first positions
-// in pos_sub ([batch]), its output unpadded from out_pad.
+// The prefill of those groups on the prefill kernels of groups 4 / 8 (head
+// sizes prefill_head_dim takes): the chunk goes through in sub-chunks of
+// chunk_tokens tokens, each padded into q_pad
+// ([batch][chunk_tokens][Hkv][padded group][D]), its first positions in
+// pos_sub ([batch]), its output unpadded from out_pad.
 struct PadBuffers {
   void* q_pad;
   void* out_pad;

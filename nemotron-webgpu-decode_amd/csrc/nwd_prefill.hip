@@ -59,6 +59,12 @@
 // records to the context's workspace (o / sum in fp16 when the output is
 // fp16, o in fp32 otherwise), and prefill_merge_kernel combines them; with
 // one split the workgroup writes O directly.
+// Head sizes below 128 (multiples of 8) run the same kernel on rows padded
+// with zeros to 128 dims (prefill_pad_kernel): the query's and the K/V
+// rows' missing 16-byte chunks read as zeros (the copies' offsets pushed
+// past the buffer range), so the scores are those of the real dims, the
+// padded dims of O come out zero and are not stored. The MFMA work is that
+// of head size 128.
 #include <atomic>
 
 #include "nwd_common.h"
@@ -131,6 +137,7 @@ struct PrefillArgs {
   int batch, n_heads, n_kv, cap, n_new, mtiles, nsplit;
   float qk_scale_log2;
   int* status;
+  int head_dim;     // D (prefill_pad_kernel; 128 in prefill_kernel)
 };
 
 // LDS of a workgroup: K0 K1 V0 V1 tiles, 32 KB each; with fp32 queries also
@@ -140,10 +147,13 @@ constexpr int kQloOffset = 4 * kTileBytes;
 template <bool kQ16>
 constexpr size_t prefill_lds_bytes() { return (size_t)(kQ16 ? 4 : 5) * kTileBytes; }
 
-template <int G, bool kQ16, bool kO16>
-__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs a) {
+// The body of prefill_kernel (kPadD false: D = 128) and prefill_pad_kernel
+// (kPadD: D = a.head_dim, a multiple of 8 below 128, rows padded to 128).
+template <int G, bool kQ16, bool kO16, bool kPadD>
+__device__ __forceinline__ void prefill_body(const PrefillArgs a) {
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
   char* lds = reinterpret_cast<char*>(smem);
+  const int D = kPadD ? a.head_dim : kHeadDim;
 
   const int id = blockIdx.x;
   const int hkv = id % a.n_kv;
@@ -193,11 +203,11 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
     qi[rb] = ok ? R / G : 0;
     gq[rb] = ok ? R - qi[rb] * G : 0;
     lim[rb] = ok ? P0 + qi[rb] : -1;
-    const int64_t qrow = (((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * kHeadDim;
+    const int64_t qrow = (((int64_t)b * a.n_new + qi[rb]) * a.n_heads + hkv * G + gq[rb]) * D;
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       f16x8 lo{};
-      if (ok) {
+      if (ok && (!kPadD || db * 32 + 8 * lq < D)) {
         load_q8<kQ16>(a.q, qrow + db * 32 + 8 * lq, c, qf[rb][db], lo, q_range);
       } else {
 #pragma unroll
@@ -212,11 +222,11 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   const bool wave_has_pad = r0 + 31 >= total_rows;
   const int wave_min_lim = P0 + r0 / G;
 
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * D;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.k_cache + slab), 0,
-                                                    kend_s * (kHeadDim * 2), kBufferWord3);
+                                                    kend_s * (D * 2), kBufferWord3);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.v_cache + slab), 0,
-                                                    kend_s * (kHeadDim * 2), kBufferWord3);
+                                                    kend_s * (D * 2), kBufferWord3);
   // Staging: wave w copies rows 16w .. 16w+15 of a tile, 4 rows (1 KB) per
   // instruction: lane l fills physical chunk l & 15 of row 16w + 4i + l/16
   // and so loads the logical chunk the swizzle puts there. Rows past the
@@ -227,15 +237,25 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   // Copy j of this wave's part of tile kt into buffer bb: j < kStageInsts
   // are K rows, the rest V rows. `oob` (0 or 2^31) pushes the offset past
   // the range, which makes the copy a no-op read of zeros.
+  // With kPadD a row holds D * 2 bytes in memory, and the chunks at or past
+  // it are pushed out of range too (they would read the next row).
   auto stage = [&](int kt, int bb, int j, uint32_t oob) {
     const int i = j % kStageInsts;
     const bool kpart = j < kStageInsts;
     const int row = st_row + 4 * i;
-    const uint32_t rb_off = (uint32_t)(kt * kPBN + row) * kRowBytes + oob;
-    char* dst = lds + ((kpart ? 0 : 2) + bb) * kTileBytes + wv * 16 * kRowBytes + i * 1024;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(kpart ? rk : rv, (lds_void*)dst, 16,
-                                             rb_off + ((st_p ^ (kpart ? kswz(row) : vswz(row))) << 4),
-                                             0, 0, 0);
+    if constexpr (kPadD) {
+      char* dst = lds + ((kpart ? 0 : 2) + bb) * kTileBytes + wv * 16 * kRowBytes + i * 1024;
+      const int lc = st_p ^ (kpart ? kswz(row) : vswz(row));  // logical chunk
+      const uint32_t off = ((uint32_t)(kt * kPBN + row) * (uint32_t)(D * 2) + (lc << 4)) |
+                           (8 * lc >= D ? 0x80000000u : oob);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kpart ? rk : rv, (lds_void*)dst, 16, off, 0, 0, 0);
+    } else {
+      const uint32_t rb_off = (uint32_t)(kt * kPBN + row) * kRowBytes + oob;
+      char* dst = lds + ((kpart ? 0 : 2) + bb) * kTileBytes + wv * 16 * kRowBytes + i * 1024;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(kpart ? rk : rv, (lds_void*)dst, 16,
+                                               rb_off + ((st_p ^ (kpart ? kswz(row) : vswz(row))) << 4),
+                                               0, 0, 0);
+    }
   };
   auto load_tile = [&](int kt, int bb) {
 #pragma unroll
@@ -458,7 +478,8 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
         f32x4 r = o[rb][dblk] * a0;
 #pragma unroll
         for (int e = 0; e < 4; ++e) r[e] = fmaf(x[2 + dblk * 4 + e], a1, r[e]);
-        store_o4<kO16>(a.out, grow * kHeadDim + dblk * 16 + 4 * lq, r * inv);
+        if (kPadD && dblk * 16 + 4 * lq >= D) continue;  // a padded dim
+        store_o4<kO16>(a.out, grow * D + dblk * 16 + 4 * lq, r * inv);
       }
     } else {
       // This split's record: (M, lt) and o. With an fp16 output, o is
@@ -482,21 +503,31 @@ __global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs
   }
 }
 
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kPThreads, 1) void prefill_kernel(const PrefillArgs a) {
+  prefill_body<G, kQ16, kO16, false>(a);
+}
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kPThreads, 1) void prefill_pad_kernel(const PrefillArgs a) {
+  prefill_body<G, kQ16, kO16, true>(a);
+}
+
 // out[row] = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M) over the
 // row's split records, merged in one pass (online maximum) so every load is
 // independent of the others; 32 threads per row, 4 dims each. With kO16 the
 // records hold o_s / l_s in fp16 (see prefill_kernel) and are weighted by
 // l_s 2^(m_s - M).
-template <bool kO16>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
-                                                            const float2* __restrict__ part_ml,
-                                                            void* __restrict__ out, int64_t rows,
-                                                            int nsplit, int64_t records,
-                                                            int* status) {
+// Records hold 128 dims at every head size (zeros past D); the output rows
+// hold D.
+template <bool kO16, bool kPadD>
+__device__ __forceinline__ void prefill_merge_body(const float* __restrict__ part_o,
+                                                   const float2* __restrict__ part_ml,
+                                                   void* __restrict__ out, int64_t rows, int nsplit,
+                                                   int64_t records, int* status, int D) {
   const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int64_t row = t >> 5;
   const int d4 = t & 31;
-  if (row >= rows) return;
+  if (row >= rows || (kPadD && d4 * 4 >= D)) return;
   if (!in_bounds(row * nsplit, nsplit, records, status)) return;
   float M = kNegBig, L = 0.f;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -525,8 +556,23 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restr
     acc = acc * sc + ov * w;
     M = Mn;
   }
-  if (!in_bounds(row * kHeadDim + d4 * 4, 4, rows * kHeadDim, status)) return;
-  store_o4<kO16>(out, row * kHeadDim + d4 * 4, acc * (1.f / L));
+  if (!in_bounds(row * D + d4 * 4, 4, rows * D, status)) return;
+  store_o4<kO16>(out, row * D + d4 * 4, acc * (1.f / L));
+}
+
+template <bool kO16>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(const float* __restrict__ part_o,
+                                                            const float2* __restrict__ part_ml,
+                                                            void* __restrict__ out, int64_t rows,
+                                                            int nsplit, int64_t records,
+                                                            int* status) {
+  prefill_merge_body<kO16, false>(part_o, part_ml, out, rows, nsplit, records, status, kHeadDim);
+}
+template <bool kO16>
+__global__ __launch_bounds__(256) void prefill_merge_pad_kernel(
+    const float* __restrict__ part_o, const float2* __restrict__ part_ml, void* __restrict__ out,
+    int64_t rows, int nsplit, int64_t records, int* status, int D) {
+  prefill_merge_body<kO16, true>(part_o, part_ml, out, rows, nsplit, records, status, D);
 }
 
 static_assert(prefill_lds_bytes<true>() >= (size_t)4 * 64 * kRB * 34 * sizeof(float),
@@ -556,11 +602,11 @@ static int prefill_splits(int64_t row_tiles, int64_t rows, int max_len, const Wo
   return n < 1 ? 1 : (int)n;
 }
 
-template <int G, bool kQ16, bool kO16>
+template <int G, bool kQ16, bool kO16, bool kPadD>
 static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
                                    int max_len, const Workspace& ws, hipStream_t stream) {
-  auto kern = prefill_kernel<G, kQ16, kO16>;
+  auto kern = kPadD ? prefill_pad_kernel<G, kQ16, kO16> : prefill_kernel<G, kQ16, kO16>;
   constexpr size_t kPrefillLds = prefill_lds_bytes<kQ16>();
   // The dynamic LDS size exceeds the 64 KB default: raise the kernel's limit
   // once per device (the attribute is per device).
@@ -588,6 +634,7 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
   a.mtiles = (n_new * G + kPBM - 1) / kPBM;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
+  a.head_dim = s.head_dim;
   const int64_t row_tiles = (int64_t)a.mtiles * s.n_kv * batch;
   const int64_t rows = (int64_t)n_new * s.n_heads * batch;
   const int nsplit = prefill_splits(row_tiles, rows, max_len, ws);
@@ -600,26 +647,45 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || nsplit == 1) return e;
   const unsigned blocks = (unsigned)((rows * 32 + 255) / 256);
-  prefill_merge_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows, nsplit,
-                                                                 ws.records, ws.status);
+  if constexpr (kPadD)
+    prefill_merge_pad_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows,
+                                                                nsplit, ws.records, ws.status,
+                                                                s.head_dim);
+  else
+    prefill_merge_kernel<kO16><<<blocks, 256, 0, stream>>>(ws.part_o, ws.part_ml, out, rows, nsplit,
+                                                           ws.records, ws.status);
   return hipGetLastError();
+}
+
+template <int G, bool kPadD>
+static hipError_t launch_prefill_p(const Shape& s, const void* q, const void* kc, const void* vc,
+                                   const int32_t* pos0, void* out, int batch, int n_new,
+                                   int max_len, const Workspace& ws, hipStream_t stream) {
+  if (s.q16)
+    return s.o16 ? launch_prefill_t<G, true, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
+                 : launch_prefill_t<G, true, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+  return s.o16 ? launch_prefill_t<G, false, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
+               : launch_prefill_t<G, false, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
 }
 
 template <int G>
 static hipError_t launch_prefill_g(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
                                    int max_len, const Workspace& ws, hipStream_t stream) {
-  if (s.q16)
-    return s.o16 ? launch_prefill_t<G, true, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
-                 : launch_prefill_t<G, true, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
-  return s.o16 ? launch_prefill_t<G, false, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
-               : launch_prefill_t<G, false, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+  if (s.head_dim == kHeadDim)
+    return launch_prefill_p<G, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+  return launch_prefill_p<G, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+}
+
+bool prefill_head_dim(int head_dim) {
+  return head_dim == kHeadDim || (head_dim >= 8 && head_dim < kHeadDim && head_dim % 8 == 0);
 }
 
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,
                           int batch, int n_new, int max_len, const Workspace& ws,
                           hipStream_t stream) {
+  if (!prefill_head_dim(s.head_dim)) return hipErrorInvalidValue;
   switch (s.group) {
     case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
     case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);

@@ -9,7 +9,9 @@ kernels; these tests cover head sizes that are and are not multiples of 8,
 above 256 (two runs per thread), down to 1, and groups 3, 6, 7 and 12.
 Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
 runs the dot-product split kernel built for those sizes (csrc/nwd_decode.hip);
-test_head_size_split_decode covers its launch forms and knobs.
+test_head_size_split_decode covers its launch forms and knobs. Prefill at
+head sizes below 128 that are multiples of 8 runs the MFMA prefill kernel on
+rows padded to 128 dims (test_padded_head_prefill).
 
 Bars, as for the specialised path: the append bit-exact (fp16 rows copied,
 fp32 rows rounded to nearest even); attention max-abs <= 2e-3 against the
@@ -280,6 +282,38 @@ def test_general_prefill_matches_token_by_token(D, H, Hkv, splits):
         for i in range(n_new):
             L = pos0[b] + i + 1
             want = oracle.sparse_attn_f32(q[b, i], f32(k[:L]), f32(v[:L]))
+            worst = max(worst, max_abs(got[b, i], want))
+    say(f"  max-abs {worst:.2e}")
+    assert worst < TOL
+
+
+@pytest.mark.parametrize("D,H,Hkv", [(64, 32, 8), (64, 8, 8), (96, 10, 2), (32, 16, 2),
+                                     (120, 4, 2), (64, 6, 2), (96, 7, 1)])
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_padded_head_prefill(D, H, Hkv, io):
+    """Head sizes below 128 (multiples of 8) prefill on the MFMA prefill
+    kernel with rows padded to 128 dims (groups 3 and 7 also through padded
+    query rows): two sequences, pos0 1500 (several key tiles, split over
+    workgroups and merged) and 3, 40 new tokens; every row against the
+    oracle's decode over keys 0..pos0+i."""
+    say(f"padded-head prefill D={D} H={H} Hkv={Hkv} io={io}")
+    g = rng(860 + D + H)
+    n_new, pos0 = 40, [1500, 3]
+    B, cap = 2, 1600
+    rows = [_rows(g, p + n_new, Hkv, D, scale=0.5) for p in pos0]
+    q = _q(g, (B, n_new, H, D), io)
+    with nw.AttnContext(H, Hkv, cap, head_dim=D, max_batch=B, q_dtype=io, o_dtype=io) as ctx:
+        kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+        out = torch.empty((B, n_new, H, D), dtype=_tdtype(io), device="cuda")
+        ctx.prefill(dev(q), kc, vc, pos_tensor(pos0), out, B, n_new, max(pos0) + n_new)
+        assert ctx.device_status() == nw.NWD_OK
+        got = host(out).astype(np.float32)
+    worst = 0.0
+    for b, (k, v) in enumerate(rows):
+        for i in range(n_new):
+            L = pos0[b] + i + 1
+            want = oracle.sparse_attn_f32(q[b, i].astype(np.float32), f32(k[:L]), f32(v[:L]))
             worst = max(worst, max_abs(got[b, i], want))
     say(f"  max-abs {worst:.2e}")
     assert worst < TOL
