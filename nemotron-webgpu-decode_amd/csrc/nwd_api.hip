@@ -149,12 +149,24 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 // keys, 17.3 at 32768; 24q/8kv (group 3): 10.0 against 14.0 at 1024 keys,
 // 28.2 at 32768. The prefill of these groups runs the prefill kernels the
 // same way. The allocation-free entry point, which has no padded buffers,
-// uses the general kernels. Decode at head size 64 (groups 1, 2, 4, 5, 8)
-// and 256 (groups 1, 2, 4, 5) runs the dot-product split kernel built for
-// those sizes; their prefill runs the general kernels.
+// uses the general kernels. Decode at head sizes 64 and 256 runs the
+// dot-product split kernel built for them, and at the other multiples of 8
+// up to 256 that kernel's padded form (groups 1, 2, 4, 5, and 8 up to 128).
+// Decode calls on MI355X, B = 1, against the general kernels: 32q/32kv/d96
+// at 4096 keys 12.0 against 16.3 us, 32q/32kv/d80 11.6 against 15.0,
+// 16q/8kv/d192 at 8192 keys 14.0 against 20.6, 64q/8kv/d120 15.5 against
+// 30.3.
 enum DecodeRoute { kRouteSpecialised = 0, kRoutePadded = 1, kRouteGeneral = 2 };
 
+// The split kernels address a (sequence, KV head) slab with 32-bit byte
+// offsets through buffer descriptors, so a slab may hold at most 1 GiB
+// (head sizes above 128 with a longer max_seq take the general kernels).
+bool slab_fits(const nwd::Shape& s) {
+  return (int64_t)s.cap * s.head_dim * 2 <= ((int64_t)1 << 30);
+}
+
 DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
+  if (!slab_fits(s)) return kRouteGeneral;
   if (nwd::split_decode_shape(s.head_dim, s.group)) return kRouteSpecialised;
   if (have_pad && nwd::padded_decode_shape(s.head_dim, s.group)) return kRoutePadded;
   return kRouteGeneral;

@@ -76,6 +76,15 @@ struct DecodeShape {
   static constexpr int kBlockKeys = kW * kWaveKeys;
   static_assert(kL == 8 || kL == 16, "rows of 8 or 16 lanes");
   static_assert(kD % (8 * kL) == 0, "whole 16-byte runs per lane");
+  static constexpr bool kPadD = false;
+};
+// The same workgroup for rows of fewer dims (a multiple of 8 below kD, the
+// call's head_dim): the 16-byte runs past a row's dims load as zeros (their
+// offsets pushed past the buffer range) and are not stored, so the scores
+// and outputs are those of the real dims; records keep kD dims.
+template <int kW, int kL, int kKpr_, int kT, int kD_>
+struct DecodePadShape : DecodeShape<kW, kL, kKpr_, kT, kD_> {
+  static constexpr bool kPadD = true;
 };
 // The head-128 form.
 template <int kW, int kL, int kKpr_, int kT>
@@ -182,11 +191,11 @@ constexpr int kMergePass = 32;
 // against 9.0, 40q/8kv at 32K 24.7 against 25.1.)
 // The same for head sizes other than 128 (kD / 64 dims per lane, one
 // 4-, 8- or 16-byte load per split and lane).
-template <bool kO16, int kPolicy, int kD>
+template <bool kO16, int kPolicy, int kD, bool kPadD>
 __device__ inline void merge_row_wave_d(const float* __restrict__ part_o,
                                         const float2* __restrict__ part_ml, void* __restrict__ out,
                                         int64_t row, int nsplit, int64_t out_rows, int64_t records,
-                                        int* status) {
+                                        int* status, int od) {
   constexpr int kDL = kD / 64;  // dims per lane
   static_assert(kDL == 1 || kDL == 4, "head size 64 or 256");
   const int lane = threadIdx.x & 63;
@@ -231,8 +240,9 @@ __device__ inline void merge_row_wave_d(const float* __restrict__ part_o,
     M = mn;
   }
   const float inv = 1.f / L;
-  const int64_t at = row * kD + kDL * lane;
-  if (!in_bounds(at, kDL, out_rows * kD, status)) return;
+  if (kPadD && kDL * lane >= od) return;  // padded dims
+  const int64_t at = row * od + kDL * lane;
+  if (!in_bounds(at, kDL, out_rows * od, status)) return;
 #pragma unroll
   for (int i = 0; i < kDL; ++i) {
     if constexpr (kO16) static_cast<f16*>(out)[at + i] = (f16)(acc[i] * inv);
@@ -240,13 +250,15 @@ __device__ inline void merge_row_wave_d(const float* __restrict__ part_o,
   }
 }
 
-template <bool kO16, int kPolicy, int kD = kHeadDim>
+// od: the output rows' width (kD, or the padded form's head_dim).
+template <bool kO16, int kPolicy, int kD = kHeadDim, bool kPadD = false>
 __device__ inline void merge_row_wave(const float* __restrict__ part_o,
                                       const float2* __restrict__ part_ml, void* __restrict__ out,
                                       int64_t row, int nsplit, int64_t out_rows, int64_t records,
-                                      int* status) {
+                                      int* status, int od = kD) {
   if constexpr (kD != kHeadDim) {
-    merge_row_wave_d<kO16, kPolicy, kD>(part_o, part_ml, out, row, nsplit, out_rows, records, status);
+    merge_row_wave_d<kO16, kPolicy, kD, kPadD>(part_o, part_ml, out, row, nsplit, out_rows,
+                                                records, status, od);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -284,8 +296,9 @@ __device__ inline void merge_row_wave(const float* __restrict__ part_o,
     M = mn;
   }
   const float inv = 1.f / L;
-  const int64_t at = row * kHeadDim + 2 * lane;
-  if (!in_bounds(at, 2, out_rows * kHeadDim, status)) return;
+  if (kPadD && 2 * lane >= od) return;  // padded dims
+  const int64_t at = row * od + 2 * lane;
+  if (!in_bounds(at, 2, out_rows * od, status)) return;
   if constexpr (kO16) {
     f16x2 v;
     v[0] = (f16)(a0 * inv);
@@ -315,6 +328,7 @@ struct DecodeArgs {
   int fused_merge;    // merge in the split kernel's last workgroup
   float qk_scale_log2;
   int* status;
+  int head_dim;       // D of the rows in memory (a DecodePadShape kernel's; kD otherwise)
 };
 
 // Record stores of the in-kernel merge write through to memory (agent
@@ -332,9 +346,10 @@ template <int kN>
 using f32xn = float __attribute__((ext_vector_type(kN)));
 template <int kN>
 using f16xn = f16 __attribute__((ext_vector_type(kN)));
-template <int G, bool kO16, int kStates, int kD = kHeadDim>
+template <int G, bool kO16, int kStates, int kD = kHeadDim, bool kPadD = false>
 __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_o,
-                                          const float* lds_ml, int64_t hrow0, int split) {
+                                          const float* lds_ml, int64_t hrow0, int split,
+                                          int od = kD) {
   constexpr int kR = kD / 32;  // dims per thread: 2, 4 or 8
   static_assert(kR == 2 || kR == 4 || kR == 8, "head size 64, 128 or 256");
   using vec = f32xn<kR>;
@@ -356,8 +371,10 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
     const int64_t out_rows = (int64_t)a.batch * a.n_heads;
     if (nsplit == 1) {
       const float inv = 1.f / lt;
-      const int64_t at = (hrow0 + g) * kD + d4 * kR;
-      if (!in_bounds(at, kR, out_rows * kD, a.status)) {
+      const int64_t at = (hrow0 + g) * od + d4 * kR;
+      if (kPadD && d4 * kR >= od) {
+        // a padded run: nothing to store
+      } else if (!in_bounds(at, kR, out_rows * od, a.status)) {
         // (bounds-checked builds only) the store is dropped
       } else if constexpr (kO16) {
         f16xn<kR> v;
@@ -429,7 +446,7 @@ __device__ inline void store_split_states(const DecodeArgs& a, const float* lds_
 // barrier that precedes the ticket, and the acquire to the sc1 loads in
 // merge_row_wave, which are issued only after the ticket has returned (they
 // depend on it through lds_last). Wavefront w merges heads w, w + waves, ...
-template <int G, bool kO16, int kD = kHeadDim>
+template <int G, bool kO16, int kD = kHeadDim, bool kPadD = false>
 __device__ inline void merge_on_last_arrival(const DecodeArgs& a, int* counter, int64_t hrow0) {
   __shared__ int lds_last;
   wait_vm();
@@ -441,8 +458,9 @@ __device__ inline void merge_on_last_arrival(const DecodeArgs& a, int* counter, 
   __syncthreads();
   if (!lds_last) return;
   for (int g = (int)threadIdx.x >> 6; g < G; g += (int)blockDim.x >> 6)
-    merge_row_wave<kO16, kRecPolicy, kD>(a.part_o, a.part_ml, a.out, hrow0 + g, a.nsplit,
-                                         (int64_t)a.batch * a.n_heads, a.records, a.status);
+    merge_row_wave<kO16, kRecPolicy, kD, kPadD>(a.part_o, a.part_ml, a.out, hrow0 + g, a.nsplit,
+                                                (int64_t)a.batch * a.n_heads, a.records, a.status,
+                                                kPadD ? a.head_dim : kD);
   if (threadIdx.x == 0)
     __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -465,6 +483,9 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   constexpr int kKpr = C::kKpr, kBlockKeys = C::kBlockKeys, kWaveKeys = C::kWaveKeys;
   constexpr int kTiles = C::kTiles;
   constexpr int kD = C::kD;
+  constexpr bool kPadD = C::kPadD;
+  // Row width in memory: kD, or the call's head size in the padded form.
+  const int Dm = kPadD ? a.head_dim : kD;
   static_assert(G * 32 <= kThreads, "one run of each head per thread");
   // Row states written to LDS per wavefront (see the end of the kernel). The
   // rule depends on the shape's group size, not on the heads this
@@ -516,16 +537,26 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int it_keys = a.strided ? nsplit * kBlockKeys : kBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
 
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kD;
+  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * Dm;
   // K/V are read through buffer descriptors over the slab that end at the
   // last key a load may need: a load at or past the end fails the hardware
   // range check and returns zeros without a memory access. So the prefetch
   // past the last tile (unconditional, to keep the compiler's wait counts
   // exact) costs no memory round trip for the waits that follow the loop.
   auto slab_rsrc = [&](f16* cache, int end_key) {
-    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kD * 2),
+    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (Dm * 2),
                                              kBufferWord3);
   };
+
+  // Byte offset of this lane's run i of a row at `off`; a padded run's is
+  // pushed past the buffer range (the load returns zeros).
+  auto run_off = [&](uint32_t off, int i) -> uint32_t {
+    const uint32_t o = off + i * kLanes * 16;
+    if constexpr (kPadD) return (col + i * kLanes) * 8 >= Dm ? o | 0x80000000u : o;
+    return o;
+  };
+  // Whether this lane's run i holds dims of the row (always, unpadded).
+  auto run_real = [&](int i) { return !kPadD || (col + i * kLanes) * 8 < Dm; };
 
   struct Tile {
     f16x8 k[kKpr][kRuns], v[kKpr][kRuns];
@@ -538,13 +569,13 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     const int base = t0 + it * it_keys + wave * kWaveKeys + row;
 #pragma unroll
     for (int j = 0; j < kKpr; ++j) {
-      const uint32_t off = (uint32_t)(base + j * kRows) * (kD * 2) + col * 16;
+      const uint32_t off = (uint32_t)(base + j * kRows) * (Dm * 2) + col * 16;
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
         tl.k[j][i] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off + i * kLanes * 16, 0, kStreamPolicy));
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, run_off(off, i), 0, kStreamPolicy));
         tl.v[j][i] = __builtin_bit_cast(
-            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, off + i * kLanes * 16, 0, kStreamPolicy));
+            f16x8, __builtin_amdgcn_raw_buffer_load_b128(rv, run_off(off, i), 0, kStreamPolicy));
       }
     }
   };
@@ -557,7 +588,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   if (has_new) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      const int64_t src = (int64_t)(b * a.n_kv + hkv) * kD + (col + i * kLanes) * 8;
+      const int64_t src = (int64_t)(b * a.n_kv + hkv) * Dm + (col + i * kLanes) * 8;
+      if (!run_real(i)) {
+        nk_raw[i] = nv_raw[i] = SrcRun{{f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}}};
+        continue;
+      }
       nk_raw[i] = load_src_run_raw(a.k_new, src, a.new16);
       nv_raw[i] = load_src_run_raw(a.v_new, src, a.new16);
     }
@@ -579,14 +614,22 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
 
   // Query registers: this lane's dims of each of the G heads.
   const int h0 = hgrp * G;
-  const int64_t qoff = ((int64_t)b * a.n_heads + h0) * kD + col * 8;
+  const int64_t qoff = ((int64_t)b * a.n_heads + h0) * Dm + col * 8;
   f16x8 q16[kQ16 ? G : 1][kRuns];
   float q32[kQ16 ? 1 : G][kDims];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      const int64_t e = qoff + g * kD + i * kLanes * 8;
+      const int64_t e = qoff + g * Dm + i * kLanes * 8;
+      if (!run_real(i)) {  // a padded run: zero query dims
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if constexpr (kQ16) q16[g][i][k] = (f16)0.f;
+          else q32[g][i * 8 + k] = 0.f;
+        }
+        continue;
+      }
       if constexpr (kQ16) {
         q16[g][i] = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + e);
       } else {
@@ -637,8 +680,8 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     if (wave == 0 && row < 2 && sub == 0) {
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
-        const int64_t at = slab + (int64_t)pnew * kD + (col + i * kLanes) * 8;
-        if (in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * kD, a.status)) {
+        const int64_t at = slab + (int64_t)pnew * Dm + (col + i * kLanes) * 8;
+        if (run_real(i) && in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * Dm, a.status)) {
           f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
           *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
         }
@@ -797,10 +840,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   }
   __syncthreads();
 
-  store_split_states<G, kO16, kStates, kD>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0, split);
+  store_split_states<G, kO16, kStates, kD, kPadD>(a, lds_o, lds_ml, (int64_t)b * a.n_heads + h0,
+                                                  split, Dm);
   if (nsplit == 1 || !a.fused_merge) return;
-  merge_on_last_arrival<G, kO16, kD>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
-                                     (int64_t)b * a.n_heads + h0);
+  merge_on_last_arrival<G, kO16, kD, kPadD>(a, a.counters + b * (a.n_kv * kQsub) + hgrp,
+                                            (int64_t)b * a.n_heads + h0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1197,6 +1241,16 @@ __global__ __launch_bounds__(64) void decode_merge_hd_kernel(
   merge_row_wave<kO16, 0, kD>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit,
                               (int64_t)gridDim.y * n_heads, records, status);
 }
+// The merge of the padded form: records of kD dims, output rows of od.
+template <bool kO16, int kD>
+__global__ __launch_bounds__(64) void decode_merge_pad_kernel(
+    const float* __restrict__ part_o, const float2* __restrict__ part_ml,
+    void* __restrict__ out, int n_heads, int nsplit, int64_t records, int* __restrict__ status,
+    int od) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  merge_row_wave<kO16, 0, kD, true>(part_o, part_ml, out, (int64_t)b * n_heads + h, nsplit,
+                                    (int64_t)gridDim.y * n_heads, records, status, od);
+}
 
 // The split workgroup's shape, from sweeps on MI355X (decode-only, per call,
 // 32K / 4K / 153 keys): 4 wavefronts, 16-lane rows, 2 keys per row, 2 tiles
@@ -1213,11 +1267,14 @@ using SplitCfg = DecodeCfg<4, 16, 2, 2>;
 template <int kD>
 using SplitCfgD = std::conditional_t<kD == kHeadDim, SplitCfg,
                                      DecodeShape<4, kD == 64 ? 8 : 16, 2, 2, kD>>;
+template <int kD, bool kPadD>
+using SplitCfgP = std::conditional_t<kPadD, DecodePadShape<4, kD == 64 ? 8 : 16, 2, 2, kD>,
+                                     SplitCfgD<kD>>;
 
-template <int G, bool kQ16, bool kO16, int kQsub, int kD = kHeadDim>
+template <int G, bool kQ16, bool kO16, int kQsub, int kD = kHeadDim, bool kPadD = false>
 static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, void* ev_start,
                            void* ev_stop) {
-  using C = SplitCfgD<kD>;
+  using C = SplitCfgP<kD, kPadD>;
   dim3 grid((unsigned)a.nsplit, (unsigned)(a.n_kv * kQsub), (unsigned)batch);
   hipError_t e;
   if (ev_start || ev_stop) {
@@ -1234,7 +1291,11 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, v
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
   const dim3 mgrid((unsigned)a.n_heads, (unsigned)batch);
-  if constexpr (kD == kHeadDim)
+  if constexpr (kPadD)
+    decode_merge_pad_kernel<kO16, kD><<<mgrid, 64, 0, stream>>>(a.part_o, a.part_ml, a.out,
+                                                                a.n_heads, a.nsplit, a.records,
+                                                                a.status, a.head_dim);
+  else if constexpr (kD == kHeadDim)
     decode_merge_kernel<kO16><<<mgrid, 64, 0, stream>>>(a.part_o, a.part_ml, a.out, a.n_heads,
                                                         a.nsplit, a.records, a.status);
   else
@@ -1244,15 +1305,15 @@ static hipError_t launch_g(const DecodeArgs& a, int batch, hipStream_t stream, v
   return hipGetLastError();
 }
 
-template <int G, int kQsub = 1, int kD = kHeadDim>
+template <int G, int kQsub = 1, int kD = kHeadDim, bool kPadD = false>
 static hipError_t launch_qo(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                             hipStream_t st) {
   const int B = c.batch;
   if (s.q16)
-    return s.o16 ? launch_g<G, true, true, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop)
-                 : launch_g<G, true, false, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop);
-  return s.o16 ? launch_g<G, false, true, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop)
-               : launch_g<G, false, false, kQsub, kD>(a, B, st, c.ev_start, c.ev_stop);
+    return s.o16 ? launch_g<G, true, true, kQsub, kD, kPadD>(a, B, st, c.ev_start, c.ev_stop)
+                 : launch_g<G, true, false, kQsub, kD, kPadD>(a, B, st, c.ev_start, c.ev_stop);
+  return s.o16 ? launch_g<G, false, true, kQsub, kD, kPadD>(a, B, st, c.ev_start, c.ev_stop)
+               : launch_g<G, false, false, kQsub, kD, kPadD>(a, B, st, c.ev_start, c.ev_stop);
 }
 
 
@@ -1300,41 +1361,42 @@ static hipError_t launch_mfma(const Shape& s, const DecodeArgs& a, const DecodeC
                : launch_mfma_t<G, false, false>(a, B, st, c.ev_start, c.ev_stop);
 }
 
-// Head sizes 64 and 256 (decode_split_kernel only; the matrix-core kernel is
-// built for 128): the same per-query-head rule, then one workgroup per KV
-// head. Group 8 at 256 is not built (its accumulators and query registers
-// would not fit one lane's registers) and takes the general-shape kernels.
-template <int kD>
+// Head sizes other than 128 (decode_split_kernel only; the matrix-core
+// kernel is built for 128): 64 and 256 as they are, other multiples of 8 up
+// to 256 in the padded form of the next of 64, 128, 256. The same
+// per-query-head rule, then one workgroup per KV head. Group 8 above 128 is
+// not built (its accumulators and query registers would not fit one lane's
+// registers) and takes the general-shape kernels.
+template <int kD, bool kPadD>
 static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                    hipStream_t stream) {
   if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
     switch (s.group) {
-      case 2: return launch_qo<1, 2, kD>(s, a, c, stream);
-      case 4: return launch_qo<1, 4, kD>(s, a, c, stream);
-      case 5: return launch_qo<1, 5, kD>(s, a, c, stream);
+      case 2: return launch_qo<1, 2, kD, kPadD>(s, a, c, stream);
+      case 4: return launch_qo<1, 4, kD, kPadD>(s, a, c, stream);
+      case 5: return launch_qo<1, 5, kD, kPadD>(s, a, c, stream);
       case 8:
-        if constexpr (kD == 64) return launch_qo<1, 8, kD>(s, a, c, stream);
+        if constexpr (kD <= kHeadDim) return launch_qo<1, 8, kD, kPadD>(s, a, c, stream);
         break;
       default: break;
     }
   }
   switch (s.group) {
-    case 1: return launch_qo<1, 1, kD>(s, a, c, stream);
-    case 2: return launch_qo<2, 1, kD>(s, a, c, stream);
-    case 4: return launch_qo<4, 1, kD>(s, a, c, stream);
-    case 5: return launch_qo<5, 1, kD>(s, a, c, stream);
+    case 1: return launch_qo<1, 1, kD, kPadD>(s, a, c, stream);
+    case 2: return launch_qo<2, 1, kD, kPadD>(s, a, c, stream);
+    case 4: return launch_qo<4, 1, kD, kPadD>(s, a, c, stream);
+    case 5: return launch_qo<5, 1, kD, kPadD>(s, a, c, stream);
     case 8:
-      if constexpr (kD == 64) return launch_qo<8, 1, kD>(s, a, c, stream);
+      if constexpr (kD <= kHeadDim) return launch_qo<8, 1, kD, kPadD>(s, a, c, stream);
       return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
   }
 }
 
 bool split_decode_shape(int head_dim, int group) {
-  if (head_dim == kHeadDim) return specialised_group(group);
-  if (head_dim == 64) return specialised_group(group);
-  if (head_dim == 256) return specialised_group(group) && group != 8;
-  return false;
+  if (head_dim < 8 || head_dim > 256 || head_dim % 8 != 0 || !specialised_group(group))
+    return false;
+  return group != 8 || head_dim <= kHeadDim;
 }
 
 hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
@@ -1363,8 +1425,12 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.strided = c.layout == 1;
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
-  if (s.head_dim == 64) return launch_decode_hd<64>(s, a, c, stream);
-  if (s.head_dim == 256) return launch_decode_hd<256>(s, a, c, stream);
+  a.head_dim = s.head_dim;
+  if (s.head_dim == 64) return launch_decode_hd<64, false>(s, a, c, stream);
+  if (s.head_dim == 256) return launch_decode_hd<256, false>(s, a, c, stream);
+  if (s.head_dim < 64) return launch_decode_hd<64, true>(s, a, c, stream);
+  if (s.head_dim < kHeadDim) return launch_decode_hd<kHeadDim, true>(s, a, c, stream);
+  if (s.head_dim > kHeadDim) return launch_decode_hd<256, true>(s, a, c, stream);
   // When one workgroup per (sequence, query head, split) fits the chip, each
   // query head gets its own workgroups: a workgroup's time is its serial
   // chain of key iterations, whose compute grows with the heads it serves,

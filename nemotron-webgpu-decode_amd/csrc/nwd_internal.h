@@ -59,8 +59,9 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
                             int batch, int n_tokens, int* status,
                             hipStream_t stream);
 
-// Shapes launch_decode takes: head size 128, 64 or 256 with a group of 1, 2,
-// 4, 5 or 8 (not 8 at 256).
+// Shapes launch_decode takes: a head size that is a multiple of 8 up to 256
+// with a group of 1, 2, 4, 5 or 8 (8 only up to 128). 64, 128 and 256 run
+// kernels built for them, the other sizes those kernels' padded form.
 bool split_decode_shape(int head_dim, int group);
 
 // nsplit == 1 writes `out` directly; otherwise partial records then a merge.

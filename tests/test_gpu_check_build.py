@@ -215,9 +215,10 @@ def test_general_checked_build_matches(Dh, H, Hkv):
         _same(lambda c, k, v: c.kv_append(kn, vn, k, v, pos, B, 3), prod, chk, [kc, vc])
         for c in (prod, chk):
             c.set_decode_splits(256)
-        # 256, or what the workspace holds for the padded heads (H * 256
+        # 256, or what the workspace holds for padded groups' heads (H * 256
         # records over Hkv * padded group heads)
-        assert prod.decode_splits(B, cap) == (256 if Dh != 128 else min(256, prod.decode_splits(B, cap)))
+        if H // Hkv not in (3, 6, 7):
+            assert prod.decode_splits(B, cap) == 256
         assert prod.decode_splits(B, cap) > 64
         _same(lambda c, o: c.decode(q, kc, vc, pos, o, B), prod, chk, [out])
         _same(lambda c, o, k, v: c.append_decode(q, kn[:, 0], vn[:, 0], k, v, pos, o, B), prod, chk,

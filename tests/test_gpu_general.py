@@ -8,7 +8,8 @@ kernels' set (head_dim 128 with a group of 1, 2, 4, 5 or 8) run the general
 kernels; these tests cover head sizes that are and are not multiples of 8,
 above 256 (two runs per thread), down to 1, and groups 3, 6, 7 and 12.
 Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
-runs the dot-product split kernel built for those sizes (csrc/nwd_decode.hip);
+runs the dot-product split kernel built for those sizes (csrc/nwd_decode.hip),
+and at the other multiples of 8 up to 256 its padded form;
 test_head_size_split_decode covers its launch forms and knobs. Prefill at
 head sizes below 128 that are multiples of 8 runs the MFMA prefill kernel on
 rows padded to 128 dims (test_padded_head_prefill).
@@ -100,10 +101,15 @@ def test_general_decode_matches_oracle(D, H, Hkv):
 
 @pytest.mark.parametrize("D,H,Hkv", [(64, 8, 8), (64, 16, 8), (64, 32, 8), (64, 40, 8),
                                      (64, 64, 8), (256, 8, 8), (256, 16, 8), (256, 32, 8),
-                                     (256, 20, 4)])
+                                     (256, 20, 4),
+                                     # the padded form at other multiples of 8
+                                     (96, 32, 32), (96, 32, 8), (80, 16, 8), (40, 64, 8),
+                                     (192, 16, 8), (136, 40, 8), (120, 64, 8), (248, 8, 8)])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_head_size_split_decode(D, H, Hkv, io):
-    """Head sizes 64 and 256 on the dot-product split kernel: a batch of one
+    """Head sizes 64 and 256 on the dot-product split kernel built for them,
+    other multiples of 8 on its padded form (rows of 40 dims on the head-64
+    kernel, 80-120 on the head-128 one, 136-248 on the head-256 one): a batch of one
     at 3000 keys (one workgroup per query head when batch x heads x splits
     fits 256 workgroups, else one per KV head) and a ragged batch of three,
     against the oracle; forced split counts 1, 7 and 64, the in-kernel merge
