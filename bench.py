@@ -733,11 +733,17 @@ GENERAL_SHAPES = {
                        "layout, decoded as group 8 on padded query rows), 32768 keys, fp16 I/O, "
                        "decode call"),
     "general-d256-8k": (16, 8, 256, 8192, "B=1, 16q/8kv/d256 (group 2, head size 256: the "
-                        "Gemma-2-9B layout), 8192 keys, fp16 I/O, decode call"),
+                        "Gemma-2-9B layout, on the split kernel built for head size 256), 8192 "
+                        "keys, fp16 I/O, decode call"),
     "general-d96-4k": (32, 32, 96, 4096, "B=1, 32q/32kv/d96 (group 1, head size 96: the "
-                       "Phi-3-mini layout), 4096 keys, fp16 I/O, decode call"),
+                       "Phi-3-mini layout, on the head-128 split kernel's padded form), 4096 "
+                       "keys, fp16 I/O, decode call"),
+    "general-g16-8k": (128, 8, 128, 8192, "B=1, 128q/8kv/d128 (group 16: the Llama-3.1-405B "
+                       "layout, as two groups of 8 per KV head on the matrix-core split kernel), "
+                       "8192 keys, fp16 I/O, decode call"),
     "general-d64-16k": (32, 8, 64, 16384, "B=1, 32q/8kv/d64 (group 4, head size 64: the "
-                        "Llama-3.2-1B layout), 16384 keys, fp16 I/O, decode call"),
+                        "Llama-3.2-1B layout, on the split kernel built for head size 64), "
+                        "16384 keys, fp16 I/O, decode call"),
 }
 # Prefill on other head layouts: (heads, kv heads, head_dim, past, new tokens, description).
 GENERAL_PREFILL_SHAPES = {
@@ -747,6 +753,9 @@ GENERAL_PREFILL_SHAPES = {
     "general-prefill-d96": (32, 32, 96, 8192, 512, "B=1, 32q/32kv/d96 (Phi-3-mini layout), 512 "
                             "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
                             "padded to 128 dims)"),
+    "general-prefill-d256": (16, 8, 256, 8192, 512, "B=1, 16q/8kv/d256 (Gemma-2-9B layout), 512 "
+                             "new tokens onto 8192, fp16 I/O, prefill call (the general-shape "
+                             "kernels, fp32 on the vector units)"),
 }
 
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,

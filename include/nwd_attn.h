@@ -74,10 +74,12 @@ typedef struct nwd_desc {
                           D = 64 (G 1, 2, 4, 5, 8) and D = 256 (G 1, 2, 4, 5)
                           run the dot-product split kernel built for those
                           sizes, and at the other multiples of 8 up to 256
-                          its form for rows padded to 64, 128 or 256 dims
-                          (G 8 only up to 128; G 3, 6, 7 padded where the
-                          padded group is built; a K/V slab above 1 GiB,
-                          max_seq * D * 2 bytes, takes the general kernels);
+                          its form for rows padded to 64, 128 or 256 dims;
+                          groups other than 1, 2, 4, 5, 8 (8 up to D = 128)
+                          run as several of those per KV head or on query
+                          rows padded to such groups (a K/V slab above
+                          1 GiB, max_seq * D * 2 bytes, takes the general
+                          kernels);
                           prefills at D below 128 and a multiple of
                           8 run the MFMA prefill kernel on rows padded to
                           128 dims (G 3, 6, 7 through padded query rows);

@@ -151,7 +151,9 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
 // same way. The allocation-free entry point, which has no padded buffers,
 // uses the general kernels. Decode at head sizes 64 and 256 runs the
 // dot-product split kernel built for them, and at the other multiples of 8
-// up to 256 that kernel's padded form (groups 1, 2, 4, 5, and 8 up to 128).
+// up to 256 that kernel's padded form (groups 1, 2, 4, 5, and 8 up to 128;
+// larger groups as several of those per KV head, nwd::kernel_group, or
+// padded to one).
 // Decode calls on MI355X, B = 1, against the general kernels: 32q/32kv/d96
 // at 4096 keys 12.0 against 16.3 us, 32q/32kv/d80 11.6 against 15.0,
 // 16q/8kv/d192 at 8192 keys 14.0 against 20.6, 64q/8kv/d120 15.5 against
@@ -173,21 +175,31 @@ DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
 }
 
 // Prefill: the MFMA prefill kernel at head size 128 and the multiples of 8
-// below it (rows padded with zeros to 128 dims) with groups 1, 2, 4, 5, 8,
-// and groups 3, 6, 7 there through padded query rows; the general kernels
-// otherwise. 512 tokens onto 8192 on MI355X, per call, against the general
-// kernels: 32q/8kv/d64 77.6 against 1640 us, 32q/32kv/d96 79.1 against 7738.
+// below it (rows padded with zeros to 128 dims) with the groups
+// nwd::kernel_group maps, and the others there through padded query rows;
+// the general kernels otherwise. 512 tokens onto 8192 on MI355X, per call,
+// against the general kernels: 32q/8kv/d64 77.6 against 1640 us,
+// 32q/32kv/d96 79.1 against 7738.
 DecodeRoute prefill_route(const nwd::Shape& s, bool have_pad) {
   if (!nwd::prefill_head_dim(s.head_dim)) return kRouteGeneral;
-  if (nwd::specialised_group(s.group)) return kRouteSpecialised;
-  if (have_pad && nwd::padded_group(s.group) > 0) return kRoutePadded;
+  int rep = 0;
+  if (nwd::kernel_group(s.head_dim, s.group, &rep) > 0) return kRouteSpecialised;
+  if (have_pad && nwd::padded_group(s.head_dim, s.group) > 0) return kRoutePadded;
   return kRouteGeneral;
 }
 
 // Whether a context of this shape gets the padded-row buffers.
 bool wants_pad_buffers(int head_dim, int group) {
-  return nwd::padded_group(group) > 0 &&
+  return nwd::padded_group(head_dim, group) > 0 &&
          (nwd::padded_decode_shape(head_dim, group) || nwd::prefill_head_dim(head_dim));
+}
+
+// Workgroups per split of a decode on the split kernels: one per group of
+// query heads the kernels run (nwd::kernel_group: kv_rep per KV head).
+int kv_groups(const nwd::Shape& s) {
+  int rep = 1;
+  nwd::kernel_group(s.head_dim, s.group, &rep);
+  return s.n_kv * rep;
 }
 
 int64_t general_units(const nwd::Shape& s, int batch, int n_new) {
@@ -364,9 +376,9 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   ctx->ws.status = nullptr;
   ctx->ws.counters = nullptr;
   ctx->status_host = nullptr;
-  // Merge tickets: one per (sequence, KV head), or per (sequence, query
-  // head) in the per-query-head form (at most kSubSplitMaxWorkgroups).
-  size_t n_counters = (size_t)d->max_batch * d->n_kv_heads;
+  // Merge tickets: one per (sequence, group of query heads a workgroup
+  // serves), at most one per (sequence, query head).
+  size_t n_counters = (size_t)d->max_batch * d->n_heads;
   if (n_counters < (size_t)nwd::kSubSplitMaxWorkgroups) n_counters = nwd::kSubSplitMaxWorkgroups;
   // o rows of max(D, 128) floats: the general kernels' records of D floats
   // and the argmax records (which reuse part_o) both fit.
@@ -375,7 +387,7 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.counters, n_counters * sizeof(int));
   if (e == hipSuccess) e = hipMemset(ctx->ws.counters, 0, n_counters * sizeof(int));
-  const int gp = nwd::padded_group(group);
+  const int gp = nwd::padded_group(d->head_dim, group);
   if (e == hipSuccess && wants_pad_buffers(d->head_dim, group)) {
     // Padded rows of up to 512 prefill tokens per sub-chunk, within 32 MiB
     // per buffer (at least one token: the decode's rows).
@@ -468,7 +480,7 @@ int32_t nwd_decode_splits(const nwd_ctx* ctx, int32_t batch, int32_t max_len) {
   const nwd::Shape s = route == kRoutePadded ? nwd::padded_shape(ctx->shape) : ctx->shape;
   int n = ctx->forced_splits > 0 ? ctx->forced_splits
           : route == kRouteGeneral ? general_splits(general_units(s, batch, 1), len)
-                                   : auto_splits(s.n_heads, s.n_kv, batch, len);
+                                   : auto_splits(s.n_heads, kv_groups(s), batch, len);
   return clamp_splits(ctx, s, batch, n);
 }
 
@@ -568,7 +580,7 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   const nwd::Shape sh = shape_of(desc);
   const bool general = decode_route(sh, false) == kRouteGeneral;
   int n = general ? general_splits(general_units(sh, batch, 1), len)
-                  : auto_splits(desc->n_heads, desc->n_kv_heads, batch, len);
+                  : auto_splits(desc->n_heads, kv_groups(sh), batch, len);
   if (n > kMaxSplits) n = kMaxSplits;
   const int64_t records = n > 1 ? (int64_t)batch * desc->n_heads * n : 0;
   const int64_t have = scratch_records(desc->head_dim);

@@ -329,6 +329,10 @@ struct DecodeArgs {
   float qk_scale_log2;
   int* status;
   int head_dim;       // D of the rows in memory (a DecodePadShape kernel's; kD otherwise)
+  // Groups of G query heads per KV head: the grid's KV index runs over
+  // n_kv = KV heads x kv_rep such groups, and group j reads KV head
+  // j / kv_rep (1: one group per KV head).
+  int kv_rep;
 };
 
 // Record stores of the in-kernel merge write through to memory (agent
@@ -517,6 +521,9 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int hkv = kQsub > 1 ? (int)blockIdx.y % a.n_kv : (int)blockIdx.y;
   const int sub = kQsub > 1 ? (int)blockIdx.y / a.n_kv : 0;
   const int hgrp = hkv * kQsub + sub;  // this workgroup's group of G query heads
+  // The KV head this group reads, and the KV heads in memory.
+  const int kv_m = a.kv_rep > 1 ? hkv / a.kv_rep : hkv;
+  const int nkv_m = a.kv_rep > 1 ? a.n_kv / a.kv_rep : a.n_kv;
   int split = blockIdx.x + (b & 7);
   while (split >= a.nsplit) split -= a.nsplit;
   const int tid = threadIdx.x;
@@ -537,7 +544,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   const int it_keys = a.strided ? nsplit * kBlockKeys : kBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
 
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * Dm;
+  const int64_t slab = (int64_t)(b * nkv_m + kv_m) * a.cap * Dm;
   // K/V are read through buffer descriptors over the slab that end at the
   // last key a load may need: a load at or past the end fails the hardware
   // range check and returns zeros without a memory access. So the prefetch
@@ -588,7 +595,7 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
   if (has_new) {
 #pragma unroll
     for (int i = 0; i < kRuns; ++i) {
-      const int64_t src = (int64_t)(b * a.n_kv + hkv) * Dm + (col + i * kLanes) * 8;
+      const int64_t src = (int64_t)(b * nkv_m + kv_m) * Dm + (col + i * kLanes) * 8;
       if (!run_real(i)) {
         nk_raw[i] = nv_raw[i] = SrcRun{{f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}}};
         continue;
@@ -677,11 +684,11 @@ __global__ __launch_bounds__(C::kThreads) void decode_split_kernel(const DecodeA
     }
     // the lanes of row 0 of wavefront 0 hold the runs of the new K row, those
     // of row 1 the V row's
-    if (wave == 0 && row < 2 && sub == 0) {
+    if (wave == 0 && row < 2 && sub == 0 && kv_m * a.kv_rep == hkv) {
 #pragma unroll
       for (int i = 0; i < kRuns; ++i) {
         const int64_t at = slab + (int64_t)pnew * Dm + (col + i * kLanes) * 8;
-        if (run_real(i) && in_bounds(at, 8, (int64_t)a.batch * a.n_kv * a.cap * Dm, a.status)) {
+        if (run_real(i) && in_bounds(at, 8, (int64_t)a.batch * nkv_m * a.cap * Dm, a.status)) {
           f16* dst = (row == 0 ? a.k_cache : a.v_cache) + at;
           *reinterpret_cast<f16x8*>(dst) = row == 0 ? nk[i] : nv[i];
         }
@@ -936,6 +943,9 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   char* lds = reinterpret_cast<char*>(dsmem);
 
   const int b = blockIdx.z, hkv = blockIdx.y;
+  // The KV head this group of query heads reads (DecodeArgs::kv_rep).
+  const int kv_m = a.kv_rep > 1 ? hkv / a.kv_rep : hkv;
+  const int nkv_m = a.kv_rep > 1 ? a.n_kv / a.kv_rep : a.n_kv;
   int split = blockIdx.x + (b & 7);  // XCD rotation, as decode_split_kernel
   while (split >= a.nsplit) split -= a.nsplit;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -950,7 +960,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const int t0 = a.strided ? split * kMBlockKeys : u0 * kUnitKeys;
   const int it_keys = a.strided ? nsplit * kMBlockKeys : kMBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * kHeadDim;
+  const int64_t slab = (int64_t)(b * nkv_m + kv_m) * a.cap * kHeadDim;
   auto slab_rsrc = [&](f16* cache, int end_key) {
     return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kHeadDim * 2),
                                              kBufferWord3);
@@ -990,7 +1000,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const bool has_new = a.k_new != nullptr;
   SrcRun nk_raw[4], nv_raw;
   if (has_new) {
-    const int64_t src = (int64_t)(b * a.n_kv + hkv) * kHeadDim;
+    const int64_t src = (int64_t)(b * nkv_m + kv_m) * kHeadDim;
 #pragma unroll
     for (int db = 0; db < 4; ++db) nk_raw[db] = load_src_run_raw(a.k_new, src + db * 32 + 8 * lq, a.new16);
     nv_raw = load_src_run_raw(a.v_new, src + 8 * lr, a.new16);
@@ -1065,9 +1075,9 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     nv = convert_src_run(nv_raw, a.new16);
     // K chunks 4 db + lq from the lanes of key row 0, V chunk lr from lane
     // group 0
-    if (wave == w_new) {
+    if (wave == w_new && kv_m * a.kv_rep == hkv) {
       const int64_t at = slab + (int64_t)pnew * kHeadDim;
-      const int64_t cache_elems = (int64_t)a.batch * a.n_kv * a.cap * kHeadDim;
+      const int64_t cache_elems = (int64_t)a.batch * nkv_m * a.cap * kHeadDim;
       if (lr == 0) {
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
@@ -1393,15 +1403,54 @@ static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const De
   }
 }
 
-bool split_decode_shape(int head_dim, int group) {
-  if (head_dim < 8 || head_dim > 256 || head_dim % 8 != 0 || !specialised_group(group))
-    return false;
-  return group != 8 || head_dim <= kHeadDim;
+// A larger group runs as groups of the largest built size (8 up to head size
+// 128, 5 above), so that each KV head's rows are read as few times as
+// possible: kv_rep = ceil(group / largest) reads. A divisor among 8, 5, 4
+// that gives that many groups takes the group as it is; otherwise it is
+// padded to a multiple of the largest size. Decode calls on MI355X, B = 1,
+// 8192 keys: 96q/8kv/d128 (group 12) as 3 groups of 4, 20.6 us, padded to
+// 16 as 2 groups of 8, 16.6 (128q/8kv, 2 groups of 8: 12.4; on the general
+// kernels 43.3).
+int kernel_group(int head_dim, int group, int* kv_rep) {
+  *kv_rep = 1;
+  const int top = head_dim <= kHeadDim ? 8 : 5;  // group 8 is built up to head size 128
+  if (group == 1 || group == 2 || group == 4 || group == 5 || group == top) return group;
+  if (group < 8) return 0;  // 3, 6, 7: padded first
+  const int reads = (group + top - 1) / top;
+  for (int gs : {top, 5, 4}) {
+    if (group % gs == 0 && group / gs == reads) {
+      *kv_rep = reads;
+      return gs;
+    }
+  }
+  return 0;
 }
 
-hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,
+int padded_group(int head_dim, int group) {
+  int rep = 0;
+  if (kernel_group(head_dim, group, &rep) > 0) return 0;
+  if (group == 3) return 4;
+  if (group < 8) return 8;
+  const int top = head_dim <= kHeadDim ? 8 : 5;
+  return (group + top - 1) / top * top;
+}
+
+bool split_decode_shape(int head_dim, int group) {
+  int rep = 0;
+  return head_dim >= 8 && head_dim <= 256 && head_dim % 8 == 0 &&
+         kernel_group(head_dim, group, &rep) > 0;
+}
+
+hipError_t launch_decode(const Shape& s0, const DecodeCall& c, const Workspace& ws,
                          hipStream_t stream) {
-  if (!split_decode_shape(s.head_dim, s.group)) return hipErrorInvalidValue;
+  if (!split_decode_shape(s0.head_dim, s0.group)) return hipErrorInvalidValue;
+  // A group the kernels are not built for runs as kv_rep groups of a built
+  // size per KV head (kernel_group); the kernels then see n_kv * kv_rep KV
+  // heads of that group.
+  int kv_rep = 1;
+  Shape s = s0;
+  s.group = kernel_group(s0.head_dim, s0.group, &kv_rep);
+  s.n_kv = s0.n_kv * kv_rep;
   DecodeArgs a;
   a.q = c.q;
   a.k_cache = static_cast<f16*>(c.k_cache);
@@ -1426,6 +1475,7 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
   a.head_dim = s.head_dim;
+  a.kv_rep = kv_rep;
   if (s.head_dim == 64) return launch_decode_hd<64, false>(s, a, c, stream);
   if (s.head_dim == 256) return launch_decode_hd<256, false>(s, a, c, stream);
   if (s.head_dim < 64) return launch_decode_hd<64, true>(s, a, c, stream);

@@ -22,8 +22,6 @@ struct Shape {
 // Head sizes the general-shape kernels take (sparse_attn.wgsl:12-17 takes
 // any; a row of q and the partial output stay in LDS).
 constexpr int kMaxHeadDim = 512;
-// Group sizes the specialised kernels are built for (D = 128).
-inline bool specialised_group(int g) { return g == 1 || g == 2 || g == 4 || g == 5 || g == 8; }
 
 // Split-K workspace owned by the context.
 struct Workspace {
@@ -59,9 +57,16 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
                             int batch, int n_tokens, int* status,
                             hipStream_t stream);
 
+// The group the decode and prefill kernels run a group of `group` query
+// heads as, with *kv_rep such groups per KV head: the group itself for 1, 2,
+// 4, 5 and 8 (8 only up to head size 128); for larger groups one of 8, 5, 4
+// that divides them into ceil(group / largest built size) groups; 0 when
+// the group must be padded first (padded_group).
+int kernel_group(int head_dim, int group, int* kv_rep);
+
 // Shapes launch_decode takes: a head size that is a multiple of 8 up to 256
-// with a group of 1, 2, 4, 5 or 8 (8 only up to 128). 64, 128 and 256 run
-// kernels built for them, the other sizes those kernels' padded form.
+// and a group kernel_group maps. 64, 128 and 256 run kernels built for
+// them, the other sizes those kernels' padded form.
 bool split_decode_shape(int head_dim, int group);
 
 // nsplit == 1 writes `out` directly; otherwise partial records then a merge.
@@ -87,12 +92,14 @@ hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
 // Largest decode split count supported for `batch` sequences by `ws`.
 int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
-// Groups of 3, 6 and 7 query heads run the decode kernels as groups of 4, 8
-// and 8 (padded_group, 0 for other groups) where launch_decode takes the
-// padded group at the head size (padded_decode_shape), their query rows
-// copied into a padded layout (q_pad, [batch][Hkv][padded group][D], the
-// call's q dtype) and the real rows copied out of out_pad afterwards.
-int padded_group(int group);
+// Groups kernel_group does not map run as a padded group (padded_group; 0
+// for groups that need no padding): 3 as 4, 6 and 7 as 8, larger groups as
+// the next multiple of 8 (of 5 above head size 128), where launch_decode
+// takes the padded group at the head size (padded_decode_shape), their
+// query rows copied into a padded layout (q_pad, [batch][Hkv][padded
+// group][D], the call's q dtype) and the real rows copied out of out_pad
+// afterwards.
+int padded_group(int head_dim, int group);
 bool padded_decode_shape(int head_dim, int group);
 Shape padded_shape(const Shape& s);
 hipError_t launch_padded_decode(const Shape& s, const DecodeCall& c, const Workspace& ws,

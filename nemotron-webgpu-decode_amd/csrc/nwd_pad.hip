@@ -1,7 +1,8 @@
-// nwd_pad.hip — decode and prefill with groups of 3, 6 or 7 query heads on
-// the kernels built for groups of 4 and 8 (nwd_decode.hip, nwd_prefill.hip),
-// at the head sizes those kernels take (decode: 64, 128, 256; prefill: 128
-// and the multiples of 8 below it).
+// nwd_pad.hip — decode and prefill with groups the kernels cannot take as
+// they are (3, 6, 7, and larger groups with no divisor among 8, 5, 4) on the
+// kernels of the next group they take (nwd_decode.hip, nwd_prefill.hip),
+// at the head sizes those kernels take (decode: multiples of 8 up to 256;
+// prefill: 128 and the multiples of 8 below it).
 //
 // The reference kernel maps query head h to KV head h / (H / Hkv) for any
 // group (kernels/sparse_attn.wgsl:38-39). The decode and prefill kernels
@@ -98,20 +99,14 @@ __global__ __launch_bounds__(kPadThreads) void unpad_chunk_kernel(
       op[(((b * nc + t) * n_kv + hk) * Gf + g) * D + d];
 }
 
-int padded_group(int group) {
-  if (group == 3) return 4;
-  if (group == 6 || group == 7) return 8;
-  return 0;
-}
-
 bool padded_decode_shape(int head_dim, int group) {
-  const int gp = padded_group(group);
+  const int gp = padded_group(head_dim, group);
   return gp > 0 && split_decode_shape(head_dim, gp);
 }
 
 Shape padded_shape(const Shape& s) {
   Shape p = s;
-  p.group = padded_group(s.group);
+  p.group = padded_group(s.head_dim, s.group);
   p.n_heads = s.n_kv * p.group;
   return p;
 }
@@ -180,7 +175,7 @@ hipError_t launch_padded_prefill(const Shape& s, const void* q, const void* k_ca
                                  const void* v_cache, const int32_t* pos0, void* out, int batch,
                                  int n_new, int max_len, const Workspace& ws, const PadBuffers& pb,
                                  hipStream_t stream) {
-  if (padded_group(s.group) == 0 || !prefill_head_dim(s.head_dim) || !pb.q_pad || !pb.out_pad ||
+  if (padded_group(s.head_dim, s.group) == 0 || !prefill_head_dim(s.head_dim) || !pb.q_pad || !pb.out_pad ||
       !pb.pos_sub || pb.chunk_tokens < 1)
     return hipErrorInvalidValue;
   if (s.q16)

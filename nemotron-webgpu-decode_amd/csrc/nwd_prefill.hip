@@ -138,6 +138,7 @@ struct PrefillArgs {
   float qk_scale_log2;
   int* status;
   int head_dim;     // D (prefill_pad_kernel; 128 in prefill_kernel)
+  int kv_rep;       // groups of G query heads per KV head (n_kv counts the groups)
 };
 
 // LDS of a workgroup: K0 K1 V0 V1 tiles, 32 KB each; with fp32 queries also
@@ -222,7 +223,10 @@ __device__ __forceinline__ void prefill_body(const PrefillArgs a) {
   const bool wave_has_pad = r0 + 31 >= total_rows;
   const int wave_min_lim = P0 + r0 / G;
 
-  const int64_t slab = (int64_t)(b * a.n_kv + hkv) * a.cap * D;
+  // The KV head this group of query heads reads (kv_rep groups per KV head).
+  const int kv_m = a.kv_rep > 1 ? hkv / a.kv_rep : hkv;
+  const int nkv_m = a.kv_rep > 1 ? a.n_kv / a.kv_rep : a.n_kv;
+  const int64_t slab = (int64_t)(b * nkv_m + kv_m) * a.cap * D;
   const auto rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.k_cache + slab), 0,
                                                     kend_s * (D * 2), kBufferWord3);
   const auto rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(a.v_cache + slab), 0,
@@ -605,7 +609,8 @@ static int prefill_splits(int64_t row_tiles, int64_t rows, int max_len, const Wo
 template <int G, bool kQ16, bool kO16, bool kPadD>
 static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
-                                   int max_len, const Workspace& ws, hipStream_t stream) {
+                                   int max_len, const Workspace& ws, int kv_rep,
+                                   hipStream_t stream) {
   auto kern = kPadD ? prefill_pad_kernel<G, kQ16, kO16> : prefill_kernel<G, kQ16, kO16>;
   constexpr size_t kPrefillLds = prefill_lds_bytes<kQ16>();
   // The dynamic LDS size exceeds the 64 KB default: raise the kernel's limit
@@ -635,6 +640,7 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
   a.qk_scale_log2 = s.qk_scale * kLog2e;
   a.status = ws.status;
   a.head_dim = s.head_dim;
+  a.kv_rep = kv_rep;
   const int64_t row_tiles = (int64_t)a.mtiles * s.n_kv * batch;
   const int64_t rows = (int64_t)n_new * s.n_heads * batch;
   const int nsplit = prefill_splits(row_tiles, rows, max_len, ws);
@@ -660,38 +666,45 @@ static hipError_t launch_prefill_t(const Shape& s, const void* q, const void* kc
 template <int G, bool kPadD>
 static hipError_t launch_prefill_p(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
-                                   int max_len, const Workspace& ws, hipStream_t stream) {
+                                   int max_len, const Workspace& ws, int r, hipStream_t stream) {
   if (s.q16)
-    return s.o16 ? launch_prefill_t<G, true, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
-                 : launch_prefill_t<G, true, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
-  return s.o16 ? launch_prefill_t<G, false, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream)
-               : launch_prefill_t<G, false, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+    return s.o16 ? launch_prefill_t<G, true, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream)
+                 : launch_prefill_t<G, true, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream);
+  return s.o16 ? launch_prefill_t<G, false, true, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream)
+               : launch_prefill_t<G, false, false, kPadD>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream);
 }
 
 template <int G>
 static hipError_t launch_prefill_g(const Shape& s, const void* q, const void* kc, const void* vc,
                                    const int32_t* pos0, void* out, int batch, int n_new,
-                                   int max_len, const Workspace& ws, hipStream_t stream) {
+                                   int max_len, const Workspace& ws, int r, hipStream_t stream) {
   if (s.head_dim == kHeadDim)
-    return launch_prefill_p<G, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
-  return launch_prefill_p<G, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, stream);
+    return launch_prefill_p<G, false>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream);
+  return launch_prefill_p<G, true>(s, q, kc, vc, pos0, out, batch, n_new, max_len, ws, r, stream);
 }
 
 bool prefill_head_dim(int head_dim) {
   return head_dim == kHeadDim || (head_dim >= 8 && head_dim < kHeadDim && head_dim % 8 == 0);
 }
 
-hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
+hipError_t launch_prefill(const Shape& s0, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,
                           int batch, int n_new, int max_len, const Workspace& ws,
                           hipStream_t stream) {
-  if (!prefill_head_dim(s.head_dim)) return hipErrorInvalidValue;
+  if (!prefill_head_dim(s0.head_dim)) return hipErrorInvalidValue;
+  // A group the kernel is not built for runs as r groups of a built size per
+  // KV head (kernel_group): n_kv * r KV heads of that group, each group's
+  // workgroups reading its KV head's rows.
+  int r = 1;
+  Shape s = s0;
+  s.group = kernel_group(s0.head_dim, s0.group, &r);
+  s.n_kv = s0.n_kv * r;
   switch (s.group) {
-    case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
-    case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
-    case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
-    case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
-    case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, stream);
+    case 1: return launch_prefill_g<1>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 2: return launch_prefill_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -192,7 +192,7 @@ def test_q4_checked_build_matches():
 
 
 @pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1), (128, 7, 1), (128, 12, 4),
-                                      (64, 8, 2), (256, 10, 2)])
+                                      (64, 8, 2), (256, 10, 2), (128, 32, 2), (96, 18, 2)])
 def test_general_checked_build_matches(Dh, H, Hkv):
     """The general-shape kernels in the checked build: append, decode with
     the workspace filled exactly (max_seq 64 gives H * 256 records, and 256
@@ -217,7 +217,7 @@ def test_general_checked_build_matches(Dh, H, Hkv):
             c.set_decode_splits(256)
         # 256, or what the workspace holds for padded groups' heads (H * 256
         # records over Hkv * padded group heads)
-        if H // Hkv not in (3, 6, 7):
+        if H // Hkv not in (3, 6, 7, 9):  # the padded groups (9 -> 16)
             assert prod.decode_splits(B, cap) == 256
         assert prod.decode_splits(B, cap) > 64
         _same(lambda c, o: c.decode(q, kc, vc, pos, o, B), prod, chk, [out])
@@ -251,4 +251,5 @@ def test_asan_host_driver_on_gpu():
     assert "gpu cycle group 7 head_dim 128" in res.stdout  # the padded-group route
     assert "gpu cycle group 4 head_dim 64" in res.stdout  # the split kernel at other head sizes
     assert "gpu cycle group 5 head_dim 256" in res.stdout
+    assert "gpu cycle group 12 head_dim 96" in res.stdout  # padded to 16: two groups of 8
     assert "0 failed so far" in res.stdout.splitlines()[-1]

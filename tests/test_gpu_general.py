@@ -172,6 +172,77 @@ def test_head_size_split_decode(D, H, Hkv, io):
             assert max_abs(res[0][0][b], want) < TOL, b
 
 
+@pytest.mark.parametrize("D,H,Hkv", [(128, 128, 8), (128, 96, 8), (64, 48, 1), (128, 71, 1),
+                                     (96, 20, 2), (256, 16, 2), (192, 14, 2), (128, 9, 1)])
+@pytest.mark.parametrize("io", ["f16", "f32"])
+def test_large_group_decode_and_prefill(D, H, Hkv, io):
+    """Groups the kernels are not built for run as several built groups per
+    KV head (16 = 2 x 8, 48 = 6 x 8, 10 = 2 x 5, 8 at head size 256 =
+    2 x 4) or padded to such groups (12 -> 16 = 2 x 8, 71 -> 72 = 9 x 8,
+    9 -> 16, 7 at 192 -> 8 = 2 x 4): decode of a ragged pair (2000 and 37 keys) and
+    forced split counts against the oracle, the fused append bit-identical
+    to append + decode in the caches, and (head sizes up to 128) a prefill
+    chunk row by row."""
+    say(f"large group D={D} {H}q/{Hkv}kv io={io}")
+    g = rng(900 + D + H)
+    lens = [2000, 37]
+    cap = 2050
+    rows = [_rows(g, L, Hkv, D, scale=0.5) for L in lens]
+    q = _q(g, (2, H, D), io)
+    kn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
+    vn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
+    rt = 2e-3 if io == "f16" else 2e-5
+    with nw.AttnContext(H, Hkv, cap, head_dim=D, max_batch=2, q_dtype=io, o_dtype=io) as ctx:
+        kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
+        vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
+        pos = pos_tensor([L - 1 for L in lens])
+        outs = []
+        for n in (0, 1, 9):
+            ctx.set_decode_splits(n)
+            out = torch.empty((2, H, D), dtype=_tdtype(io), device="cuda")
+            ctx.decode(dev(q), kc, vc, pos, out, 2, max(lens))
+            outs.append(host(out).astype(np.float32))
+        ctx.set_decode_splits(0)
+        assert ctx.device_status() == nw.NWD_OK
+        for b, (k, v) in enumerate(rows):
+            want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k), f32(v))
+            assert max_abs(outs[0][b], want) < TOL, b
+        for o in outs[1:]:
+            assert max_abs(o, outs[0]) < rt
+        res = []
+        for fused in (True, False):
+            kc2, vc2 = kc.clone(), vc.clone()
+            out = torch.empty((2, H, D), dtype=_tdtype(io), device="cuda")
+            p2 = pos_tensor(lens)
+            if fused:
+                ctx.append_decode(dev(q), dev(kn), dev(vn), kc2, vc2, p2, out, 2, cap)
+            else:
+                ctx.kv_append(dev(kn[:, None]), dev(vn[:, None]), kc2, vc2, p2, 2, 1)
+                ctx.decode(dev(q), kc2, vc2, p2, out, 2, cap)
+            assert ctx.device_status() == nw.NWD_OK
+            res.append((host(out).astype(np.float32), host(kc2).view(np.uint16),
+                        host(vc2).view(np.uint16)))
+        assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
+        assert max_abs(res[0][0], res[1][0]) < rt
+        if D <= 128:
+            n_new, p0 = 21, [1500, 2]
+            qp = _q(g, (2, n_new, H, D), io)
+            out = torch.empty((2, n_new, H, D), dtype=_tdtype(io), device="cuda")
+            ctx.prefill(dev(qp), kc, vc, pos_tensor(p0), out, 2, n_new, max(p0) + n_new)
+            assert ctx.device_status() == nw.NWD_OK
+            got = host(out).astype(np.float32)
+            kh, vh = host(kc), host(vc)
+            worst = 0.0
+            for b in range(2):
+                for i in range(n_new):
+                    L = p0[b] + i + 1
+                    want = oracle.sparse_attn_f32(qp[b, i].astype(np.float32),
+                                                  f32(from_cache(kh, b, L)), f32(from_cache(vh, b, L)))
+                    worst = max(worst, max_abs(got[b, i], want))
+            say(f"  prefill max-abs {worst:.2e}")
+            assert worst < TOL
+
+
 @pytest.mark.parametrize("D,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1)])
 def test_general_split_count_does_not_change_results(D, H, Hkv):
     """Forced split counts 1, 3, 17 and 64 (the last leaves splits with no
