@@ -754,8 +754,8 @@ GENERAL_PREFILL_SHAPES = {
                             "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
                             "padded to 128 dims)"),
     "general-prefill-d256": (16, 8, 256, 8192, 512, "B=1, 16q/8kv/d256 (Gemma-2-9B layout), 512 "
-                             "new tokens onto 8192, fp16 I/O, prefill call (the general-shape "
-                             "kernels, fp32 on the vector units)"),
+                             "new tokens onto 8192, fp16 I/O, prefill call (the head-256 MFMA "
+                             "prefill)"),
 }
 
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,

@@ -80,9 +80,10 @@ typedef struct nwd_desc {
                           rows padded to such groups (a K/V slab above
                           1 GiB, max_seq * D * 2 bytes, takes the general
                           kernels);
-                          prefills at D below 128 and a multiple of
-                          8 run the MFMA prefill kernel on rows padded to
-                          128 dims (G 3, 6, 7 through padded query rows);
+                          prefills at D = 256, and at the other
+                          multiples of 8 up to 256, run MFMA prefill
+                          kernels built for D = 128 and 256 on rows padded
+                          to those dims (other groups as for decode);
                           every other (D, G) runs the general kernels, with
                           the same contract and cache layout (a coverage
                           path, not tuned like the others)                   */
@@ -200,9 +201,10 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * accumulation: an fp16 q enters exact and its scores are scaled in fp32;
  * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
  * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
- * makes nwd_device_status report NWD_ERR_DEVICE (head sizes below 128 run
- * these kernels on rows padded with zeros to 128 dims, and groups 3, 6, 7
- * on padded query rows, in sub-chunks). The shapes of the general kernels
+ * makes nwd_device_status report NWD_ERR_DEVICE (head sizes up to 256 run
+ * these kernels, or a head-256 form of them, on rows padded with zeros to
+ * 128 or 256 dims, and padded groups on padded query rows, in sub-chunks).
+ * The shapes of the general kernels
  * (see nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
  * outside the cache (pos0[b] < 0 or pos0[b] + n_new > max_seq) is flagged in
  * the device status and run at the nearest valid pos0. max_len bounds

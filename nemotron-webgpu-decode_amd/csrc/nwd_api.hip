@@ -174,14 +174,14 @@ DecodeRoute decode_route(const nwd::Shape& s, bool have_pad) {
   return kRouteGeneral;
 }
 
-// Prefill: the MFMA prefill kernel at head size 128 and the multiples of 8
-// below it (rows padded with zeros to 128 dims) with the groups
-// nwd::kernel_group maps, and the others there through padded query rows;
-// the general kernels otherwise. 512 tokens onto 8192 on MI355X, per call,
-// against the general kernels: 32q/8kv/d64 77.6 against 1640 us,
-// 32q/32kv/d96 79.1 against 7738.
+// Prefill: the MFMA prefill kernels at head sizes 128 and 256 and the other
+// multiples of 8 up to 256 (rows padded with zeros to 128 or 256 dims) with
+// the groups nwd::kernel_group maps, and the others there through padded
+// query rows; the general kernels otherwise. 512 tokens onto 8192 on MI355X,
+// per call, against the general kernels: 32q/8kv/d64 77.6 against 1640 us,
+// 32q/32kv/d96 79.1 against 7738, 16q/8kv/d256 80.7 against 3466.
 DecodeRoute prefill_route(const nwd::Shape& s, bool have_pad) {
-  if (!nwd::prefill_head_dim(s.head_dim)) return kRouteGeneral;
+  if (!nwd::prefill_head_dim(s.head_dim) || !slab_fits(s)) return kRouteGeneral;
   int rep = 0;
   if (nwd::kernel_group(s.head_dim, s.group, &rep) > 0) return kRouteSpecialised;
   if (have_pad && nwd::padded_group(s.head_dim, s.group) > 0) return kRoutePadded;
@@ -338,7 +338,10 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   *out_ctx = nullptr;
   if (int rc = check_desc(d, "nwd_create")) return rc;
   const int group = d->n_heads / d->n_kv_heads;
-  const int o_dim = d->head_dim > nwd::kHeadDim ? d->head_dim : nwd::kHeadDim;
+  // Split records of the kernels' width, and at least 128 floats per record:
+  // the argmax records reuse part_o.
+  const int o_dim = nwd::record_width(d->head_dim) > nwd::kHeadDim ? nwd::record_width(d->head_dim)
+                                                                   : nwd::kHeadDim;
 
   nwd_ctx* ctx = new nwd_ctx();
   ctx->desc = *d;
@@ -380,8 +383,6 @@ int nwd_create(const nwd_desc* d, nwd_ctx** out_ctx) {
   // serves), at most one per (sequence, query head).
   size_t n_counters = (size_t)d->max_batch * d->n_heads;
   if (n_counters < (size_t)nwd::kSubSplitMaxWorkgroups) n_counters = nwd::kSubSplitMaxWorkgroups;
-  // o rows of max(D, 128) floats: the general kernels' records of D floats
-  // and the argmax records (which reuse part_o) both fit.
   ctx->o_floats = ctx->ws.records * o_dim;
   e = hipMalloc(&ctx->ws.part_o, ctx->o_floats * sizeof(float));
   if (e == hipSuccess) e = hipMalloc(&ctx->ws.part_ml, ctx->ws.records * sizeof(float2));
@@ -583,7 +584,8 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
                   : auto_splits(desc->n_heads, kv_groups(sh), batch, len);
   if (n > kMaxSplits) n = kMaxSplits;
   const int64_t records = n > 1 ? (int64_t)batch * desc->n_heads * n : 0;
-  const int64_t have = scratch_records(desc->head_dim);
+  const int rw = nwd::record_width(desc->head_dim);  // floats per record
+  const int64_t have = scratch_records(rw);
   if (records > have)
     return fail(nullptr, NWD_ERR_CAPACITY,
                 "%s: %d sequences x %d heads x %d splits need %lld split records; the static "
@@ -594,7 +596,7 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
   if (int rc = scratch_address(who, &base)) return rc;
   nwd::Workspace ws;
   ws.part_ml = reinterpret_cast<float2*>(base + kScratchMlOffset);
-  ws.part_o = reinterpret_cast<float*>(base + scratch_o_offset(desc->head_dim));
+  ws.part_o = reinterpret_cast<float*>(base + scratch_o_offset(rw));
   ws.records = have;
   ws.counters = nullptr;  // the separate merge kernel takes no arrival tickets
   ws.status = status ? status : reinterpret_cast<int*>(base);

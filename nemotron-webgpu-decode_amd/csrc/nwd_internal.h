@@ -22,6 +22,13 @@ struct Shape {
 // Head sizes the general-shape kernels take (sparse_attn.wgsl:12-17 takes
 // any; a row of q and the partial output stay in LDS).
 constexpr int kMaxHeadDim = 512;
+// Floats per split-K record at head size D: the split kernels and the MFMA
+// prefills keep the dims of the kernel they run on (128 for the multiples of
+// 8 up to 128, 256 above), the general kernels D.
+inline int record_width(int head_dim) {
+  if (head_dim % 8 == 0 && head_dim <= 256) return head_dim <= 128 ? 128 : 256;
+  return head_dim;
+}
 
 // Split-K workspace owned by the context.
 struct Workspace {
@@ -80,9 +87,14 @@ hipError_t launch_decode(const Shape& s, const DecodeCall& c, const Workspace& w
 // B = 32: 13.4 against 7.2 (B = 1-8 gain or tie).
 constexpr int kSubSplitMaxWorkgroups = 256;
 
-// Head sizes launch_prefill takes: 128, and the multiples of 8 below it
-// (rows padded with zeros to 128 dims).
+// Head sizes launch_prefill takes: the multiples of 8 up to 256. 128 and 256
+// run kernels built for them, the others those kernels' rows padded with
+// zeros (below 128: nwd_prefill.hip; above: nwd_prefill_wide.hip).
 bool prefill_head_dim(int head_dim);
+bool prefill_wide_head_dim(int head_dim);  // 136 .. 256
+hipError_t launch_prefill_wide(const Shape& s, const void* q, const void* k_cache,
+                               const void* v_cache, const int32_t* pos0, void* out, int batch,
+                               int n_new, int max_len, const Workspace& ws, hipStream_t stream);
 
 hipError_t launch_prefill(const Shape& s, const void* q, const void* k_cache,
                           const void* v_cache, const int32_t* pos0, void* out,

@@ -684,7 +684,7 @@ static hipError_t launch_prefill_g(const Shape& s, const void* q, const void* kc
 }
 
 bool prefill_head_dim(int head_dim) {
-  return head_dim == kHeadDim || (head_dim >= 8 && head_dim < kHeadDim && head_dim % 8 == 0);
+  return head_dim >= 8 && head_dim <= 256 && head_dim % 8 == 0;
 }
 
 hipError_t launch_prefill(const Shape& s0, const void* q, const void* k_cache,
@@ -692,6 +692,9 @@ hipError_t launch_prefill(const Shape& s0, const void* q, const void* k_cache,
                           int batch, int n_new, int max_len, const Workspace& ws,
                           hipStream_t stream) {
   if (!prefill_head_dim(s0.head_dim)) return hipErrorInvalidValue;
+  if (prefill_wide_head_dim(s0.head_dim))  // above 128 (nwd_prefill_wide.hip)
+    return launch_prefill_wide(s0, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws,
+                               stream);
   // A group the kernel is not built for runs as r groups of a built size per
   // KV head (kernel_group): n_kv * r KV heads of that group, each group's
   // workgroups reading its KV head's rows.

@@ -192,7 +192,8 @@ def test_q4_checked_build_matches():
 
 
 @pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1), (128, 7, 1), (128, 12, 4),
-                                      (64, 8, 2), (256, 10, 2), (128, 32, 2), (96, 18, 2)])
+                                      (64, 8, 2), (256, 10, 2), (128, 32, 2), (96, 18, 2),
+                                      (200, 16, 8)])
 def test_general_checked_build_matches(Dh, H, Hkv):
     """The general-shape kernels in the checked build: append, decode with
     the workspace filled exactly (max_seq 64 gives H * 256 records, and 256

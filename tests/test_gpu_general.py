@@ -181,8 +181,7 @@ def test_large_group_decode_and_prefill(D, H, Hkv, io):
     2 x 4) or padded to such groups (12 -> 16 = 2 x 8, 71 -> 72 = 9 x 8,
     9 -> 16, 7 at 192 -> 8 = 2 x 4): decode of a ragged pair (2000 and 37 keys) and
     forced split counts against the oracle, the fused append bit-identical
-    to append + decode in the caches, and (head sizes up to 128) a prefill
-    chunk row by row."""
+    to append + decode in the caches, and a prefill chunk row by row."""
     say(f"large group D={D} {H}q/{Hkv}kv io={io}")
     g = rng(900 + D + H)
     lens = [2000, 37]
@@ -224,7 +223,7 @@ def test_large_group_decode_and_prefill(D, H, Hkv, io):
                         host(vc2).view(np.uint16)))
         assert np.array_equal(res[0][1], res[1][1]) and np.array_equal(res[0][2], res[1][2])
         assert max_abs(res[0][0], res[1][0]) < rt
-        if D <= 128:
+        if D <= 256:
             n_new, p0 = 21, [1500, 2]
             qp = _q(g, (2, n_new, H, D), io)
             out = torch.empty((2, n_new, H, D), dtype=_tdtype(io), device="cuda")
@@ -365,12 +364,16 @@ def test_general_prefill_matches_token_by_token(D, H, Hkv, splits):
 
 
 @pytest.mark.parametrize("D,H,Hkv", [(64, 32, 8), (64, 8, 8), (96, 10, 2), (32, 16, 2),
-                                     (120, 4, 2), (64, 6, 2), (96, 7, 1)])
+                                     (120, 4, 2), (64, 6, 2), (96, 7, 1),
+                                     # the head-256 prefill, as it is and padded
+                                     (256, 16, 8), (256, 8, 8), (256, 20, 4), (200, 8, 4),
+                                     (136, 6, 2), (256, 14, 2)])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_padded_head_prefill(D, H, Hkv, io):
     """Head sizes below 128 (multiples of 8) prefill on the MFMA prefill
-    kernel with rows padded to 128 dims (groups 3 and 7 also through padded
-    query rows): two sequences, pos0 1500 (several key tiles, split over
+    kernel with rows padded to 128 dims, head sizes 136 to 256 on the head-256
+    MFMA prefill (padded below 256); groups 3 and 7 also through padded
+    query rows: two sequences, pos0 1500 (several key tiles, split over
     workgroups and merged) and 3, 40 new tokens; every row against the
     oracle's decode over keys 0..pos0+i."""
     say(f"padded-head prefill D={D} H={H} Hkv={Hkv} io={io}")
