@@ -45,10 +45,14 @@ def _run(tmp_path, heads, kv_heads, tokens, max_seq, chunks="", head_dim=128):
     (40, 8, 153, 256, "37,64", 128),
     # the whole capacity through prefill chunks, then both guards
     (32, 8, 256, 256, "1,127,128", 128),
-    # shapes of the general kernels: head size 96 with group 3, head size 64
-    # with group 3 through a prefill chunk first
+    # other head layouts: head size 96 with group 3 (padded group, padded
+    # rows), head size 64 with group 3 through prefill chunks first, head
+    # size 256 (the head-256 prefill) and group 16 (two groups of 8 per KV
+    # head) through prefill chunks
     (6, 2, 90, 128, "", 96),
     (12, 4, 70, 96, "17,20", 64),
+    (4, 2, 60, 64, "9,30", 256),
+    (32, 2, 40, 48, "5,19", 128),
 ])
 def test_node_host_matches_oracle(tmp_path, heads, kv_heads, tokens, max_seq, chunks, head_dim):
     """Every token through the decode step, or the first ones through chunked
