@@ -152,8 +152,12 @@ def build_asan(jobs: int | None = None) -> Path:
 
 
 def build_variants(jobs: int | None = None) -> list:
-    """Both debug variants; each compiles every source again."""
-    return [build_check(jobs), build_asan(jobs)]
+    """Both debug variants; each compiles every source again. The two builds
+    run side by side: each is bound by its longest source (nwd_decode.hip)."""
+    with cf.ThreadPoolExecutor(max_workers=2) as ex:
+        check = ex.submit(build_check, jobs)
+        asan = ex.submit(build_asan, jobs)
+        return [check.result(), asan.result()]
 
 
 def build_bench() -> Path:
