@@ -321,7 +321,7 @@ struct DecodeArgs {
   const void* k_new;  // optional new rows [batch][n_kv][D] (fused append)
   const void* v_new;
   int new16;          // new rows are fp16 (else fp32)
-  int* counters;      // [batch][n_kv] arrival tickets, zero between calls
+  int* counters;      // [batch][n_kv] arrival tickets (the grid's n_kv), zero between calls
   int batch, n_heads, n_kv, cap, nsplit;
   int span;           // host bound on L: keys [0, span) are partitioned
   int strided;        // key layout over the splits: 0 contiguous ranges, 1 interleaved blocks

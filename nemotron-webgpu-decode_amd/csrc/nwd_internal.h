@@ -35,7 +35,7 @@ struct Workspace {
   float* part_o;     // [records][D] unnormalised partial outputs
   float2* part_ml;   // [records] (running max in log2 units, sum of weights)
   int64_t records;   // capacity in records
-  int* counters;     // [max_batch][n_kv] merge arrival tickets (zero between calls)
+  int* counters;     // merge arrival tickets per (sequence, query head group), zero between calls
   int* status;       // device status word (kStatus* bits)
 };
 
