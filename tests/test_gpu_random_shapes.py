@@ -30,7 +30,7 @@ TOL = 2e-3
 N_CASES = 200
 HEAD_DIMS = [1, 3, 8, 16, 24, 32, 40, 48, 64, 64, 72, 80, 96, 96, 100, 112, 120, 128, 128, 128,
              136, 160, 192, 200, 256, 256, 320, 512]
-GROUPS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 16, 24]
+GROUPS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 16, 24, 25, 40]
 # bound on B * H * L * D of a case, which keeps the oracle to a fraction of a second
 WORK = 60_000_000
 
