@@ -4,11 +4,14 @@
 //
 // The reference kernel takes head_dim and both head counts as parameters
 // (kernels/sparse_attn.wgsl:12-17, :38-43), so a caller may bind any of them.
-// nwd_decode.hip and nwd_prefill.hip are specialised for D = 128 and G in
-// {1, 2, 4, 5, 8} (the benchmark and Nano-4B shapes). Every other shape runs
-// here under the same contract: the same cache layout, position rules,
-// status bits, split-K records (max in log2 units, weight sum, unnormalised
-// o) and fp32 arithmetic.
+// The split and MFMA kernels (nwd_decode.hip, nwd_decode_hd.hip,
+// nwd_prefill.hip, nwd_prefill_wide.hip) take the head sizes that are
+// multiples of 8 up to 256 and, through several groups per KV head or padded
+// query rows, every group. The shapes left (other head sizes, K/V slabs above
+// 1 GiB, and the allocation-free entry point's padded groups) run here under
+// the same contract: the same cache layout, position rules, status bits,
+// split-K records (max in log2 units, weight sum, unnormalised o) and fp32
+// arithmetic.
 //
 // A 256-thread workgroup serves one split of the keys of one (sequence,
 // query) for gp query heads of one group (gp = G up to 8 at D <= 128, up to

@@ -8,7 +8,7 @@ kernels' set (head_dim 128 with a group of 1, 2, 4, 5 or 8) run the general
 kernels; these tests cover head sizes that are and are not multiples of 8,
 above 256 (two runs per thread), down to 1, and groups 3, 6, 7 and 12.
 Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
-runs the dot-product split kernel built for those sizes (csrc/nwd_decode.hip),
+runs the dot-product split kernel built for those sizes (csrc/nwd_decode_hd.hip),
 and at the other multiples of 8 up to 256 its padded form;
 test_head_size_split_decode covers its launch forms and knobs. Prefill at
 head sizes below 128 that are multiples of 8 runs the MFMA prefill kernel on
