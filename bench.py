@@ -724,14 +724,13 @@ EXTRA_WORKLOADS = {
 }
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
-# Head layouts outside the benchmark's (group 7 at head_dim 128 through the
-# padded-group decode, nwd_pad.hip; head sizes 256 and 96 on the general
-# kernels, nwd_general.hip), decode-only, B = 1:
+# Head layouts outside the benchmark's (groups 7 and 16, head sizes 256, 96
+# and 64), decode-only, B = 1:
 # name: (n_heads, n_kv_heads, head_dim, keys, description)
 GENERAL_SHAPES = {
     "general-g7-32k": (28, 4, 128, 32768, "B=1, 28q/4kv/d128 (group 7: the Qwen2.5-7B head "
-                       "layout, decoded as group 8 on padded query rows), 32768 keys, fp16 I/O, "
-                       "decode call"),
+                       "layout, on the matrix-core split kernel built for group 7), 32768 keys, "
+                       "fp16 I/O, decode call"),
     "general-d256-8k": (16, 8, 256, 8192, "B=1, 16q/8kv/d256 (group 2, head size 256: the "
                         "Gemma-2-9B layout, on the split kernel built for head size 256), 8192 "
                         "keys, fp16 I/O, decode call"),
@@ -756,6 +755,9 @@ GENERAL_PREFILL_SHAPES = {
     "general-prefill-d256": (16, 8, 256, 8192, 512, "B=1, 16q/8kv/d256 (Gemma-2-9B layout), 512 "
                              "new tokens onto 8192, fp16 I/O, prefill call (the head-256 MFMA "
                              "prefill)"),
+    "general-prefill-g7": (28, 4, 128, 8192, 512, "B=1, 28q/4kv/d128 (Qwen2.5-7B layout, group "
+                           "7), 512 new tokens onto 8192, fp16 I/O, prefill call (the MFMA "
+                           "prefill built for group 7)"),
 }
 
 SECONDARY_STEPS = {"decode-1k": 512, "decode-32k": 256, "decode-32k-nano": 256, "decode-4k": 512,

@@ -67,17 +67,16 @@ typedef struct nwd_desc {
   int32_t n_kv_heads;  /* Hkv; H must be a multiple of Hkv, any group
                           G = H/Hkv (sparse_attn.wgsl:38-39)                */
   int32_t head_dim;    /* D, 1 .. 512 (128 in engine/config.js:12). D = 128
-                          with G one of 1, 2, 4, 5, 8 runs the kernels built
-                          for those shapes, and decodes with G = 3, 6, 7 run
-                          them as G = 4, 8, 8 on zero-padded query rows
-                          (buffers allocated by nwd_create); decodes at
-                          D = 64 (G 1, 2, 4, 5, 8) and D = 256 (G 1, 2, 4, 5)
-                          run the dot-product split kernel built for those
-                          sizes, and at the other multiples of 8 up to 256
-                          its form for rows padded to 64, 128 or 256 dims;
-                          groups other than 1, 2, 4, 5, 8 (8 up to D = 128)
-                          run as several of those per KV head or on query
-                          rows padded to such groups (a K/V slab above
+                          with G from 1 to 8 runs the kernels built for
+                          those shapes; decodes at D = 64 (G 1, 2, 4, 5, 8)
+                          and D = 256 (G 1, 2, 4, 5) run the dot-product
+                          split kernel built for those sizes, and at the
+                          other multiples of 8 up to 256 its form for rows
+                          padded to 64, 128 or 256 dims, there with G = 3,
+                          6, 7 as G = 4, 8, 8 on zero-padded query rows
+                          (buffers allocated by nwd_create); larger groups
+                          run as several built groups per KV head or on
+                          query rows padded to such groups (a K/V slab above
                           1 GiB, max_seq * D * 2 bytes, takes the general
                           kernels);
                           prefills at D = 256, and at the other

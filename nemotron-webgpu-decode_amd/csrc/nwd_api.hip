@@ -41,7 +41,7 @@ struct nwd_ctx {
   int* status_host;    // pinned copy target of the device status word
   int64_t o_floats;    // floats allocated for ws.part_o
   void* q_pad;         // padded query / output rows of the padded-group decode
-  void* out_pad;       //   and prefill (groups 3, 6, 7 at D = 128), or NULL
+  void* out_pad;       //   and prefill (nwd::padded_group), or NULL
   int32_t* pos_sub;    // first positions of a padded prefill sub-chunk
   int pad_tokens;      // tokens of a padded prefill sub-chunk
   std::string err;
@@ -141,15 +141,18 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   return n < 1 ? 1 : n;
 }
 
-// Decode calls at D = 128 with a group of 3, 6 or 7 run the kernels of
-// groups 4 / 8 on padded query rows (nwd_pad.hip), at every length: the two
-// copy launches cost less than the general kernels' longer chains. Decode
-// calls on MI355X, 28q/4kv (group 7): 9.2 against 22.3 us at 1024 keys,
-// 21.0 against 40.5 at 32768; 12q/2kv (group 6): 8.8 against 20.1 at 1024
-// keys, 17.3 at 32768; 24q/8kv (group 3): 10.0 against 14.0 at 1024 keys,
-// 28.2 at 32768. The prefill of these groups runs the prefill kernels the
-// same way. The allocation-free entry point, which has no padded buffers,
-// uses the general kernels. Decode at head sizes 64 and 256 runs the
+// At D = 128 every group up to 8 has split kernels and a prefill kernel
+// built for it (groups 3, 6, 7: nwd_decode_groups.hip). At the other head
+// sizes a group of 3, 6 or 7 runs the kernels of groups 4 / 8 on padded
+// query rows (nwd_pad.hip), at every length: the two copy launches cost less
+// than the general kernels' longer chains (decode calls on MI355X at D =
+// 128, before those groups were built there, padded against general:
+// 28q/4kv (group 7) 9.2 against 22.3 us at 1024 keys, 21.0 against 40.5 at
+// 32768; 12q/2kv (group 6) 8.8 against 20.1 at 1024 keys; 24q/8kv (group
+// 3) 10.0 against 14.0; built for the group: 6.1, 16.6, 5.9 and 6.3). The
+// prefill of these groups runs the prefill kernels the same way. The
+// allocation-free entry point, which has no padded buffers, uses the
+// general kernels for them. Decode at head sizes 64 and 256 runs the
 // dot-product split kernel built for them, and at the other multiples of 8
 // up to 256 that kernel's padded form (groups 1, 2, 4, 5, and 8 up to 128;
 // larger groups as several of those per KV head, nwd::kernel_group, or

@@ -8,7 +8,8 @@
 // nwd_prefill.hip, nwd_prefill_wide.hip) take the head sizes that are
 // multiples of 8 up to 256 and, through several groups per KV head or padded
 // query rows, every group. The shapes left (other head sizes, K/V slabs above
-// 1 GiB, and the allocation-free entry point's padded groups) run here under
+// 1 GiB, and the allocation-free entry point's padded groups, which have no
+// padded buffers) run here under
 // the same contract: the same cache layout, position rules, status bits,
 // split-K records (max in log2 units, weight sum, unnormalised o) and fp32
 // arithmetic.

@@ -708,6 +708,13 @@ hipError_t launch_prefill(const Shape& s0, const void* q, const void* k_cache,
     case 4: return launch_prefill_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     case 5: return launch_prefill_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    default: break;
+  }
+  if (s.head_dim != kHeadDim) return hipErrorInvalidValue;
+  switch (s.group) {  // built at head size 128 only
+    case 3: return launch_prefill_p<3, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 6: return launch_prefill_p<6, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 7: return launch_prefill_p<7, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -4,9 +4,12 @@ any head size) with the oracle, through the C ABI.
 The reference's attention takes head_dim and both head counts as parameters
 (kernels/sparse_attn.wgsl:12-17, :38-43), and kv_append its row width
 (kernels/kv_append.wgsl:1-6, n = n_kv * hd). Shapes outside the specialised
-kernels' set (head_dim 128 with a group of 1, 2, 4, 5 or 8) run the general
-kernels; these tests cover head sizes that are and are not multiples of 8,
-above 256 (two runs per thread), down to 1, and groups 3, 6, 7 and 12.
+kernels' set (head_dim 128 with a group up to 8, and the head sizes and
+groups below) run the general kernels; these tests cover head sizes that
+are and are not multiples of 8, above 256 (two runs per thread), down to 1,
+and groups 3, 6, 7 and 12 (groups 3, 6 and 7 are built at head_dim 128,
+csrc/nwd_decode_groups.hip, and padded to 4 / 8 at the other multiples of
+8: test_group_3_6_7_*).
 Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
 runs the dot-product split kernel built for those sizes (csrc/nwd_decode_hd.hip),
 and at the other multiples of 8 up to 256 its padded form;
@@ -34,20 +37,20 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
 
-# (head_dim, n_heads, n_kv_heads): general by head size, by group, or both
+# (head_dim, n_heads, n_kv_heads) and the route each takes
 SHAPES = [
-    (64, 8, 2),     # G 4, runs of 8
-    (96, 6, 2),     # G 3
-    (80, 12, 1),    # G 12
-    (100, 3, 3),    # single-value runs (100 % 8 != 0)
-    (256, 4, 1),    # G 4, 32 runs per row
-    (256, 8, 1),    # G 8 at 256: the general kernels (the split kernel is not built for it)
-    (320, 2, 2),    # 40 runs: 6 key groups, 16 threads idle in P.V
-    (300, 2, 1),    # single values, 300 > 256 threads: two runs per thread
-    (512, 2, 1),    # the largest head size
-    (128, 6, 2),    # D 128 with group 3
-    (128, 7, 1),    # D 128 with group 7
-    (1, 4, 2),      # one dim
+    (64, 8, 2),     # G 4: the split kernel built for head size 64
+    (96, 6, 2),     # G 3 padded to 4, on the head-128 split kernel's padded form
+    (80, 12, 1),    # G 12 padded to 16 (two groups of 8), padded head form
+    (100, 3, 3),    # the general kernels, single-value runs (100 % 8 != 0)
+    (256, 4, 1),    # G 4: the split kernel built for head size 256
+    (256, 8, 1),    # G 8 at 256 (not built there): two groups of 4 per KV head
+    (320, 2, 2),    # the general kernels, 40 runs: 6 key groups, 16 threads idle in P.V
+    (300, 2, 1),    # the general kernels, single values, 300 > 256 threads: two runs per thread
+    (512, 2, 1),    # the general kernels at the largest head size
+    (128, 6, 2),    # D 128 with group 3, built for it
+    (128, 7, 1),    # D 128 with group 7, built for it
+    (1, 4, 2),      # the general kernels, one dim
 ]
 
 
@@ -436,25 +439,26 @@ def test_general_cache_rows_read_back():
         assert np.array_equal(from_cache(host(vc), 0, 9)[4:].view(np.uint16), v.view(np.uint16))
 
 
-# ----------------------------------------------- groups 3, 6, 7 at D = 128 ---
+# ----------------------------------------------------- groups 3, 6, 7 ---
 
-@pytest.mark.parametrize("H,Hkv", [(12, 4), (6, 1), (28, 4), (14, 2)])
+@pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 6, 1), (128, 28, 4), (128, 14, 2),
+                                     (64, 28, 4), (96, 12, 4)])
 @pytest.mark.parametrize("io", ["f16", "f32"])
-def test_padded_group_decode(H, Hkv, io):
-    """Groups 3, 6 and 7 at head_dim 128 run the decode kernels of groups 4
-    and 8 on padded query rows: against the oracle at 5000 and 1100 keys, with
-    two key bounds (different split partitions) within fp32 rounding of each
-    other, and the fused append bit-identical to append + decode in the
-    caches."""
-    D, cap = 128, 5010
+def test_group_3_6_7_decode(D, H, Hkv, io):
+    """Groups 3, 6 and 7 run decode kernels built for them at head_dim 128,
+    and at other head sizes the kernels of groups 4 and 8 on padded query
+    rows: against the oracle at 5000 and 1100 keys, with two key bounds
+    (different split partitions) within fp32 rounding of each other, and the
+    fused append bit-identical to append + decode in the caches."""
+    cap = 5010
     lens = [5000, 1100]
-    say(f"padded group decode {H}q/{Hkv}kv io={io}")
+    say(f"group 3/6/7 decode {H}q/{Hkv}kv/d{D} io={io}")
     g = rng(780 + H)
     rows = [_rows(g, L, Hkv, D) for L in lens]
     q = _q(g, (2, H, D), io)
     kn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
     vn = g.standard_normal((2, Hkv, D), dtype=np.float32).astype(np.float16)
-    with nw.AttnContext(H, Hkv, cap, max_batch=2, q_dtype=io, o_dtype=io) as ctx:
+    with nw.AttnContext(H, Hkv, cap, head_dim=D, max_batch=2, q_dtype=io, o_dtype=io) as ctx:
         kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
         vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
         pos = pos_tensor([L - 1 for L in lens])
@@ -468,7 +472,7 @@ def test_padded_group_decode(H, Hkv, io):
             want = oracle.sparse_attn_f32(q[b].astype(np.float32), f32(k), f32(v))
             assert max_abs(outs[cap][b], want) < TOL, b
         assert max_abs(outs[cap], outs[1000]) < (2e-3 if io == "f16" else 2e-5)  # other splits
-        # fused append + attend at the bound that takes the padded kernels
+        # fused append + attend
         res = []
         for fused in (True, False):
             kc2, vc2 = kc.clone(), vc.clone()
@@ -491,15 +495,18 @@ def test_padded_group_decode(H, Hkv, io):
             assert max_abs(res[0][0][b].astype(np.float32), want) < TOL, b
 
 
-def test_padded_group_knobs():
-    """The decode knobs apply on the padded path: forced split counts and both
-    split kernels give the same results within fp32 rounding."""
-    H, Hkv, D, L = 14, 2, 128, 3000
-    g = rng(790)
+@pytest.mark.parametrize("H,Hkv,D", [(14, 2, 128), (6, 2, 128), (14, 2, 64)])
+def test_group_3_6_7_knobs(H, Hkv, D):
+    """The decode knobs apply to groups 3, 6 and 7, built (head_dim 128) or
+    padded (64): forced split counts and both split kernels give the same
+    results within fp32 rounding."""
+    L = 3000
+    say(f"group 3/6/7 knobs {H}q/{Hkv}kv/d{D}")
+    g = rng(790 + H + D)
     k, v = _rows(g, L, Hkv, D)
     q = _q(g, (1, H, D), "f32")
     outs = []
-    with nw.AttnContext(H, Hkv, L, q_dtype="f32", o_dtype="f32") as ctx:
+    with nw.AttnContext(H, Hkv, L, head_dim=D, q_dtype="f32", o_dtype="f32") as ctx:
         kc, vc = dev(to_cache([k], Hkv, L)), dev(to_cache([v], Hkv, L))
         for n, kern in ((0, None), (3, None), (40, None), (0, 0), (0, 1)):
             ctx.set_decode_splits(n)
@@ -514,21 +521,24 @@ def test_padded_group_knobs():
         assert max_abs(o, outs[0]) < 1e-5
 
 
-@pytest.mark.parametrize("H,Hkv", [(12, 4), (7, 1)])
+@pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 7, 1), (128, 12, 2), (96, 12, 4),
+                                     (64, 7, 1)])
 @pytest.mark.parametrize("max_batch", [2, 2048])
 @pytest.mark.parametrize("io", ["f16", "f32"])
-def test_padded_group_prefill(H, Hkv, max_batch, io):
-    """Groups 3 and 7 at head_dim 128 prefill on the fp16 MFMA prefill kernels
-    of groups 4 and 8 through padded query rows: 37 queries onto pos0 90 and
-    0, row by row against the oracle's decode over keys 0..pos0+i. With
-    max_batch 2048 the context's padded buffers hold a few tokens, so the
-    chunk runs in several sub-chunks."""
-    D, n_new, pos0, cap = 128, 37, [90, 0], 140
-    say(f"padded group prefill {H}q/{Hkv}kv max_batch={max_batch} io={io}")
+def test_group_3_6_7_prefill(D, H, Hkv, max_batch, io):
+    """Groups 3, 6 and 7 prefill on the fp16 MFMA prefill kernel built for
+    them at head_dim 128, and at other head sizes on the kernels of groups 4
+    and 8 through padded query rows: 37 queries onto pos0 90 and 0, row by
+    row against the oracle's decode over keys 0..pos0+i. With max_batch 2048
+    the padded route's buffers hold a few tokens, so the chunk runs in
+    several sub-chunks."""
+    n_new, pos0, cap = 37, [90, 0], 140
+    say(f"group 3/6/7 prefill {H}q/{Hkv}kv/d{D} max_batch={max_batch} io={io}")
     g = rng(800 + H)
     rows = [_rows(g, p + n_new, Hkv, D, scale=0.5) for p in pos0]
     q = _q(g, (2, n_new, H, D), io)
-    with nw.AttnContext(H, Hkv, cap, max_batch=max_batch, q_dtype=io, o_dtype="f32") as ctx:
+    with nw.AttnContext(H, Hkv, cap, head_dim=D, max_batch=max_batch, q_dtype=io,
+                        o_dtype="f32") as ctx:
         kc = dev(to_cache([r[0] for r in rows], Hkv, cap))
         vc = dev(to_cache([r[1] for r in rows], Hkv, cap))
         out = torch.empty((2, n_new, H, D), device="cuda")
