@@ -141,9 +141,9 @@ int auto_splits(int n_heads, int n_kv_heads, int batch, int max_len) {
   return n < 1 ? 1 : n;
 }
 
-// At D = 128 every group up to 8 has split kernels and a prefill kernel
-// built for it (groups 3, 6, 7: nwd_decode_groups.hip). At the other head
-// sizes a group of 3, 6 or 7 runs the kernels of groups 4 / 8 on padded
+// At D = 128 and 64 every group up to 8 has split kernels and a prefill
+// kernel built for it (groups 3, 6, 7: nwd_decode_groups.hip). At the other
+// head sizes a group of 3, 6 or 7 runs the kernels of groups 4 / 8 on padded
 // query rows (nwd_pad.hip), at every length: the two copy launches cost less
 // than the general kernels' longer chains (decode calls on MI355X at D =
 // 128, before those groups were built there, padded against general:

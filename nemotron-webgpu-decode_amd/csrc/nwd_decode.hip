@@ -53,7 +53,7 @@
 namespace nwd {
 
 // Groups built as they are: 1, 2, 4, 5 and 8 (8 up to head size 128), and
-// at head size 128 every group up to 8 (3, 6 and 7 in
+// at head sizes 128 and 64 every group up to 8 (3, 6 and 7 in
 // nwd_decode_groups.hip). A larger group runs as groups of a built size, so
 // that each KV head's rows are read as few times as possible: kv_rep =
 // ceil(group / largest) reads. A built divisor (the largest first) that
@@ -64,7 +64,7 @@ namespace nwd {
 // 12.4; on the general kernels 43.3).
 int kernel_group(int head_dim, int group, int* kv_rep) {
   *kv_rep = 1;
-  const bool every = head_dim == kHeadDim;       // 1 .. 8 all built
+  const bool every = head_dim == kHeadDim || head_dim == 64;  // 1 .. 8 all built
   const int top = head_dim <= kHeadDim ? 8 : 5;  // group 8 is built up to head size 128
   auto built = [&](int g) {
     return g == 1 || g == 2 || g == 4 || g == 5 || g == top || (every && g >= 3 && g <= 8);

@@ -4,6 +4,7 @@
 // 64, 128, 256). A translation unit of its own, so that its kernels and
 // the head-128 ones compile side by side.
 #include "nwd_decode.h"
+#include "nwd_decode_mfma.h"
 
 namespace nwd {
 
@@ -12,7 +13,8 @@ namespace nwd {
 // to 256 in the padded form of the next of 64, 128, 256. The same
 // per-query-head rule, then one workgroup per KV head. Group 8 above 128 is
 // not built (its accumulators and query registers would not fit one lane's
-// registers) and takes the general-shape kernels.
+// registers; kernel_group runs it as two groups of 4). Groups 3, 6 and 7 at
+// head size 64 are built in nwd_decode_groups.hip.
 template <int kD, bool kPadD>
 static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                    hipStream_t stream) {
@@ -35,7 +37,9 @@ static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const De
     case 8:
       if constexpr (kD <= kHeadDim) return launch_qo<8, 1, kD, kPadD>(s, a, c, stream);
       return hipErrorInvalidValue;
-    default: return hipErrorInvalidValue;
+    default:
+      if constexpr (kD == 64 && !kPadD) return launch_decode_groups(s, a, c, stream);
+      return hipErrorInvalidValue;
   }
 }
 

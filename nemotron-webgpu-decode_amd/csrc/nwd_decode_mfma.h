@@ -464,7 +464,7 @@ static hipError_t launch_decode_128(const Shape& s, const DecodeArgs& a, const D
   return launch_qo<G>(s, a, c, stream);
 }
 
-// Head size 128, groups 3, 6 and 7 (nwd_decode_groups.hip).
+// Groups 3, 6 and 7 at head sizes 128 and 64 (nwd_decode_groups.hip).
 hipError_t launch_decode_groups(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                 hipStream_t stream);
 

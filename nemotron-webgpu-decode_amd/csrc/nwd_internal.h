@@ -66,8 +66,8 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
 
 // The group the decode and prefill kernels run a group of `group` query
 // heads as, with *kv_rep such groups per KV head: the group itself for 1, 2,
-// 4, 5 and 8 (8 only up to head size 128) and at head size 128 for every
-// group up to 8; for larger groups a built size that divides them into
+// 4, 5 and 8 (8 only up to head size 128) and at head sizes 128 and 64 for
+// every group up to 8; for larger groups a built size that divides them into
 // ceil(group / largest built size) groups; 0 when the group must be padded
 // first (padded_group).
 int kernel_group(int head_dim, int group, int* kv_rep);
@@ -107,7 +107,7 @@ int max_decode_splits(const Shape& s, const Workspace& ws, int batch);
 
 // Groups kernel_group does not map run as a padded group (padded_group; 0
 // for groups that need no padding): 3 as 4, 6 and 7 as 8 (at head sizes
-// other than 128), larger groups as the next multiple of 8 (of 5 above head
+// other than 128 and 64), larger groups as the next multiple of 8 (of 5 above head
 // size 128), where launch_decode takes the padded group at the head size
 // (padded_decode_shape), their
 // query rows copied into a padded layout (q_pad, [batch][Hkv][padded

@@ -1,20 +1,21 @@
 // nwd_pad.hip — decode and prefill with groups the kernels cannot take as
-// they are (3, 6, 7 at head sizes other than 128, and larger groups with no
-// built divisor, nwd::kernel_group) on the kernels of the next group they
-// take (nwd_decode.hip, nwd_decode_hd.hip, nwd_prefill.hip,
+// they are (3, 6, 7 at head sizes other than 128 and 64, and larger groups
+// with no built divisor, nwd::kernel_group) on the kernels of the next
+// group they take (nwd_decode.hip, nwd_decode_hd.hip, nwd_prefill.hip,
 // nwd_prefill_wide.hip), at the head sizes those kernels take (multiples of
 // 8 up to 256).
 //
 // The reference kernel maps query head h to KV head h / (H / Hkv) for any
 // group (kernels/sparse_attn.wgsl:38-39). The decode and prefill kernels
 // serve a whole group per workgroup, reading each K/V row once, for groups
-// 1, 2, 4, 5 and 8 (and at head size 128 every group up to 8). A group of
-// 3 (6, 7) is run as a group of 4 (8): the query rows are copied into a
-// padded layout with zero rows after each group's real heads, the kernels
-// run on it, and the real heads' rows are copied out. Decode is bound by the K/V stream, which the padding leaves
-// unchanged; the zero rows' outputs are discarded. A prefill chunk goes
-// through in sub-chunks sized to the context's padded buffers, each with its
-// first positions offset.
+// 1, 2, 4, 5 and 8 (and at head sizes 128 and 64 every group up to 8). A
+// group of 3 (6, 7) is run as a group of 4 (8): the query rows are copied
+// into a padded layout with zero rows after each group's real heads, the
+// kernels run on it, and the real heads' rows are copied out. Decode is
+// bound by the K/V stream, which the padding leaves unchanged; the zero
+// rows' outputs are discarded. A prefill chunk goes through in sub-chunks
+// sized to the context's padded buffers, each with its first positions
+// offset.
 #include "nwd_common.h"
 #include "nwd_internal.h"
 

@@ -710,11 +710,11 @@ hipError_t launch_prefill(const Shape& s0, const void* q, const void* k_cache,
     case 8: return launch_prefill_g<8>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     default: break;
   }
-  if (s.head_dim != kHeadDim) return hipErrorInvalidValue;
-  switch (s.group) {  // built at head size 128 only
-    case 3: return launch_prefill_p<3, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
-    case 6: return launch_prefill_p<6, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
-    case 7: return launch_prefill_p<7, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+  if (s.head_dim != kHeadDim && s.head_dim != 64) return hipErrorInvalidValue;
+  switch (s.group) {  // built at head sizes 128 and 64 (rows padded to 128)
+    case 3: return launch_prefill_g<3>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 6: return launch_prefill_g<6>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 7: return launch_prefill_g<7>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -156,11 +156,11 @@ struct Q4 {
 
 // One context of group g and head size d through every entry point: batch
 // 2, 512 positions (d = 128 runs the kernels built for each group up to 8,
-// group 4 at d = 64 and group 5 at d = 256 the decode split kernel built for
-// those sizes and the MFMA prefills, group 3 at d = 96 and group 7 at d = 64
-// the padded-group route, group 12 at d = 96 padded to two groups of 8 per
-// KV head on the padded head-size forms, group 2 at d = 100 the general
-// kernels).
+// groups 4 and 7 at d = 64 and group 5 at d = 256 the decode split kernel
+// built for those sizes and the MFMA prefills, group 3 at d = 96 and group 7
+// at d = 80 the padded-group route, group 12 at d = 96 padded to two groups
+// of 8 per KV head on the padded head-size forms, group 2 at d = 100 the
+// general kernels).
 static void gpu_cycle(int group, int d) {
   const int hkv = 8, h = hkv * group, batch = 2, max_seq = 512;
   nwd_desc desc = make_desc(h, hkv, max_seq, batch);
@@ -262,7 +262,8 @@ int main(int argc, char** argv) {
   std::fflush(stdout);
   if (gpu) {
     const int shapes[][2] = {{1, 128}, {2, 128}, {4, 128}, {5, 128}, {8, 128}, {3, 96}, {2, 100},
-                             {7, 128}, {6, 128}, {4, 64}, {5, 256}, {12, 96}, {7, 64}};
+                             {7, 128}, {6, 128}, {4, 64}, {5, 256}, {12, 96}, {7, 64},
+                             {7, 80}};
     for (const auto& gd : shapes) {
       const int before = g_calls;
       gpu_cycle(gd[0], gd[1]);

@@ -193,16 +193,16 @@ def test_q4_checked_build_matches():
 
 @pytest.mark.parametrize("Dh,H,Hkv", [(96, 6, 2), (100, 3, 3), (300, 2, 1), (128, 7, 1), (128, 12, 4),
                                       (64, 8, 2), (256, 10, 2), (128, 32, 2), (96, 18, 2),
-                                      (200, 16, 8), (64, 14, 2), (128, 12, 2)])
+                                      (200, 16, 8), (64, 14, 2), (128, 12, 2), (80, 14, 2)])
 def test_general_checked_build_matches(Dh, H, Hkv):
     """The general-shape kernels in the checked build: append, decode with
     the workspace filled exactly (max_seq 64 gives H * 256 records, and 256
     forced splits use them all, most with no key), append + decode, and a
     split prefill; nothing flagged, the product build's bits. Groups 3, 6
-    and 7 run the kernels built for them at head_dim 128 and the padded-group
-    route at 96 and 64 (the group-4 / group-8 kernels on padded rows, decode
-    and prefill); head sizes 64 and 256 the split kernel built for them
-    (decode) and the MFMA prefills."""
+    and 7 run the kernels built for them at head_dim 128 and 64 and the
+    padded-group route at 96 and 80 (the group-4 / group-8 kernels on padded
+    rows, decode and prefill); head sizes 64 and 256 the split kernel built
+    for them (decode) and the MFMA prefills."""
     say("check build general", Dh, H, Hkv)
     cap, B = 64, 1
     prod, chk = _pair(H, Hkv, cap, head_dim=Dh, o_dtype="f32")
@@ -219,7 +219,7 @@ def test_general_checked_build_matches(Dh, H, Hkv):
             c.set_decode_splits(256)
         # 256, or what the workspace holds for padded groups' heads (H * 256
         # records over Hkv * padded group heads)
-        padded = H // Hkv == 9 or (H // Hkv in (3, 6, 7) and Dh != 128)  # 9 -> 16
+        padded = H // Hkv == 9 or (H // Hkv in (3, 6, 7) and Dh not in (64, 128))  # 9 -> 16
         if not padded:
             assert prod.decode_splits(B, cap) == 256
         assert prod.decode_splits(B, cap) > 64
@@ -250,7 +250,8 @@ def test_asan_host_driver_on_gpu():
     assert "AddressSanitizer" not in res.stderr
     assert "gpu cycle group 8 head_dim 128" in res.stdout
     assert "gpu cycle group 3 head_dim 96" in res.stdout  # the padded-group route
-    assert "gpu cycle group 7 head_dim 64" in res.stdout
+    assert "gpu cycle group 7 head_dim 80" in res.stdout
+    assert "gpu cycle group 7 head_dim 64" in res.stdout  # groups 3, 6, 7 built at 64
     assert "gpu cycle group 2 head_dim 100" in res.stdout  # the general kernels' host paths
     assert "gpu cycle group 7 head_dim 128" in res.stdout  # groups 3, 6, 7 built at 128
     assert "gpu cycle group 6 head_dim 128" in res.stdout

@@ -7,9 +7,9 @@ The reference's attention takes head_dim and both head counts as parameters
 kernels' set (head_dim 128 with a group up to 8, and the head sizes and
 groups below) run the general kernels; these tests cover head sizes that
 are and are not multiples of 8, above 256 (two runs per thread), down to 1,
-and groups 3, 6, 7 and 12 (groups 3, 6 and 7 are built at head_dim 128,
-csrc/nwd_decode_groups.hip, and padded to 4 / 8 at the other multiples of
-8: test_group_3_6_7_*).
+and groups 3, 6, 7 and 12 (groups 3, 6 and 7 are built at head_dim 128 and
+64, csrc/nwd_decode_groups.hip, and padded to 4 / 8 at the other multiples
+of 8: test_group_3_6_7_*).
 Decode at head sizes 64 (groups 1, 2, 4, 5, 8) and 256 (groups 1, 2, 4, 5)
 runs the dot-product split kernel built for those sizes (csrc/nwd_decode_hd.hip),
 and at the other multiples of 8 up to 256 its padded form;
@@ -442,12 +442,12 @@ def test_general_cache_rows_read_back():
 # ----------------------------------------------------- groups 3, 6, 7 ---
 
 @pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 6, 1), (128, 28, 4), (128, 14, 2),
-                                     (64, 28, 4), (96, 12, 4)])
+                                     (64, 28, 4), (64, 12, 4), (96, 12, 4), (80, 28, 4)])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_group_3_6_7_decode(D, H, Hkv, io):
-    """Groups 3, 6 and 7 run decode kernels built for them at head_dim 128,
-    and at other head sizes the kernels of groups 4 and 8 on padded query
-    rows: against the oracle at 5000 and 1100 keys, with two key bounds
+    """Groups 3, 6 and 7 run decode kernels built for them at head_dim 128
+    and 64, and at other head sizes the kernels of groups 4 and 8 on padded
+    query rows: against the oracle at 5000 and 1100 keys, with two key bounds
     (different split partitions) within fp32 rounding of each other, and the
     fused append bit-identical to append + decode in the caches."""
     cap = 5010
@@ -495,11 +495,11 @@ def test_group_3_6_7_decode(D, H, Hkv, io):
             assert max_abs(res[0][0][b].astype(np.float32), want) < TOL, b
 
 
-@pytest.mark.parametrize("H,Hkv,D", [(14, 2, 128), (6, 2, 128), (14, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,D", [(14, 2, 128), (6, 2, 128), (14, 2, 64), (14, 2, 96)])
 def test_group_3_6_7_knobs(H, Hkv, D):
-    """The decode knobs apply to groups 3, 6 and 7, built (head_dim 128) or
-    padded (64): forced split counts and both split kernels give the same
-    results within fp32 rounding."""
+    """The decode knobs apply to groups 3, 6 and 7, built (head_dim 128 and
+    64) or padded (96): forced split counts and both split kernels give the
+    same results within fp32 rounding."""
     L = 3000
     say(f"group 3/6/7 knobs {H}q/{Hkv}kv/d{D}")
     g = rng(790 + H + D)
@@ -521,14 +521,14 @@ def test_group_3_6_7_knobs(H, Hkv, D):
         assert max_abs(o, outs[0]) < 1e-5
 
 
-@pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 7, 1), (128, 12, 2), (96, 12, 4),
-                                     (64, 7, 1)])
+@pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 7, 1), (128, 12, 2), (64, 7, 1),
+                                     (96, 12, 4), (80, 7, 1)])
 @pytest.mark.parametrize("max_batch", [2, 2048])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_group_3_6_7_prefill(D, H, Hkv, max_batch, io):
     """Groups 3, 6 and 7 prefill on the fp16 MFMA prefill kernel built for
-    them at head_dim 128, and at other head sizes on the kernels of groups 4
-    and 8 through padded query rows: 37 queries onto pos0 90 and 0, row by
+    them at head_dim 128 and 64 (rows padded to 128 dims), and at other head
+    sizes on the kernels of groups 4 and 8 through padded query rows: 37 queries onto pos0 90 and 0, row by
     row against the oracle's decode over keys 0..pos0+i. With max_batch 2048
     the padded route's buffers hold a few tokens, so the chunk runs in
     several sub-chunks."""
