@@ -12,7 +12,9 @@ every output row against the oracle's op-for-op f32 restatement of
 sparse_attn.wgsl (max-abs 2e-3, fp16 inputs widened exactly) and the
 appended cache rows bit for bit (fp16 rows copied, fp32 rows rounded to
 nearest even). The draw is fixed by the case number, so a failure names a
-case that can be rerun.
+case that can be rerun. A second sweep draws only head sizes 64 and 128 with
+groups 3, 6, 7 and the larger groups that divide into them (12, 14, 21),
+which run kernels built for those groups there.
 """
 import numpy as np
 import pytest
@@ -42,10 +44,10 @@ def _gpu():
     nw.load_library()
 
 
-def _draw(i: int) -> dict:
-    g = rng(5000 + i)
-    D = int(g.choice(HEAD_DIMS))
-    G = int(g.choice(GROUPS))
+def _draw(i: int, dims=HEAD_DIMS, groups=GROUPS, base: int = 5000) -> dict:
+    g = rng(base + i)
+    D = int(g.choice(dims))
+    G = int(g.choice(groups))
     Hkv = int(g.choice([1, 2, 4, 8]))
     H = Hkv * G
     B = int(g.integers(1, 5))
@@ -56,7 +58,7 @@ def _draw(i: int) -> dict:
     past = [int(g.integers(0, max(1, max_len - n_new))) for _ in range(B)]
     return {"D": D, "H": H, "Hkv": Hkv, "B": B, "op": op, "n_new": n_new, "past": past,
             "io": str(g.choice(["f16", "f32"])), "kv": str(g.choice(["f16", "f32"])),
-            "splits": int(g.choice([0, 0, 1, 3, 17])), "seed": 6000 + i}
+            "splits": int(g.choice([0, 0, 1, 3, 17])), "seed": base + 1000 + i}
 
 
 def _tdtype(name):
@@ -70,7 +72,17 @@ def _rows(g, n, Hkv, D, dtype="f16"):
 
 @pytest.mark.parametrize("case", range(N_CASES))
 def test_random_shape_matches_oracle(case):
-    c = _draw(case)
+    _check(_draw(case), case)
+
+
+# Groups 3, 6 and 7 (and the larger groups that divide into them) at the
+# head sizes where kernels are built for them, 64 and 128.
+@pytest.mark.parametrize("case", range(40))
+def test_random_built_group_matches_oracle(case):
+    _check(_draw(case, dims=[64, 128], groups=[3, 6, 7, 12, 14, 21], base=8000), case)
+
+
+def _check(c: dict, case: int):
     say(f"random case {case}: {c}")
     g = rng(c["seed"])
     D, H, Hkv, B, n_new, past = c["D"], c["H"], c["Hkv"], c["B"], c["n_new"], c["past"]
