@@ -747,8 +747,8 @@ GENERAL_SHAPES = {
 # Prefill on other head layouts: (heads, kv heads, head_dim, past, new tokens, description).
 GENERAL_PREFILL_SHAPES = {
     "general-prefill-d64": (32, 8, 64, 8192, 512, "B=1, 32q/8kv/d64 (Llama-3.2-1B layout), 512 "
-                            "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
-                            "padded to 128 dims)"),
+                            "new tokens onto 8192, fp16 I/O, prefill call (the MFMA prefill "
+                            "built for head size 64)"),
     "general-prefill-d96": (32, 32, 96, 8192, 512, "B=1, 32q/32kv/d96 (Phi-3-mini layout), 512 "
                             "new tokens onto 8192, fp16 I/O, prefill call (MFMA kernel, rows "
                             "padded to 128 dims)"),

@@ -79,10 +79,11 @@ typedef struct nwd_desc {
                           query rows padded to such groups (a K/V slab above
                           1 GiB, max_seq * D * 2 bytes, takes the general
                           kernels);
-                          prefills at D = 256, and at the other
+                          prefills at D = 64 and 256, and at the other
                           multiples of 8 up to 256, run MFMA prefill
-                          kernels built for D = 128 and 256 on rows padded
-                          to those dims (other groups as for decode);
+                          kernels built for D = 64, 128 and 256 on rows
+                          padded to those dims (other groups as for
+                          decode);
                           every other (D, G) runs the general kernels, with
                           the same contract and cache layout (a coverage
                           path, not tuned like the others)                   */
@@ -201,8 +202,9 @@ int nwd_append_decode_noalloc(const nwd_desc* desc, const void* q, const void* k
  * an fp32 q is scaled by scale * log2(e) and carried as fp16 high and low
  * parts (~22 bits). A scaled fp32 q element beyond the fp16 range (65504)
  * makes nwd_device_status report NWD_ERR_DEVICE (head sizes up to 256 run
- * these kernels, or a head-256 form of them, on rows padded with zeros to
- * 128 or 256 dims, and padded groups on padded query rows, in sub-chunks).
+ * these kernels, or head-64 and head-256 forms of them, on rows padded with
+ * zeros to 64, 128 or 256 dims, and padded groups on padded query rows, in
+ * sub-chunks).
  * The shapes of the general kernels
  * (see nwd_desc.head_dim) compute in fp32 on the vector units instead. A chunk
  * outside the cache (pos0[b] < 0 or pos0[b] + n_new > max_seq) is flagged in

@@ -57,7 +57,8 @@ DEVICE_FLAGS = [
 # Per-source flags. The prefill kernel's scores are finite or -inf (masked),
 # so its max reductions need no NaN quieting: without it each fmaxf operand
 # costs an extra v_max (measured 12% of the kernel's time).
-FILE_FLAGS = {"nwd_prefill.hip": ["-fno-honor-nans"], "nwd_prefill_wide.hip": ["-fno-honor-nans"]}
+FILE_FLAGS = {"nwd_prefill.hip": ["-fno-honor-nans"], "nwd_prefill_d64.hip": ["-fno-honor-nans"],
+              "nwd_prefill_wide.hip": ["-fno-honor-nans"]}
 
 # Host-only AddressSanitizer: -Xarch_host sits right before each -fsanitize=,
 # so the device code is built exactly as in the product library.
