@@ -26,9 +26,9 @@
 //     bytes at +16l), double-buffered: the next tile's copies are issued
 //     between the current tile's K fragment reads and land while it is
 //     computed; one wait plus one barrier per tile publish them. Rows are
-//     unpadded (256 B); the 16-byte chunks of a row are XOR-swizzled by the
-//     row index so the MFMA operand reads hit distinct banks (each lane
-//     fetches the chunk its LDS slot must hold);
+//     unpadded (256 B at head size 128, 128 B at 64); the 16-byte chunks of
+//     a row are XOR-swizzled by the row index so the MFMA operand reads hit
+//     distinct banks (each lane fetches the chunk its LDS slot must hold);
 //   - S^T = K Q^T on v_mfma_f32_16x16x32_f16 (K from LDS as the A operand,
 //     all 16 fragments of a tile read before its MFMAs, the query rows held
 //     in registers as the B operand), so each lane holds 4 consecutive keys
@@ -87,6 +87,7 @@ constexpr int kPBN = 128;                   // keys per tile
 constexpr int kRB = 2;                      // 16-row MFMA blocks per wavefront
 constexpr int kKB = 4;                      // 16-key blocks per wavefront per tile
 constexpr float kPSlack = 8.f;              // lazy-rescale slack, log2 units
+// Head size 128 (the kernel body takes these from PRow<kD> below):
 constexpr int kRowBytes = kHeadDim * 2;     // 256: K/V rows are unpadded in LDS
 constexpr int kTileBytes = kPBN * kRowBytes;  // 32 KB
 constexpr int kStageInsts = kTileBytes / (kPWaves * 1024);  // 1 KB per wave per load (4)

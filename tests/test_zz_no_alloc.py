@@ -74,15 +74,16 @@ def test_noalloc_matches_context_entry_point():
 
 
 @pytest.mark.parametrize("H,Hkv,Dg", [(9, 3, 100), (8, 2, 96), (16, 4, 64), (10, 2, 256),
-                                      (14, 2, 128)])
+                                      (14, 2, 128), (14, 2, 64)])
 def test_noalloc_general_shape_matches_context_entry_point(H, Hkv, Dg):
     """The same at other shapes: the general kernels (head_dim 100, group
     3), the split kernel's padded form (head_dim 96), the split kernel built
-    for head sizes 64 and 256, and group 7 at head_dim 128, their records in
-    the scratch, two calls in a row (the second smaller), bit-identical to
-    nwd_append_decode. (Groups 3, 6 and 7 that the context decodes as padded
-    groups, at head sizes other than 128, take the general kernels here,
-    which have no padded buffers: not the same bits.)"""
+    for head sizes 64 and 256, and group 7 at head_dim 128 and 64, their
+    records in the scratch, two calls in a row (the second smaller),
+    bit-identical to nwd_append_decode. (Groups 3, 6 and 7 that the context
+    decodes as padded groups, at head sizes other than 128 and 64, take the
+    general kernels here, which have no padded buffers: not the same
+    bits.)"""
     cap = 4096
     g = rng(910 + Dg)
     cases = [(2, [4000, 1500], 0), (1, [200], 256)]
