@@ -179,9 +179,14 @@ int nwd_append_decode(nwd_ctx* ctx, const void* q, const void* k_new,
  * split-K records live in a static 16 MiB device array of the library (one
  * per GPU, held until the process ends), so a call whose records would not
  * fit (batch * n_heads * splits > 32262 when it splits) fails with
- * NWD_ERR_CAPACITY before any launch. The merge always runs as a separate
- * kernel. Results are bit-identical to nwd_append_decode on a context made
- * from the same descriptor (default merge form, automatic split count).
+ * NWD_ERR_CAPACITY before any launch; records hold 128 floats up to head_dim
+ * 128, 256 up to 256 (multiples of 8), head_dim otherwise. The merge always
+ * runs as a separate kernel. Results are bit-identical to nwd_append_decode
+ * on a context made from the same descriptor (default merge form, automatic
+ * split count), except for the groups a context runs on padded query rows
+ * (3, 6 and 7 at head sizes other than 64 and 128, and larger groups with no
+ * built divisor), which take the general kernels here (no padded buffers):
+ * the same results within fp32 rounding.
  * status, if not NULL, is a caller-owned device int32 that gets bit 1 OR-ed
  * in when a position is outside [0, max_seq) (nothing is written there and
  * attention is clamped, as in nwd_append_decode); with NULL such a position
