@@ -16,6 +16,8 @@ case that can be rerun. A second sweep draws only head sizes 64 and 128 with
 groups 3, 6, 7 and the larger groups that divide into them (12, 14, 21),
 which run kernels built for those groups there.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -29,7 +31,11 @@ from gpu_util import dev, host, pos_tensor, say  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
-N_CASES = 200
+# Case counts and the first seed can be raised for a longer sweep, e.g.
+# NWD_RANDOM_CASES=2000 NWD_RANDOM_BASE=20000 NWD_RANDOM_BUILT_CASES=500.
+N_CASES = int(os.environ.get("NWD_RANDOM_CASES", "200"))
+BASE = int(os.environ.get("NWD_RANDOM_BASE", "5000"))
+N_BUILT = int(os.environ.get("NWD_RANDOM_BUILT_CASES", "40"))
 HEAD_DIMS = [1, 3, 8, 16, 24, 32, 40, 48, 64, 64, 72, 80, 96, 96, 100, 112, 120, 128, 128, 128,
              136, 160, 192, 200, 256, 256, 320, 512]
 GROUPS = [1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 16, 24, 25, 40]
@@ -72,14 +78,14 @@ def _rows(g, n, Hkv, D, dtype="f16"):
 
 @pytest.mark.parametrize("case", range(N_CASES))
 def test_random_shape_matches_oracle(case):
-    _check(_draw(case), case)
+    _check(_draw(case, base=BASE), case)
 
 
 # Groups 3, 6 and 7 (and the larger groups that divide into them) at the
 # head sizes where kernels are built for them, 64 and 128.
-@pytest.mark.parametrize("case", range(40))
+@pytest.mark.parametrize("case", range(N_BUILT))
 def test_random_built_group_matches_oracle(case):
-    _check(_draw(case, dims=[64, 128], groups=[3, 6, 7, 12, 14, 21], base=8000), case)
+    _check(_draw(case, dims=[64, 128], groups=[3, 6, 7, 12, 14, 21], base=BASE + 3000), case)
 
 
 def _check(c: dict, case: int):
