@@ -101,16 +101,18 @@ def _compile(src: Path, objdir: Path = OBJ, extra: tuple = ()) -> Path:
     return out
 
 
-def _build_lib(lib: Path, objdir: Path, extra: tuple = (), link_extra: tuple = (),
-               jobs: int | None = None) -> Path:
+def _sources() -> list:
+    """csrc/*.hip, the largest first: the longest compiles start at once."""
+    return sorted(CSRC.glob("*.hip"), key=lambda p: (-p.stat().st_size, p.name))
+
+
+def _check_hipcc() -> None:
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found: the HIP library cannot be built")
-    objdir.mkdir(parents=True, exist_ok=True)
+
+
+def _link(lib: Path, objs: list, link_extra: tuple = ()) -> Path:
     lib.parent.mkdir(parents=True, exist_ok=True)
-    sources = sorted(CSRC.glob("*.hip"))
-    jobs = jobs or min(len(sources), os.cpu_count() or 1, 8)
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(s, objdir, extra), sources))
     tmp = lib.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_extra, "-o", str(tmp),
            *map(str, objs)]
@@ -119,6 +121,17 @@ def _build_lib(lib: Path, objdir: Path, extra: tuple = (), link_extra: tuple = (
         raise RuntimeError(f"link of {lib.name} failed:\n{res.stdout}{res.stderr}")
     os.replace(tmp, lib)
     return lib
+
+
+def _build_lib(lib: Path, objdir: Path, extra: tuple = (), link_extra: tuple = (),
+               jobs: int | None = None) -> Path:
+    _check_hipcc()
+    objdir.mkdir(parents=True, exist_ok=True)
+    sources = _sources()
+    jobs = jobs or min(len(sources), os.cpu_count() or 1, 8)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda s: _compile(s, objdir, extra), sources))
+    return _link(lib, sorted(objs), link_extra)
 
 
 def build(jobs: int | None = None) -> Path:
@@ -139,6 +152,11 @@ def build_asan(jobs: int | None = None) -> Path:
     leaves the ASan runtime to the program that loads it: the driver links it
     in, so nothing is preloaded."""
     _build_lib(ASAN_LIB, OBJ / "asan", tuple(ASAN_HOST_FLAGS), jobs=jobs)
+    _build_asan_driver()
+    return ASAN_LIB
+
+
+def _build_asan_driver() -> None:
     tmp = ASAN_DRIVER.with_suffix(".tmp")
     # a host-only program (no .hip source): hipcc drives clang, whose ASan
     # runtime matches the library's instrumentation
@@ -149,7 +167,6 @@ def build_asan(jobs: int | None = None) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"ASan driver build failed:\n{res.stdout}{res.stderr}")
     os.replace(tmp, ASAN_DRIVER)
-    return ASAN_LIB
 
 
 def build_variants(jobs: int | None = None) -> list:
@@ -159,6 +176,29 @@ def build_variants(jobs: int | None = None) -> list:
         check = ex.submit(build_check, jobs)
         asan = ex.submit(build_asan, jobs)
         return [check.result(), asan.result()]
+
+
+def build_all(jobs: int | None = None) -> list:
+    """The product library and both debug variants from one pool of compile
+    jobs (every source three times, the largest first), then their links,
+    the ASan driver and the bench library: about the time of the product
+    build plus a third, where build() and build_variants() in turn take
+    about twice it. Returns the three library paths."""
+    _check_hipcc()
+    forms = [(LIB, OBJ, ()), (CHECK_LIB, OBJ / "check", ("-DNWD_CHECK",)),
+             (ASAN_LIB, OBJ / "asan", tuple(ASAN_HOST_FLAGS))]
+    for _, objdir, _ in forms:
+        objdir.mkdir(parents=True, exist_ok=True)
+    tasks = [(src, objdir, extra) for src in _sources() for _, objdir, extra in forms]
+    jobs = jobs or min(len(tasks), os.cpu_count() or 1, 8)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(lambda t: _compile(*t), tasks))
+    libs = []
+    for i, (lib, _, _) in enumerate(forms):
+        libs.append(_link(lib, sorted(objs[i::len(forms)])))
+    _build_asan_driver()
+    build_bench()
+    return libs
 
 
 def build_bench() -> Path:
@@ -200,7 +240,8 @@ if __name__ == "__main__":
     ap.add_argument("--variants", action="store_true",
                     help="also build lib/check and lib/asan (debug variants)")
     args = ap.parse_args()
-    print(build(args.jobs))
-    print(build_addon())
     if args.variants:
-        print(build_variants(args.jobs))
+        print(build_all(args.jobs))
+    else:
+        print(build(args.jobs))
+    print(build_addon())
