@@ -175,6 +175,9 @@ __device__ inline void lds_reads_done(f16x4 (&v)[8]) {
                :
                : "memory");
 }
+__device__ inline void lds_reads_done(f16x4 (&v)[4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]) : : "memory");
+}
 
 // D = A B + C on v_mfma_f32_16x16x32_f16: lane (r = lane % 16, q = lane / 16)
 // holds A[r][8q .. 8q+7], B[8q .. 8q+7][r] and D[4q .. 4q+3][r].

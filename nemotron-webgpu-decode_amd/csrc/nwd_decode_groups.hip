@@ -11,12 +11,15 @@
 namespace nwd {
 
 // Head size 64: the per-query-head form when it fits the chip, else one
-// workgroup per KV head, as for the other groups there (nwd_decode_hd.hip).
+// workgroup per KV head, on the matrix-core kernel where prefer_mfma says
+// so, as for the other groups there (nwd_decode_hd.hip).
 template <int G>
 static hipError_t launch_decode_64(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                    hipStream_t stream) {
+  if (c.kernel == 1) return launch_mfma_d64(s, a, c, stream);  // nwd_set_decode_kernel
   if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups)
     return launch_qo<1, G, 64, false>(s, a, c, stream);
+  if (prefer_mfma(G, s, c)) return launch_mfma_d64(s, a, c, stream);
   return launch_qo<G, 1, 64, false>(s, a, c, stream);
 }
 

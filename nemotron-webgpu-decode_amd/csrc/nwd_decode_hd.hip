@@ -8,16 +8,20 @@
 
 namespace nwd {
 
-// Head sizes other than 128 (decode_split_kernel only; the matrix-core
-// kernel is built for 128): 64 and 256 as they are, other multiples of 8 up
-// to 256 in the padded form of the next of 64, 128, 256. The same
-// per-query-head rule, then one workgroup per KV head. Group 8 above 128 is
+// Head sizes other than 128: 64 and 256 as they are, other multiples of 8
+// up to 256 in the padded form of the next of 64, 128, 256. The same
+// per-query-head rule, then one workgroup per KV head, at head size 64 on
+// the matrix-core kernel where prefer_mfma says so (nwd_decode_mfma64.hip),
+// otherwise on decode_split_kernel. Group 8 above 128 is
 // not built (its accumulators and query registers would not fit one lane's
 // registers; kernel_group runs it as two groups of 4). Groups 3, 6 and 7 at
 // head size 64 are built in nwd_decode_groups.hip.
 template <int kD, bool kPadD>
 static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                    hipStream_t stream) {
+  if constexpr (kD == 64 && !kPadD) {
+    if (c.kernel == 1) return launch_mfma_d64(s, a, c, stream);  // nwd_set_decode_kernel
+  }
   if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups) {
     switch (s.group) {
       case 2: return launch_qo<1, 2, kD, kPadD>(s, a, c, stream);
@@ -28,6 +32,10 @@ static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const De
         break;
       default: break;
     }
+  }
+  if constexpr (kD == 64 && !kPadD) {  // groups 3, 6, 7: launch_decode_groups
+    if (s.group != 3 && s.group != 6 && s.group != 7 && prefer_mfma(s.group, s, c))
+      return launch_mfma_d64(s, a, c, stream);
   }
   switch (s.group) {
     case 1: return launch_qo<1, 1, kD, kPadD>(s, a, c, stream);

@@ -78,22 +78,45 @@ static_assert(kMLdsBytes <= 160 * 1024, "LDS of one gfx950 CU");
 // transpose reads (4 rows x 2 chunks per 16 lanes) hit 8 distinct chunks.
 __device__ inline int vswz_m(int r) { return (r & 7) << 1; }
 
+// The workgroup's shape at head size kD: 128, or 64 (128-byte rows: half
+// the K fragments, V copies and O blocks per block, and more blocks in
+// flight per wavefront for the same bytes). The head-64 V rows take the
+// chunk swizzle of the head-64 prefill: the row index halved, so the 4 rows
+// of a transpose read (two per 256 bytes) still hit distinct chunk pairs.
+constexpr int kMDepth64 = 4;
+template <int kD>
+struct MShape {
+  static constexpr int kSlot = kMWaveKeys * kD * 2;             // one V block
+  static constexpr int kDepth = kD == kHeadDim ? kMDepth : kMDepth64;
+  static constexpr int kLoads = kD / 32 + kSlot / 1024;         // K fragments + V copies
+  static constexpr size_t kLds = (size_t)kMWaves * kDepth * kSlot;
+  static constexpr int kChunks = kD / 8;                        // 16-byte chunks per row
+  static constexpr int kCopyRows = 1024 / (kD * 2);             // rows per V copy
+};
+static_assert(MShape<64>::kLoads * (MShape<64>::kDepth - 1) <= 63, "vmcnt counts at most 63 loads");
+template <int kD>
+__device__ inline int vswz_md(int r) { return kD == kHeadDim ? vswz_m(r) : ((r >> 1) & 3) << 1; }
+
 // s_waitcnt vmcnt(n) that the compiler keeps in place: memory accesses do
 // not move across it.
 template <int n>
 __device__ inline void wait_vm_keep() {
-  static_assert(n == 0 || n == 8, "instantiated counts");
+  static_assert(n == 0 || n == 8 || n == 12, "instantiated counts");
   if constexpr (n == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if constexpr (n == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  if constexpr (n == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
 }
 __device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
 
-template <int G, bool kQ16, bool kO16>
-__global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeArgs a) {
+template <int G, bool kQ16, bool kO16, int kD>
+__device__ __forceinline__ void decode_mfma_body(const DecodeArgs a) {
+  constexpr int kMSlotBytes = MShape<kD>::kSlot, kMDepth = MShape<kD>::kDepth;
+  constexpr int kMBlockLoads = MShape<kD>::kLoads;
+  constexpr int kChunks = MShape<kD>::kChunks, kCopyRows = MShape<kD>::kCopyRows;
+  constexpr int kDB = kD / 32, kDBlk = kD / 16;
   static_assert(G <= 16, "the heads of a group are the MFMA's 16 columns");
-  static_assert(kMBlockLoads == 8, "wait counts below assume 8 loads per block");
   static_assert(G * 32 <= kMThreads, "one 4-dim run of each head per thread");
-  static_assert((size_t)kMWaves * G * (kHeadDim + 2) * 4 <= kMLdsBytes,
+  static_assert((size_t)kMWaves * G * (kD + 2) * 4 <= MShape<kD>::kLds,
                 "the end of the kernel reuses the ring");
   extern __shared__ __attribute__((aligned(16))) f16 dsmem[];
   char* lds = reinterpret_cast<char*>(dsmem);
@@ -116,21 +139,21 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const int t0 = a.strided ? split * kMBlockKeys : u0 * kUnitKeys;
   const int it_keys = a.strided ? nsplit * kMBlockKeys : kMBlockKeys;
   const int t1h = min(a.span, u1 * kUnitKeys);
-  const int64_t slab = (int64_t)(b * nkv_m + kv_m) * a.cap * kHeadDim;
+  const int64_t slab = (int64_t)(b * nkv_m + kv_m) * a.cap * kD;
   auto slab_rsrc = [&](f16* cache, int end_key) {
-    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kHeadDim * 2),
+    return __builtin_amdgcn_make_buffer_rsrc(cache + slab, 0, end_key * (kD * 2),
                                              kBufferWord3);
   };
   char* const ring = lds + wave * (kMDepth * kMSlotBytes);
 
   struct KFrag {
-    f16x8 k[4];  // [32-dim block]
+    f16x8 k[kDB];  // [32-dim block]
   };
   auto load_k = [&](KFrag& f, const __amdgpu_buffer_rsrc_t rk, int it) {
     const int key0 = t0 + it * it_keys + wave * kMWaveKeys;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const uint32_t off = (uint32_t)(key0 + lr) * (kHeadDim * 2) + db * 64 + lq * 16;
+    for (int db = 0; db < kDB; ++db) {
+      const uint32_t off = (uint32_t)(key0 + lr) * (kD * 2) + db * 64 + lq * 16;
       f.k[db] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
     }
   };
@@ -142,10 +165,11 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     char* dst = ring + slot * kMSlotBytes;
 #pragma unroll
     for (int i = 0; i < kMSlotBytes / 1024; ++i) {
-      const int row = 4 * i + lq;
+      const int row = kCopyRows * i + (kD == kHeadDim ? lq : lane / kChunks);
+      const int pc = kD == kHeadDim ? lr : lane % kChunks;  // physical chunk
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rv, (lds_void*)(dst + i * 1024), 16,
-          (uint32_t)(key0 + row) * (kHeadDim * 2) + ((lr ^ vswz_m(row)) << 4), 0, 0,
+          (uint32_t)(key0 + row) * (kD * 2) + ((pc ^ vswz_md<kD>(row)) << 4), 0, 0,
           kStreamPolicy);
     }
   };
@@ -154,12 +178,12 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   // lane's fragments hold, and V logical chunk lr), before the position
   // says which split owns them.
   const bool has_new = a.k_new != nullptr;
-  SrcRun nk_raw[4], nv_raw;
+  SrcRun nk_raw[kDB], nv_raw;
   if (has_new) {
-    const int64_t src = (int64_t)(b * nkv_m + kv_m) * kHeadDim;
+    const int64_t src = (int64_t)(b * nkv_m + kv_m) * kD;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) nk_raw[db] = load_src_run_raw(a.k_new, src + db * 32 + 8 * lq, a.new16);
-    nv_raw = load_src_run_raw(a.v_new, src + 8 * lr, a.new16);
+    for (int db = 0; db < kDB; ++db) nk_raw[db] = load_src_run_raw(a.k_new, src + db * 32 + 8 * lq, a.new16);
+    nv_raw = load_src_run_raw(a.v_new, src + 8 * (kD == kHeadDim ? lr : lr % kChunks), a.new16);
   }
 
   // The first kMDepth - 1 blocks are requested before the position is
@@ -180,13 +204,13 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
 
   // Q^T: column lr is head h0 + lr; the rows past the group are zero.
   const int h0 = hkv * G;
-  f16x8 qh[4], ql[kQ16 ? 1 : 4];
+  f16x8 qh[kDB], ql[kQ16 ? 1 : kDB];
   bool q_range = false;
   {
     const bool qv = lr < G;
-    const int64_t qrow = ((int64_t)b * a.n_heads + h0 + (qv ? lr : 0)) * kHeadDim + 8 * lq;
+    const int64_t qrow = ((int64_t)b * a.n_heads + h0 + (qv ? lr : 0)) * kD + 8 * lq;
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < kDB; ++db) {
       if constexpr (kQ16) {
         const f16x8 h = *reinterpret_cast<const f16x8*>(static_cast<const f16*>(a.q) + qrow + db * 32);
         qh[db] = qv ? h : f16x8{};
@@ -224,33 +248,33 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   const int it_new = owns_new ? (pnew - t0) / it_keys : -1;
   const int w_new = owns_new ? (pnew - t0) % it_keys / kMWaveKeys : -1;
   const int r_new = (pnew - t0) % kMWaveKeys;
-  f16x8 nk[4], nv;
+  f16x8 nk[kDB], nv;
   if (owns_new) {
 #pragma unroll
-    for (int db = 0; db < 4; ++db) nk[db] = convert_src_run(nk_raw[db], a.new16);
+    for (int db = 0; db < kDB; ++db) nk[db] = convert_src_run(nk_raw[db], a.new16);
     nv = convert_src_run(nv_raw, a.new16);
     // K chunks 4 db + lq from the lanes of key row 0, V chunk lr from lane
     // group 0
     if (wave == w_new && kv_m * a.kv_rep == hkv) {
-      const int64_t at = slab + (int64_t)pnew * kHeadDim;
-      const int64_t cache_elems = (int64_t)a.batch * nkv_m * a.cap * kHeadDim;
+      const int64_t at = slab + (int64_t)pnew * kD;
+      const int64_t cache_elems = (int64_t)a.batch * nkv_m * a.cap * kD;
       if (lr == 0) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db) {
+        for (int db = 0; db < kDB; ++db) {
           const int64_t e = at + db * 32 + 8 * lq;
           if (in_bounds(e, 8, cache_elems, a.status)) *reinterpret_cast<f16x8*>(a.k_cache + e) = nk[db];
         }
       }
-      if (lq == 0 && in_bounds(at + 8 * lr, 8, cache_elems, a.status))
+      if (lq == 0 && lr < kChunks && in_bounds(at + 8 * lr, 8, cache_elems, a.status))
         *reinterpret_cast<f16x8*>(a.v_cache + at + 8 * lr) = nv;
     }
   }
 
   const float c = a.qk_scale_log2;
   float m = kNegBig, lsum = 0.f;  // head lr: reference point (log2 units), sum of weights
-  f32x4 o[8];                     // O^T: dims 16 dblk + 4 lq .. +4 of head lr
+  f32x4 o[kDBlk];                 // O^T: dims 16 dblk + 4 lq .. +4 of head lr
 #pragma unroll
-  for (int d = 0; d < 8; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int d = 0; d < kDBlk; ++d) o[d] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](KFrag& f, int it, int slot) {
     wait_vm_keep<kMBlockLoads * (kMDepth - 1)>();  // block it's K fragments and V rows are in
@@ -261,8 +285,9 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     if (it == it_new && wave == w_new) {
       const bool sub = lr == r_new;
 #pragma unroll
-      for (int db = 0; db < 4; ++db) f.k[db] = sub ? nk[db] : f.k[db];
-      if (lq == 0) *reinterpret_cast<f16x8*>(vs + r_new * (kHeadDim * 2) + ((lr ^ vswz_m(r_new)) << 4)) = nv;
+      for (int db = 0; db < kDB; ++db) f.k[db] = sub ? nk[db] : f.k[db];
+      if (lq == 0 && lr < kChunks)
+        *reinterpret_cast<f16x8*>(vs + r_new * (kD * 2) + ((lr ^ vswz_md<kD>(r_new)) << 4)) = nv;
     }
     if (partial) {
       // Rows at or past t1: zeros past the descriptor's end, or stale cache
@@ -270,14 +295,16 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
       // Inf or NaN times a zero weight would be NaN, so they are zeroed.
 #pragma unroll
       for (int i = 0; i < kMSlotBytes / 1024; ++i) {
-        const int row = 4 * i + lq;
-        if (key0 + row >= t1) *reinterpret_cast<u32x4*>(vs + row * (kHeadDim * 2) + (lr << 4)) = u32x4{0u, 0u, 0u, 0u};
+        const int row = kCopyRows * i + (kD == kHeadDim ? lq : lane / kChunks);
+        const int pc = kD == kHeadDim ? lr : lane % kChunks;
+        if (key0 + row >= t1)
+          *reinterpret_cast<u32x4*>(vs + row * (kD * 2) + (pc << 4)) = u32x4{0u, 0u, 0u, 0u};
       }
     }
     // S^T: s[e] = q . k for key key0 + 4 lq + e, head lr.
     f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
+    for (int db = 0; db < kDB; ++db) {
       s = mfma16x16x32(f.k[db], qh[db], s);
       if constexpr (!kQ16) s = mfma16x16x32(f.k[db], ql[db], s);
     }
@@ -286,11 +313,11 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     // layout (keys 4 lq .. 4 lq + 3 of column lr) is that of S^T, so the
     // weights need no data movement between lanes.
     const int vr0 = 4 * lq + (lr >> 2);
-    f16x4 vf[8];
+    f16x4 vf[kDBlk];
 #pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk)
-      vf[dblk] = lds_read_tr16_asm(vs + vr0 * (kHeadDim * 2) +
-                                   (((2 * dblk + ((lr >> 1) & 1)) ^ vswz_m(vr0)) << 4) + 8 * (lr & 1));
+    for (int dblk = 0; dblk < kDBlk; ++dblk)
+      vf[dblk] = lds_read_tr16_asm(vs + vr0 * (kD * 2) +
+                                   (((2 * dblk + ((lr >> 1) & 1)) ^ vswz_md<kD>(vr0)) << 4) + 8 * (lr & 1));
     const float mu = m > kNegBig ? m : 0.f;
     float st[4];
 #pragma unroll
@@ -306,7 +333,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
         const float al = fast_exp2(m - ax);
         lsum *= al;
 #pragma unroll
-        for (int d = 0; d < 8; ++d) o[d] *= al;
+        for (int d = 0; d < kDBlk; ++d) o[d] *= al;
         m = ax;
         const float dd = mu_now - ax;
 #pragma unroll
@@ -343,7 +370,7 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
     lsum += ls;
     lds_reads_done(vf);
 #pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk) {
+    for (int dblk = 0; dblk < kDBlk; ++dblk) {
       o[dblk] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dblk], ph, o[dblk], 0, 0, 0);
       o[dblk] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[dblk], pl, o[dblk], 0, 0, 0);
     }
@@ -369,11 +396,11 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   lsum = sum_xor32(sum_xor16(lsum));  // the head's sum over its 4 lane groups
   __syncthreads();
   float* lds_o = reinterpret_cast<float*>(lds);
-  float* lds_ml = lds_o + kMWaves * G * kHeadDim;
+  float* lds_ml = lds_o + kMWaves * G * kD;
   if (lr < G) {
 #pragma unroll
-    for (int dblk = 0; dblk < 8; ++dblk)
-      *reinterpret_cast<f32x4*>(&lds_o[(wave * G + lr) * kHeadDim + dblk * 16 + 4 * lq]) = o[dblk];
+    for (int dblk = 0; dblk < kDBlk; ++dblk)
+      *reinterpret_cast<f32x4*>(&lds_o[(wave * G + lr) * kD + dblk * 16 + 4 * lq]) = o[dblk];
     if (lq == 0) {
       lds_ml[(wave * G + lr) * 2] = m;
       lds_ml[(wave * G + lr) * 2 + 1] = lsum;
@@ -381,16 +408,29 @@ __global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeA
   }
   __syncthreads();
   const int64_t hrow0 = (int64_t)b * a.n_heads + h0;
-  store_split_states<G, kO16, kMWaves>(a, lds_o, lds_ml, hrow0, split);
+  store_split_states<G, kO16, kMWaves, kD>(a, lds_o, lds_ml, hrow0, split);
   if (nsplit == 1 || !a.fused_merge) return;
-  merge_on_last_arrival<G, kO16>(a, a.counters + b * a.n_kv + hkv,
-                                 hrow0);
+  merge_on_last_arrival<G, kO16, kD>(a, a.counters + b * a.n_kv + hkv, hrow0);
 }
 
 template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kMThreads, 1) void decode_mfma_kernel(const DecodeArgs a) {
+  decode_mfma_body<G, kQ16, kO16, kHeadDim>(a);
+}
+// Head size 64 (nwd_decode_mfma64.hip).
+template <int G, bool kQ16, bool kO16>
+__global__ __launch_bounds__(kMThreads, 1) void decode_mfma_d64_kernel(const DecodeArgs a) {
+  decode_mfma_body<G, kQ16, kO16, 64>(a);
+}
+
+template <int G, bool kQ16, bool kO16, int kD = kHeadDim>
 static hipError_t launch_mfma_t(const DecodeArgs& a, int batch, hipStream_t stream, void* ev_start,
                                 void* ev_stop) {
-  auto kern = decode_mfma_kernel<G, kQ16, kO16>;
+  constexpr size_t kMLdsBytes = MShape<kD>::kLds;
+  auto kern = [] {
+    if constexpr (kD == kHeadDim) return decode_mfma_kernel<G, kQ16, kO16>;
+    else return decode_mfma_d64_kernel<G, kQ16, kO16>;
+  }();
   // The ring exceeds the 64 KB default of dynamic LDS: raise the kernel's
   // limit once per device (the attribute is per device).
   static std::atomic<uint64_t> attr_set{0};
@@ -415,21 +455,29 @@ static hipError_t launch_mfma_t(const DecodeArgs& a, int batch, hipStream_t stre
     e = hipGetLastError();
   }
   if (e != hipSuccess || a.nsplit == 1 || a.fused_merge) return e;
-  decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
-      a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
+  if constexpr (kD == kHeadDim)
+    decode_merge_kernel<kO16><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
+        a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
+  else
+    decode_merge_hd_kernel<kO16, kD><<<dim3((unsigned)a.n_heads, (unsigned)batch), 64, 0, stream>>>(
+        a.part_o, a.part_ml, a.out, a.n_heads, a.nsplit, a.records, a.status);
   return hipGetLastError();
 }
 
-template <int G>
+template <int G, int kD = kHeadDim>
 static hipError_t launch_mfma(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                               hipStream_t st) {
   const int B = c.batch;
   if (s.q16)
-    return s.o16 ? launch_mfma_t<G, true, true>(a, B, st, c.ev_start, c.ev_stop)
-                 : launch_mfma_t<G, true, false>(a, B, st, c.ev_start, c.ev_stop);
-  return s.o16 ? launch_mfma_t<G, false, true>(a, B, st, c.ev_start, c.ev_stop)
-               : launch_mfma_t<G, false, false>(a, B, st, c.ev_start, c.ev_stop);
+    return s.o16 ? launch_mfma_t<G, true, true, kD>(a, B, st, c.ev_start, c.ev_stop)
+                 : launch_mfma_t<G, true, false, kD>(a, B, st, c.ev_start, c.ev_stop);
+  return s.o16 ? launch_mfma_t<G, false, true, kD>(a, B, st, c.ev_start, c.ev_stop)
+               : launch_mfma_t<G, false, false, kD>(a, B, st, c.ev_start, c.ev_stop);
 }
+
+// The matrix-core kernel at head size 64, groups 1 to 8 (nwd_decode_mfma64.hip).
+hipError_t launch_mfma_d64(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
+                           hipStream_t stream);
 
 // Kernel choice at head size 128 for groups of G query heads per KV head.
 // When one workgroup per (sequence, query head, split) fits the chip, each
@@ -448,7 +496,17 @@ static hipError_t launch_mfma(const Shape& s, const DecodeArgs& a, const DecodeC
 // keys, 33 splits and 264 workgroups, 62.9 against 60.6). Groups up to 3
 // keep the dot-product kernel (24q/8kv, B = 1, decode call: 24.4 against
 // 25.9 us at 32K keys, 7.6 against 8.4 at 4K). nwd_set_decode_kernel forces
-// either kernel.
+// either kernel. Head size 64 takes the same rule (decode calls, B = 1,
+// dot-product against matrix-core kernel, us: 32q/8kv at 4K / 16K / 32K
+// keys 7.2 / 10.7 / 17.9 against 7.7 / 10.5 / 15.6; 64q/8kv at 16K 14.6
+// against 10.7; 40q/8kv 11.3 against 10.6; 16q/8kv 10.1 against 10.4;
+// 14q/2kv at 32K 11.9 against 10.6).
+inline bool prefer_mfma(int G, const Shape& s, const DecodeCall& c) {
+  const bool long_splits = (int64_t)c.span >= 512LL * c.nsplit &&
+                           (int64_t)c.batch * s.n_kv * c.nsplit <= kMOneWave;
+  return c.kernel < 0 && (G >= 5 || (G == 4 && (c.batch >= 2 || long_splits)));
+}
+
 template <int G>
 static hipError_t launch_decode_128(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                     hipStream_t stream) {
@@ -457,10 +515,7 @@ static hipError_t launch_decode_128(const Shape& s, const DecodeArgs& a, const D
     if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups)
       return launch_qo<1, G>(s, a, c, stream);
   }
-  const bool long_splits = (int64_t)c.span >= 512LL * c.nsplit &&
-                           (int64_t)c.batch * s.n_kv * c.nsplit <= kMOneWave;
-  if (c.kernel < 0 && (G >= 5 || (G == 4 && (c.batch >= 2 || long_splits))))
-    return launch_mfma<G>(s, a, c, stream);
+  if (prefer_mfma(G, s, c)) return launch_mfma<G>(s, a, c, stream);
   return launch_qo<G>(s, a, c, stream);
 }
 

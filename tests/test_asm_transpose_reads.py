@@ -1,12 +1,14 @@
 """Build-time check of the decode kernels' inline-assembly transpose reads.
 
-decode_mfma_kernel (csrc/nwd_decode.hip) issues its eight V^T operand reads
-as inline `ds_read_b64_tr_b16` (lds_read_tr16_asm in csrc/nwd_common.h), runs
+decode_mfma_kernel (csrc/nwd_decode_mfma.h, instantiated in nwd_decode.hip;
+its head-64 form in nwd_decode_mfma64.hip) issues its eight (four) V^T
+operand reads as inline `ds_read_b64_tr_b16` (lds_read_tr16_asm in
+csrc/nwd_common.h), runs
 the softmax, and only then waits for them with an inline
 `s_waitcnt lgkmcnt(0)` (lds_reads_done). The compiler treats each read's
 result as ready when the asm statement ends, so the code is correct only if
 nothing touches a read's destination registers before that wait: no copy,
-no move, no other use. This test compiles nwd_decode.hip for gfx950 to AMD
+no move, no other use. This test compiles both units for gfx950 to AMD
 assembly (code built here) and walks every path from each transpose read,
 through branches, to the first `lgkmcnt(0)` wait, and fails if any
 instruction on the way reads or writes one of the read's destination VGPRs.
@@ -19,7 +21,7 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
-SRC = ROOT / "nemotron-webgpu-decode_amd" / "csrc" / "nwd_decode.hip"
+CSRC = ROOT / "nemotron-webgpu-decode_amd" / "csrc"
 HIPCC = "/opt/rocm/bin/hipcc"
 
 _VREG = re.compile(r"\bv(\d+)\b")
@@ -103,11 +105,12 @@ def test_checker_flags_a_use_before_the_wait():
 
 
 @pytest.mark.skipif(shutil.which(HIPCC) is None and not Path(HIPCC).exists(), reason="hipcc absent")
-def test_transpose_read_registers_untouched_until_the_wait(tmp_path):
+@pytest.mark.parametrize("unit", ["nwd_decode.hip", "nwd_decode_mfma64.hip"])
+def test_transpose_read_registers_untouched_until_the_wait(tmp_path, unit):
     out = tmp_path / "decode.s"
     cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
            "-Xclang", "-packed-fp32-ops", f"-I{ROOT / 'include'}", "--cuda-device-only", "-S",
-           str(SRC), "-o", str(out)]
+           str(CSRC / unit), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert res.returncode == 0, res.stderr[-3000:]
     found, checked = _violations(*_parse(out.read_text()))

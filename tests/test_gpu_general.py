@@ -116,8 +116,9 @@ def test_head_size_split_decode(D, H, Hkv, io):
     at 3000 keys (one workgroup per query head when batch x heads x splits
     fits 256 workgroups, else one per KV head) and a ragged batch of three,
     against the oracle; forced split counts 1, 7 and 64, the in-kernel merge
-    and both key layouts within fp32 rounding of the default; the fused append
-    bit-identical to append + decode in the caches."""
+    and both key layouts (and at head size 64 the matrix-core kernel) within
+    fp32 rounding of the default; the fused append bit-identical to append +
+    decode in the caches."""
     g = rng(820 + D + H)
     lens = [3000, 40, 1333]
     cap = max(lens) + 2
@@ -134,12 +135,16 @@ def test_head_size_split_decode(D, H, Hkv, io):
                 f"splits {ctx.decode_splits(batch, max(lens[:batch]))}")
             pos = pos_tensor([L - 1 for L in lens[:batch]])
             outs = []
-            for n, merge, layout in ((0, None, None), (1, None, None), (7, None, None),
-                                     (64, None, None), (0, 0, None), (7, 0, None), (7, None, 1),
-                                     (7, None, 0)):
+            runs = [(0, None, None, None), (1, None, None, None), (7, None, None, None),
+                    (64, None, None, None), (0, 0, None, None), (7, 0, None, None),
+                    (7, None, 1, None), (7, None, 0, None)]
+            if D == 64:  # the matrix-core kernel built for head size 64
+                runs += [(0, None, None, 1), (7, None, None, 1), (7, 0, None, 1), (64, None, 1, 1)]
+            for n, merge, layout, kern in runs:
                 ctx.set_decode_splits(n)
                 ctx.set_decode_merge(merge)
                 ctx.set_decode_layout(layout)
+                ctx.set_decode_kernel(kern)
                 out = torch.empty((batch, H, D), dtype=_tdtype(io), device="cuda")
                 ctx.decode(dev(q[:batch]), kc, vc, pos, out, batch, max(lens[:batch]))
                 outs.append(host(out).astype(np.float32))
@@ -153,6 +158,7 @@ def test_head_size_split_decode(D, H, Hkv, io):
         ctx.set_decode_splits(0)
         ctx.set_decode_merge(None)
         ctx.set_decode_layout(None)
+        ctx.set_decode_kernel(None)
         res = []
         for fused in (True, False):
             kc2, vc2 = kc.clone(), vc.clone()
