@@ -741,8 +741,8 @@ GENERAL_SHAPES = {
                        "layout, as two groups of 8 per KV head on the matrix-core split kernel), "
                        "8192 keys, fp16 I/O, decode call"),
     "general-d64-16k": (32, 8, 64, 16384, "B=1, 32q/8kv/d64 (group 4, head size 64: the "
-                        "Llama-3.2-1B layout, on the split kernel built for head size 64), "
-                        "16384 keys, fp16 I/O, decode call"),
+                        "Llama-3.2-1B layout, on the matrix-core split kernel built for head "
+                        "size 64), 16384 keys, fp16 I/O, decode call"),
 }
 # Prefill on other head layouts: (heads, kv heads, head_dim, past, new tokens, description).
 GENERAL_PREFILL_SHAPES = {
