@@ -171,7 +171,7 @@ def _build_asan_driver() -> None:
 
 def build_variants(jobs: int | None = None) -> list:
     """Both debug variants; each compiles every source again. The two builds
-    run side by side: each is bound by its longest source (nwd_decode.hip)."""
+    run side by side: each is bound by its longest source (nwd_decode_hd.hip)."""
     with cf.ThreadPoolExecutor(max_workers=2) as ex:
         check = ex.submit(build_check, jobs)
         asan = ex.submit(build_asan, jobs)

@@ -1,7 +1,8 @@
 // nwd_decode.h — the split workgroup of decode (decode_split_kernel), its
 // state store and merges, and their launchers, shared by nwd_decode.hip
-// (head size 128, and the matrix-core kernel) and nwd_decode_hd.hip (the
-// other head sizes), which instantiate disjoint sets of them.
+// (head size 128), nwd_decode_groups.hip (groups 3, 6, 7 at 128 and 64) and
+// nwd_decode_hd.hip (the other head sizes), which instantiate disjoint sets
+// of them; the matrix-core kernel is in nwd_decode_mfma.h.
 #pragma once
 
 #include <hip/hip_ext.h>

@@ -1,7 +1,9 @@
 // nwd_decode_mfma.h — the matrix-core split workgroup of decode
-// (decode_mfma_kernel) and its launcher at head size 128, shared by
-// nwd_decode.hip (groups 1, 2, 4, 5, 8) and nwd_decode_groups.hip (groups 3,
-// 6, 7), which instantiate disjoint sets of it.
+// (decode_mfma_kernel, and decode_mfma_d64_kernel at head size 64), its
+// launcher and the kernel choice at head sizes 128 and 64, shared by
+// nwd_decode.hip (groups 1, 2, 4, 5, 8 at 128), nwd_decode_groups.hip
+// (groups 3, 6, 7) and nwd_decode_mfma64.hip (head size 64), which
+// instantiate disjoint sets of it.
 #pragma once
 
 #include <atomic>
