@@ -246,12 +246,14 @@ int nwd_set_decode_splits(nwd_ctx* ctx, int32_t n_splits);
  * default, the separate kernel (measured faster on MI355X at 4K and 32K
  * keys). Same results, bit for bit. The general kernels always use the
  * separate merge; this and the two knobs below do not apply to them (at
- * D = 64 and 256 this and the layout knob apply, the kernel knob does not:
- * only the dot-product kernel is built for those sizes). */
+ * D = 64 all three apply; at 256 and on the padded head forms this and the
+ * layout knob apply, the kernel knob does not: only the dot-product kernel
+ * is built for those sizes). */
 int nwd_set_decode_merge(nwd_ctx* ctx, int32_t separate_kernel);
 
-/* Chooses the split kernel of later decode calls (the workgroup form of
- * sparse_attn.wgsl main, kernels/sparse_attn.wgsl:31-114): 0 the dot-product
+/* Chooses the split kernel of later decode calls at head sizes 128 and 64
+ * (the workgroup form of sparse_attn.wgsl main,
+ * kernels/sparse_attn.wgsl:31-114): 0 the dot-product
  * kernel (VALU, whose work per key grows with the group size G), 1 the
  * matrix-core kernel (MFMA, the same work for every G), -1 restores the
  * default, which takes the matrix-core kernel for calls that run one
