@@ -69,8 +69,8 @@ typedef struct nwd_desc {
   int32_t head_dim;    /* D, 1 .. 512 (128 in engine/config.js:12). D = 128
                           with G from 1 to 8 runs the kernels built for
                           those shapes; decodes at D = 64 (G 1 to 8, also
-                          on the matrix-core kernel) and D = 256 (G 1, 2,
-                          4, 5) run the dot-product
+                          on the matrix-core kernel) and D = 256 (G 1 to
+                          5) run the dot-product
                           split kernel built for those sizes, and at the
                           other multiples of 8 up to 256 its form for rows
                           padded to 64, 128 or 256 dims, there with G = 3,

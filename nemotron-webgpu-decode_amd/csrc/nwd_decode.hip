@@ -52,8 +52,8 @@
 
 namespace nwd {
 
-// Groups built as they are: 1, 2, 4, 5 and 8 (8 up to head size 128), and
-// at head sizes 128 and 64 every group up to 8 (3, 6 and 7 in
+// Groups built as they are: 1, 2, 4, 5 and 8 (8 up to head size 128), at
+// head sizes 128 and 64 every group up to 8, and 3 at 256 (3, 6 and 7 in
 // nwd_decode_groups.hip). A larger group runs as groups of a built size, so
 // that each KV head's rows are read as few times as possible: kv_rep =
 // ceil(group / largest) reads. A built divisor (the largest first) that
@@ -67,10 +67,11 @@ int kernel_group(int head_dim, int group, int* kv_rep) {
   const bool every = head_dim == kHeadDim || head_dim == 64;  // 1 .. 8 all built
   const int top = head_dim <= kHeadDim ? 8 : 5;  // group 8 is built up to head size 128
   auto built = [&](int g) {
-    return g == 1 || g == 2 || g == 4 || g == 5 || g == top || (every && g >= 3 && g <= 8);
+    return g == 1 || g == 2 || g == 4 || g == 5 || g == top || (every && g >= 3 && g <= 8) ||
+           (head_dim == 256 && g == 3);
   };
   if (built(group)) return group;
-  if (group < 8) return 0;  // 3, 6, 7 at other head sizes: padded first
+  if (group <= top) return 0;  // 3, 6, 7 at other head sizes: padded first
   const int reads = (group + top - 1) / top;
   for (int gs = top; gs >= 3; --gs) {
     if (built(gs) && group % gs == 0 && group / gs == reads) {

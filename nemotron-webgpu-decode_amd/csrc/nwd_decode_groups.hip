@@ -2,8 +2,9 @@
 // KV head, at head size 128 (e.g. Qwen2.5-7B's 28q/4kv) on the same two
 // split kernels as the other groups, the dot-product one of nwd_decode.h and
 // the matrix-core one of nwd_decode_mfma.h (whose MFMA columns past the
-// group hold zero queries), and at head size 64 (e.g. Qwen2.5-0.5B's
-// 14q/2kv) on the dot-product one built for that size. A translation unit
+// group hold zero queries), at head size 64 (e.g. Qwen2.5-0.5B's 14q/2kv)
+// on both kernels built for that size, and group 3 at head size 256 on the
+// dot-product kernel built for it. A translation unit
 // of its own, so that these kernels and the other groups' compile side by
 // side.
 #include "nwd_decode_mfma.h"
@@ -25,6 +26,12 @@ static hipError_t launch_decode_64(const Shape& s, const DecodeArgs& a, const De
 
 hipError_t launch_decode_groups(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                 hipStream_t stream) {
+  if (s.head_dim == 256) {  // group 3, on the dot-product kernel built for 256
+    if (s.group != 3) return hipErrorInvalidValue;
+    if ((int64_t)c.batch * s.n_heads * a.nsplit <= kSubSplitMaxWorkgroups)
+      return launch_qo<1, 3, 256, false>(s, a, c, stream);
+    return launch_qo<3, 1, 256, false>(s, a, c, stream);
+  }
   if (s.head_dim == 64) {
     switch (s.group) {
       case 3: return launch_decode_64<3>(s, a, c, stream);

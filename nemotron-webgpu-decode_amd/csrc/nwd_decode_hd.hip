@@ -15,7 +15,7 @@ namespace nwd {
 // otherwise on decode_split_kernel. Group 8 above 128 is
 // not built (its accumulators and query registers would not fit one lane's
 // registers; kernel_group runs it as two groups of 4). Groups 3, 6 and 7 at
-// head size 64 are built in nwd_decode_groups.hip.
+// head size 64, and 3 at 256, are built in nwd_decode_groups.hip.
 template <int kD, bool kPadD>
 static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const DecodeCall& c,
                                    hipStream_t stream) {
@@ -46,7 +46,7 @@ static hipError_t launch_decode_hd(const Shape& s, const DecodeArgs& a, const De
       if constexpr (kD <= kHeadDim) return launch_qo<8, 1, kD, kPadD>(s, a, c, stream);
       return hipErrorInvalidValue;
     default:
-      if constexpr (kD == 64 && !kPadD) return launch_decode_groups(s, a, c, stream);
+      if constexpr ((kD == 64 || kD == 256) && !kPadD) return launch_decode_groups(s, a, c, stream);
       return hipErrorInvalidValue;
   }
 }

@@ -66,8 +66,8 @@ hipError_t launch_kv_append(const Shape& s, const void* k_new, const void* v_new
 
 // The group the decode and prefill kernels run a group of `group` query
 // heads as, with *kv_rep such groups per KV head: the group itself for 1, 2,
-// 4, 5 and 8 (8 only up to head size 128) and at head sizes 128 and 64 for
-// every group up to 8; for larger groups a built size that divides them into
+// 4, 5 and 8 (8 only up to head size 128), at head sizes 128 and 64 for
+// every group up to 8, and for 3 at 256; for larger groups a built size that divides them into
 // ceil(group / largest built size) groups; 0 when the group must be padded
 // first (padded_group).
 int kernel_group(int head_dim, int group, int* kv_rep);

@@ -481,6 +481,9 @@ hipError_t launch_prefill_wide(const Shape& s0, const void* q, const void* k_cac
     case 2: return launch_wide_g<2>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     case 4: return launch_wide_g<4>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     case 5: return launch_wide_g<5>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
+    case 3:  // built at head size 256 only
+      if (s.head_dim != kWD) return hipErrorInvalidValue;
+      return launch_wide_p<3, false>(s, q, k_cache, v_cache, pos0, out, batch, n_new, max_len, ws, r, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -448,12 +448,13 @@ def test_general_cache_rows_read_back():
 # ----------------------------------------------------- groups 3, 6, 7 ---
 
 @pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 6, 1), (128, 28, 4), (128, 14, 2),
-                                     (64, 28, 4), (64, 12, 4), (96, 12, 4), (80, 28, 4)])
+                                     (64, 28, 4), (64, 12, 4), (96, 12, 4), (80, 28, 4),
+                                     (256, 12, 4), (256, 12, 2)])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_group_3_6_7_decode(D, H, Hkv, io):
     """Groups 3, 6 and 7 run decode kernels built for them at head_dim 128
-    and 64, and at other head sizes the kernels of groups 4 and 8 on padded
-    query rows: against the oracle at 5000 and 1100 keys, with two key bounds
+    and 64 (group 3 at 256, and 6 as two groups of 3), and at other head
+    sizes the kernels of groups 4 and 8 on padded query rows: against the oracle at 5000 and 1100 keys, with two key bounds
     (different split partitions) within fp32 rounding of each other, and the
     fused append bit-identical to append + decode in the caches."""
     cap = 5010
@@ -528,13 +529,14 @@ def test_group_3_6_7_knobs(H, Hkv, D):
 
 
 @pytest.mark.parametrize("D,H,Hkv", [(128, 12, 4), (128, 7, 1), (128, 12, 2), (64, 7, 1),
-                                     (96, 12, 4), (80, 7, 1)])
+                                     (96, 12, 4), (80, 7, 1), (256, 12, 4), (256, 12, 2)])
 @pytest.mark.parametrize("max_batch", [2, 2048])
 @pytest.mark.parametrize("io", ["f16", "f32"])
 def test_group_3_6_7_prefill(D, H, Hkv, max_batch, io):
     """Groups 3, 6 and 7 prefill on the fp16 MFMA prefill kernel built for
-    them at head_dim 128 and 64 (rows padded to 128 dims), and at other head
-    sizes on the kernels of groups 4 and 8 through padded query rows: 37 queries onto pos0 90 and 0, row by
+    them at head_dim 128 and 64 (and group 3 at 256, 6 as two groups of 3),
+    and at other head sizes on the kernels of groups 4 and 8 through padded
+    query rows: 37 queries onto pos0 90 and 0, row by
     row against the oracle's decode over keys 0..pos0+i. With max_batch 2048
     the padded route's buffers hold a few tokens, so the chunk runs in
     several sub-chunks."""
