@@ -725,7 +725,7 @@ EXTRA_WORKLOADS = {
 # Step counts of the secondary measurements (fixed, so a short --steps only
 # shortens the headline's timed region).
 # Head layouts outside the benchmark's (groups 7 and 16, head sizes 256, 96
-# and 64), decode-only, B = 1:
+# and 64, group 7 at 64), decode-only, B = 1:
 # name: (n_heads, n_kv_heads, head_dim, keys, description)
 GENERAL_SHAPES = {
     "general-g7-32k": (28, 4, 128, 32768, "B=1, 28q/4kv/d128 (group 7: the Qwen2.5-7B head "
@@ -743,6 +743,9 @@ GENERAL_SHAPES = {
     "general-d64-16k": (32, 8, 64, 16384, "B=1, 32q/8kv/d64 (group 4, head size 64: the "
                         "Llama-3.2-1B layout, on the matrix-core split kernel built for head "
                         "size 64), 16384 keys, fp16 I/O, decode call"),
+    "general-d64-g7-32k": (14, 2, 64, 32768, "B=1, 14q/2kv/d64 (group 7, head size 64: the "
+                           "Qwen2.5-0.5B layout, on the matrix-core split kernel built for head "
+                           "size 64), 32768 keys, fp16 I/O, decode call"),
 }
 # Prefill on other head layouts: (heads, kv heads, head_dim, past, new tokens, description).
 GENERAL_PREFILL_SHAPES = {
